@@ -1,0 +1,100 @@
+// Shared device helpers and host-side error plumbing for libflower_amd (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/flower_amd.h"
+
+namespace flw {
+
+// ---------------------------------------------------------------- host: error state
+// Every entry point returns 0 on success or a FLW_E* code; the message of the last failure on
+// the calling thread is kept here for flw_last_error().
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+#define FLW_REQUIRE(cond, code, ...)                      \
+  do {                                                    \
+    if (!(cond)) return ::flw::set_error((code), __VA_ARGS__); \
+  } while (0)
+
+// ---------------------------------------------------------------- device: number formats
+constexpr float kE4m3Max = 448.0f;
+constexpr float kEps = 1e-12f;   // the reference's amax / scale floor
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (f != f) ? 0x7FC0u : r;
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
+
+// fp32 -> OCP e4m3fn code, round to nearest even, NOT saturating (|x| >= 464+ -> NaN 0x7F),
+// NaN / inf -> sign | 0x7F. Integer-exact; the low byte of the result is the code.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  // normal range: rebias the exponent (127 -> 7) and round the fraction to 3 bits
+  uint32_t r = a - (120u << 23);
+  uint32_t nrm = (r + 0x7FFFFu + ((r >> 20) & 1u)) >> 20;
+  nrm = nrm > 0x7Fu ? 0x7Fu : nrm;
+  // subnormal range (|x| < 2^-6): multiples of 2^-9, round half to even
+  uint32_t sub = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  uint32_t code = a >= 0x3C800000u ? nrm : sub;
+  return code | sign;
+}
+
+// e4m3fn code -> fp32 (exact); 0x7F / 0xFF -> NaN.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 0xFu;
+  uint32_t m = c & 7u;
+  float v = e == 0 ? (float)m * 0.001953125f                        // m * 2^-9
+                   : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  v = ((c & 0x7Fu) == 0x7Fu) ? __builtin_nanf("") : v;
+  return __uint_as_float(__float_as_uint(v) | s);
+}
+
+// |x| as an unsigned bit pattern: ordered like |x| for finite values, NaN above +inf, so an
+// integer max over it is an abs-max that propagates NaN (as torch.amax does).
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+
+// Wave64 reductions.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    uint32_t w = (uint32_t)__shfl_xor((int)v, o, 64);
+    v = v > w ? v : w;
+  }
+  return v;
+}
+
+// Loads of 16 bytes of an input tensor, widened to fp32.
+template <typename T> struct Vec16;
+template <> struct Vec16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void load(const void* p, float* out) {
+    float4 v = *reinterpret_cast<const float4*>(p);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  }
+};
+template <> struct Vec16<uint16_t> {   // bf16
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void load(const void* p, float* out) {
+    uint4 v = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(w[i] << 16);
+      out[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+
+}  // namespace flw

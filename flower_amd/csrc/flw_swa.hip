@@ -1,0 +1,381 @@
+// FP8 causal sliding-window attention forward for gfx950 (CDNA4).
+//
+// Work decomposition: one workgroup = 4 waves = 128 queries of one (b, h) slice; each wave owns
+// 32 queries. The workgroup walks 64-key tiles over the band [m0 - W + 1, m0 + 127] only (tiles
+// wholly outside the window are never visited); a wave skips the tiles that miss its own
+// 32-query band. Per tile a wave computes S^T = K Q^T with two v_mfma_f32_32x32x64_f8f6f4 (keys
+// are the MFMA rows, queries the columns, so every lane holds 32 scores of ONE query and the row
+// max / sum are lane-local plus one exchange with lane^32), runs the online softmax in base 2
+// with the softmax scale, log2(e) and the x448 P pre-scale folded into one FMA, packs P to
+// e4m3 in registers (v_cvt_pk_fp8_f32) straight into the B operand of O^T += V^T P^T
+// (D/32 more MFMAs). K tiles are staged in LDS in MFMA-fragment order (a permutation of 16-byte
+// chunks of the row-major tile); V arrives already in that order from the quantiser
+// (FLW_LAYOUT_VTILE), so every fragment read is a conflict-free linear ds_read_b128.
+// Tiles are double-buffered in LDS with one barrier per tile; the next tile's global loads are
+// issued before the current tile's MFMAs. Workgroups are dealt to the 8 XCDs so that each XCD
+// works through contiguous query tiles of the same heads and re-reads K/V from its own L2.
+#include <math.h>
+
+#include "flw_common.h"
+
+namespace flw {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f mfma_32x32x64_f8(v8i a, v8i b, v16f c) {
+  // cbsz = blgp = 0: both operands are FP8 E4M3; no block scales.
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+constexpr int kWaves = 4;
+constexpr int kBM = 32 * kWaves;   // queries per workgroup
+constexpr int kBN = 64;            // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLog2_448 = 8.807354922057604f;   // log2(448): P is produced pre-scaled by 448
+
+struct SwaParams {
+  const uint8_t* q8;
+  const uint8_t* k8;
+  const uint8_t* vt;
+  int64_t qsb, qsh, qst;      // byte strides of q8
+  int64_t ksb, ksh, kst;      // byte strides of k8
+  int64_t vt_slice;           // bytes per (b, h) slice of the tiled V
+  const float* qs;
+  const float* ks;
+  const float* vs;
+  int gran;
+  void* out;
+  int64_t osb, osh, ost;      // element strides of out
+  int H, T, W, nM;
+};
+
+template <typename OutT> struct Store4;
+template <> struct Store4<float> {
+  __device__ __forceinline__ static void st(float* p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+  }
+};
+template <> struct Store4<uint16_t> {
+  __device__ __forceinline__ static void st(uint16_t* p, float a, float b, float c, float d) {
+    uint2 w;
+    w.x = f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+    w.y = f32_to_bf16_bits(c) | (f32_to_bf16_bits(d) << 16);
+    *reinterpret_cast<uint2*>(p) = w;
+  }
+};
+
+__device__ __forceinline__ v8i load_frag(const uint8_t* lds, int off) {
+  const uint4 a = *reinterpret_cast<const uint4*>(lds + off);
+  const uint4 b = *reinterpret_cast<const uint4*>(lds + off + 1024);
+  v8i r;
+  r[0] = (int)a.x; r[1] = (int)a.y; r[2] = (int)a.z; r[3] = (int)a.w;
+  r[4] = (int)b.x; r[5] = (int)b.y; r[6] = (int)b.z; r[7] = (int)b.w;
+  return r;
+}
+
+template <int D, typename OutT>
+__global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
+  constexpr int NDC = D >= 64 ? D / 64 : 1;   // 64-deep K chunks of the QK^T product
+  constexpr int NDB = D / 32;                  // 32-row blocks of O^T
+  constexpr int KT_BYTES = 2 * NDC * 2048;     // one K tile in fragment order
+  constexpr int VT_BYTES = 64 * D;             // one V tile (VTILE layout)
+  constexpr int CPR = D / 16;                  // 16-byte chunks per K row
+  constexpr int KCH = 64 * CPR;                // chunks per K tile (== V tile chunks)
+  constexpr int CPT = (KCH + 255) / 256;       // chunks per thread
+  __shared__ __align__(16) uint8_t lds_k[2][KT_BYTES];
+  __shared__ __align__(16) uint8_t lds_v[2][VT_BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwg = gridDim.x;
+  int L = blockIdx.x;
+  if ((nwg & 7) == 0) L = (L & 7) * (nwg >> 3) + (L >> 3);   // contiguous work per XCD
+  const int bh = L / p.nM, mt = L % p.nM;
+  const int b = bh / p.H, h = bh % p.H;
+  const int T = p.T, W = p.W;
+  const int m0 = mt * kBM;
+  const int q0 = m0 + 32 * wave;
+  const int qcol = lane & 31, hh = lane >> 5;
+
+  const int si = p.gran == FLW_SCALE_TENSOR ? 0 : (p.gran == FLW_SCALE_HEAD ? h : bh);
+  const float q_s = p.qs[si], k_s = p.ks[si], v_s = p.vs[si];
+  const float rsd = D == 32 ? 0.17677669529663687f : (D == 64 ? 0.125f : 0.08838834764831845f);
+  const float c = q_s * k_s * rsd * kLog2e;
+
+  // Q fragments: B operand of S^T = K Q^T; lane (qcol, hh) holds Q[q][64 dc + 32 hh + 0..31].
+  v8i qf[NDC];
+  {
+    const int qi = q0 + qcol < T ? q0 + qcol : T - 1;
+    const uint8_t* qp = p.q8 + b * p.qsb + h * p.qsh + (int64_t)qi * p.qst;
+#pragma unroll
+    for (int dc = 0; dc < NDC; ++dc) {
+      if (D == 32 && hh) {
+        qf[dc] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      } else {
+        const uint4 a = *reinterpret_cast<const uint4*>(qp + 64 * dc + 32 * hh);
+        const uint4 bq = *reinterpret_cast<const uint4*>(qp + 64 * dc + 32 * hh + 16);
+        qf[dc] = v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)bq.x, (int)bq.y, (int)bq.z, (int)bq.w};
+      }
+    }
+  }
+
+  const uint8_t* kbase = p.k8 + b * p.ksb + h * p.ksh;
+  const uint8_t* vbase = p.vt + (int64_t)bh * p.vt_slice;
+  uint4 kreg[CPT], vreg[CPT];
+
+  auto load_tile = [&](int n0) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int i = tid + 256 * j;
+      if (i < KCH) {
+        const int kk = i / CPR, g = i % CPR;
+        const int row = n0 + kk;
+        kreg[j] = row < T ? *reinterpret_cast<const uint4*>(kbase + (int64_t)row * p.kst + 16 * g)
+                          : make_uint4(0, 0, 0, 0);
+        vreg[j] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(n0 >> 6) * VT_BYTES + 16 * i);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int i = tid + 256 * j;
+      if (i < KCH) {
+        const int kk = i / CPR, g = i % CPR;
+        const int d0 = 16 * g;
+        const int blk = kk >> 5, krow = kk & 31, dc = d0 >> 6, h2 = (d0 >> 5) & 1, cc = (d0 >> 4) & 1;
+        const int off = (((blk * NDC + dc) * 2 + cc) * 64 + krow + 32 * h2) * 16;
+        *reinterpret_cast<uint4*>(&lds_k[buf][off]) = kreg[j];
+        *reinterpret_cast<uint4*>(&lds_v[buf][16 * i]) = vreg[j];
+      }
+    }
+  };
+
+  // Key range of the workgroup, tile-aligned; and of this wave.
+  const int lo_raw = m0 - W + 1;
+  const int lo = lo_raw <= 0 ? 0 : (lo_raw & ~(kBN - 1));
+  const int hi = min(T, m0 + kBM);
+  const int wlo = q0 - W + 1, whi = q0 + 31;
+
+  v16f o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = v16f{};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  if (lo < hi) {
+    load_tile(lo);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int n0 = lo, it = 0; n0 < hi; n0 += kBN, ++it) {
+    const int buf = it & 1;
+    const bool more = n0 + kBN < hi;
+    if (more) load_tile(n0 + kBN);
+
+    if (n0 <= whi && n0 + kBN - 1 >= wlo) {
+      const uint8_t* lk = lds_k[buf];
+      const uint8_t* lv = lds_v[buf];
+      v16f s0 = v16f{}, s1 = v16f{};
+#pragma unroll
+      for (int dc = 0; dc < NDC; ++dc) {
+        v8i k0 = load_frag(lk, ((0 * NDC + dc) * 2 * 64 + lane) * 16);
+        v8i k1 = load_frag(lk, ((1 * NDC + dc) * 2 * 64 + lane) * 16);
+        if (D == 32 && hh) { k0 = v8i{0, 0, 0, 0, 0, 0, 0, 0}; k1 = k0; }
+        s0 = mfma_32x32x64_f8(k0, qf[dc], s0);
+        s1 = mfma_32x32x64_f8(k1, qf[dc], s1);
+      }
+
+      // Mask only where the tile crosses the diagonal, the window start or T.
+      const bool interior = (n0 + kBN - 1 <= q0) && (q0 + 31 - n0 < W) && (n0 + kBN <= T);
+      if (!interior) {
+        const int qi = q0 + qcol;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int kj = n0 + 8 * (v >> 2) + 4 * hh + (v & 3);
+          const int kj1 = kj + 32;
+          const bool ok0 = kj <= qi && qi - kj < W && kj < T;
+          const bool ok1 = kj1 <= qi && qi - kj1 < W && kj1 < T;
+          s0[v] = ok0 ? s0[v] : -INFINITY;
+          s1[v] = ok1 ? s1[v] : -INFINITY;
+        }
+      }
+
+      float tmax = fmaxf(s0[0], s1[0]);
+#pragma unroll
+      for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, fmaxf(s0[v], s1[v]));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_safe) * c);
+      const float nb = kLog2_448 - m_safe * c;
+
+      float lsum = 0.0f;
+      int pk[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a0 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 0], c, nb));
+        const float a1 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 1], c, nb));
+        const float a2 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 2], c, nb));
+        const float a3 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 3], c, nb));
+        const float b0 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 0], c, nb));
+        const float b1 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 1], c, nb));
+        const float b2 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 2], c, nb));
+        const float b3 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 3], c, nb));
+        lsum += (a0 + a1) + (a2 + a3) + ((b0 + b1) + (b2 + b3));
+        int wa = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
+        pk[j] = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, wa, true);
+        int wb = __builtin_amdgcn_cvt_pk_fp8_f32(b0, b1, 0, false);
+        pk[4 + j] = __builtin_amdgcn_cvt_pk_fp8_f32(b2, b3, wb, true);
+      }
+      l_run = l_run * alpha + lsum;
+      const v8i pf = v8i{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        o[db] *= alpha;
+        const v8i vf = load_frag(lv, (db * 2 * 64 + lane) * 16);
+        o[db] = mfma_32x32x64_f8(vf, pf, o[db]);
+      }
+      m_run = m_new;
+    }
+
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: out = O * v_scale / l   (l carries the x448 of P, matching pv_scale = v_s / 448)
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot == 0.0f ? 0.0f : v_s / l_tot;
+  const int qi = q0 + qcol;
+  if (qi < T) {
+    OutT* op = static_cast<OutT*>(p.out) + b * p.osb + h * p.osh + (int64_t)qi * p.ost;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * db + 8 * j + 4 * hh;
+        Store4<OutT>::st(op + d, o[db][4 * j] * inv, o[db][4 * j + 1] * inv,
+                         o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+      }
+    }
+  }
+}
+
+int quant_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
+               int64_t sh, int64_t st, int granularity, int layout, uint8_t* out, float* scale_out,
+               void* ws, size_t ws_bytes, hipStream_t stream);
+
+template <int D>
+static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s) {
+  if (out_dtype == FLW_F32)
+    hipLaunchKernelGGL((swa_fwd_kernel<D, float>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((swa_fwd_kernel<D, uint16_t>), grid, dim3(256), 0, s, p);
+}
+
+static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, const int64_t* kst,
+                   const uint8_t* vt, const float* qs, const float* ks, const float* vs, int gran,
+                   void* out, int out_dtype, const int64_t* ost, int64_t B, int64_t H, int64_t T,
+                   int64_t D, int64_t window, hipStream_t stream) {
+  FLW_REQUIRE(q8 && k8 && vt && qs && ks && vs && out && qst && kst && ost, FLW_E_INVALID, "null pointer argument");
+  FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
+  FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
+  FLW_REQUIRE(out_dtype == FLW_F32 || out_dtype == FLW_BF16, FLW_E_UNSUPPORTED, "output dtype %d", out_dtype);
+  FLW_REQUIRE(gran >= FLW_SCALE_TENSOR && gran <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", gran);
+  FLW_REQUIRE(T <= (int64_t)0x7FFFFF00, FLW_E_UNSUPPORTED, "T too large");
+  for (int i = 0; i < 3; ++i) {
+    FLW_REQUIRE(qst[i] % 16 == 0 && kst[i] % 16 == 0, FLW_E_INVALID, "q8/k8 strides must be multiples of 16 bytes");
+    FLW_REQUIRE(ost[i] % 4 == 0, FLW_E_INVALID, "output strides must be multiples of 4 elements");
+  }
+  FLW_REQUIRE(((uintptr_t)q8 & 15) == 0 && ((uintptr_t)k8 & 15) == 0 && ((uintptr_t)vt & 15) == 0,
+              FLW_E_INVALID, "q8 / k8 / v tiles must be 16-byte aligned");
+  FLW_REQUIRE(((uintptr_t)out & 15) == 0, FLW_E_INVALID, "output must be 16-byte aligned");
+  const int64_t nM = (T + kBM - 1) / kBM;
+  FLW_REQUIRE(B * H * nM <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
+  int64_t W = window;
+  if (W > T) W = T;       // i - j <= T - 1 < T: a window of T is already full causal
+  if (W < 0) W = 0;
+  SwaParams p{};
+  p.q8 = q8; p.k8 = k8; p.vt = vt;
+  p.qsb = qst[0]; p.qsh = qst[1]; p.qst = qst[2];
+  p.ksb = kst[0]; p.ksh = kst[1]; p.kst = kst[2];
+  p.vt_slice = ((T + 63) / 64) * 64 * D;
+  p.qs = qs; p.ks = ks; p.vs = vs; p.gran = gran;
+  p.out = out; p.osb = ost[0]; p.osh = ost[1]; p.ost = ost[2];
+  p.H = (int)H; p.T = (int)T; p.W = (int)W; p.nM = (int)nM;
+  dim3 grid((unsigned)(B * H * nM));
+  if (D == 32) launch_d<32>(p, out_dtype, grid, stream);
+  else if (D == 64) launch_d<64>(p, out_dtype, grid, stream);
+  else launch_d<128>(p, out_dtype, grid, stream);
+  return check_launch("flw_fp8_swa_fwd");
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct SwaWorkspace {
+  size_t q8, k8, vt, scales, partials, total;
+};
+
+static SwaWorkspace swa_ws_layout(int64_t B, int64_t H, int64_t T, int64_t D) {
+  SwaWorkspace w{};
+  const size_t n = (size_t)(B * H * T * D);
+  w.q8 = 0;
+  w.k8 = align256(n);
+  w.vt = w.k8 + align256(n);
+  w.scales = w.vt + align256(flw_vtile_bytes(B, H, T, D));
+  w.partials = w.scales + align256(3 * sizeof(float) * (size_t)(B * H));
+  w.total = w.partials + align256(flw_quant_workspace_bytes(B, H, T, D));
+  return w;
+}
+
+}  // namespace flw
+
+using namespace flw;
+
+extern "C" int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                               const int64_t* k_strides, const uint8_t* v_tiles,
+                               const float* q_scale, const float* k_scale, const float* v_scale,
+                               int granularity, void* out, int out_dtype,
+                               const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
+                               int64_t D, int64_t window, void* stream) {
+  return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, granularity,
+                 out, out_dtype, out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t flw_fp8_swa_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
+  return swa_ws_layout(B, H, T, D).total;
+}
+
+extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, int dtype,
+                                             const int64_t* strides, int64_t B, int64_t H,
+                                             int64_t T, int64_t D, int64_t window,
+                                             int granularity, void* out, float* scales_out,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  FLW_REQUIRE(strides != nullptr && workspace != nullptr, FLW_E_INVALID, "null strides / workspace");
+  FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
+  FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
+  const SwaWorkspace w = swa_ws_layout(B, H, T, D);
+  FLW_REQUIRE(workspace_bytes >= w.total, FLW_E_WORKSPACE, "workspace needs %zu bytes", w.total);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const int64_t G = granularity == FLW_SCALE_TENSOR ? 1 : (granularity == FLW_SCALE_HEAD ? H : B * H);
+  float* sc = scales_out ? scales_out : reinterpret_cast<float*>(ws + w.scales);
+  uint8_t* q8 = ws + w.q8;
+  uint8_t* k8 = ws + w.k8;
+  uint8_t* vt = ws + w.vt;
+  void* part = ws + w.partials;
+  const size_t pbytes = w.total - w.partials;
+  int rc = quant_bhtd(q, dtype, B, H, T, D, strides[0], strides[1], strides[2], granularity,
+                      FLW_LAYOUT_BHTD, q8, sc, part, pbytes, s);
+  if (rc) return rc;
+  rc = quant_bhtd(k, dtype, B, H, T, D, strides[3], strides[4], strides[5], granularity,
+                  FLW_LAYOUT_BHTD, k8, sc + G, part, pbytes, s);
+  if (rc) return rc;
+  rc = quant_bhtd(v, dtype, B, H, T, D, strides[6], strides[7], strides[8], granularity,
+                  FLW_LAYOUT_VTILE, vt, sc + 2 * G, part, pbytes, s);
+  if (rc) return rc;
+  const int64_t s8[3] = {H * T * D, T * D, D};
+  return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, granularity, out, dtype, strides + 9,
+                 B, H, T, D, window, s);
+}

@@ -1,0 +1,159 @@
+"""FP8 sliding-window causal attention forward on MI355X (gfx950), reference-compatible API.
+
+Same operator surface as flower/kernels/fp8_swa_attention.py:92-273:
+
+  ``E4M3_MAX``                   -- :92
+  ``_per_tensor_fp8(x)``         -- :195-205, returns the scale as a device tensor (no .item())
+  ``fp8_swa_attention_forward``  -- :208-259, same signature; the Triton tuning keywords are
+                                    accepted and ignored (the HIP kernel has one tuned geometry)
+  ``reference_swa_attention``    -- :262-273, dense fp32 reference (plain torch, small T only)
+
+Everything on the hot path runs in libflower_amd.so (HIP, gfx950): the amax + e4m3 quantisers
+for Q, K, V and the fused FP8 MFMA attention kernel. Scales never leave the device, so a call
+is fully asynchronous on the current stream (the reference does three ``.item()`` syncs).
+
+``granularity`` (keyword-only, default "tensor" as in the reference) selects per-tensor,
+per-head ("head": amax over B, T, D of each head) or per-(b, h) ("bh") e4m3 scales.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+E4M3_MAX = 448.0
+
+
+def _check_bhtd(x: torch.Tensor, name: str) -> None:
+    if x.dim() != 4:
+        raise ValueError(f"expected (B, H, T, D), got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        raise ValueError(f"{name} must be contiguous in its last dimension")
+
+
+def _rowmajor_strides(x: torch.Tensor, vec: int):
+    """(b, h, t) element strides if the kernel can read x in place, else None."""
+    sb, sh, st, sd = x.stride()
+    ok = sd == 1 and sb % vec == 0 and sh % vec == 0 and st % vec == 0 and x.data_ptr() % 16 == 0
+    return (sb, sh, st) if ok else None
+
+
+def _prepare(x: torch.Tensor):
+    vec = 4 if x.dtype == torch.float32 else 8
+    s = _rowmajor_strides(x, vec)
+    if s is None:
+        x = x.contiguous()
+        s = _rowmajor_strides(x, vec)
+    return x, s
+
+
+def _per_tensor_fp8(x: torch.Tensor, granularity: str = "tensor"):
+    """e4m3 quantisation with an amax scale: (x_e4m3, scale).
+
+    scale = max(amax, 1e-12) / 448 in fp32; codes = e4m3(clamp(x / scale, -448, 448)), with IEEE
+    division and round-to-nearest-even. ``scale`` is a float32 device tensor of 1 (tensor),
+    H (head) or B*H (bh) elements; ``float(scale)`` is the reference's Python float.
+    Accepts any shape for per-tensor scaling; per-head / per-(b, h) need (B, H, T, D).
+    """
+    lib = _lib.load()
+    _lib.require_gpu(x)
+    if x.numel() == 0:
+        raise ValueError("cannot quantise an empty tensor")
+    shape = x.shape
+    if x.dim() == 4:
+        x4 = x
+    elif granularity == "tensor":
+        last = shape[-1] if x.dim() else 1
+        x4 = x.reshape(1, 1, -1, last)
+    else:
+        raise ValueError(f"expected (B, H, T, D) for {granularity} scales, got {tuple(shape)}")
+    x4, (sb, sh, st) = _prepare(x4)
+    B, H, T, D = x4.shape
+    G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+    out = torch.empty((B, H, T, D), dtype=torch.uint8, device=x.device)
+    scale = torch.empty(G, dtype=torch.float32, device=x.device)
+    ws = _lib.workspace(lib.flw_quant_workspace_bytes(B, H, T, D), x.device)
+    rc = lib.flw_quant_e4m3(x4.data_ptr(), _lib.dtype_code(x.dtype), B, H, T, D, sb, sh, st,
+                            _lib.GRANULARITY[granularity], _lib.LAYOUT_BHTD, out.data_ptr(),
+                            scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    _lib.check(rc, "_per_tensor_fp8")
+    return out.view(torch.float8_e4m3fn).reshape(shape), scale
+
+
+def fp8_swa_attention_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    window: int,
+    *,
+    block_m: int = 64,
+    block_n: int = 32,
+    num_warps: int = 4,
+    num_stages: int = 3,
+    granularity: str = "tensor",
+) -> torch.Tensor:
+    """FP8 sliding-window causal attention forward.
+
+    q/k/v: (B, H, T, D) bf16 or fp32 on the GPU. Returns (B, H, T, D) in q's dtype.
+    ``window``: each query attends to the ``window`` keys at or behind it (window <= 0 gives
+    an all-zero output, as the reference's masking does).
+
+    Inference/forward only -- raises on tensors that require grad rather than silently
+    detaching them. ``block_m``/``block_n``/``num_warps``/``num_stages`` are the reference's
+    Triton tuning knobs; they are accepted for call compatibility and ignored.
+    """
+    del block_m, block_n, num_warps, num_stages
+    try:
+        lib = _lib.load()
+    except RuntimeError as e:
+        raise RuntimeError(f"fp8_swa_attention_forward requires the HIP library: {e}") from e
+    if q.requires_grad or k.requires_grad or v.requires_grad:
+        raise RuntimeError(
+            "fp8_swa_attention_forward is forward-only and has no backward; "
+            "calling it on tensors that require grad would silently detach them.")
+    if q.dim() != 4:
+        raise ValueError(f"expected (B, H, T, D), got {tuple(q.shape)}")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    B, H, T, D = q.shape
+    if D not in (32, 64, 128):
+        raise ValueError(f"head_dim must be 32/64/128 for the MFMA tiling, got {D}")
+    if granularity not in _lib.GRANULARITY:
+        raise ValueError(f"granularity must be one of {sorted(_lib.GRANULARITY)}, got {granularity!r}")
+    _lib.require_gpu(q, k, v)
+    if q.numel() == 0:
+        return torch.empty_like(q)
+    dt = _lib.dtype_code(q.dtype)
+    q, sq = _prepare(q)
+    k, sk = _prepare(k)
+    v, sv = _prepare(v)
+    out = torch.empty((B, H, T, D), device=q.device, dtype=q.dtype)
+    so = out.stride()[:3]
+    ws = _lib.workspace(lib.flw_fp8_swa_workspace_bytes(B, H, T, D), q.device)
+    strides = _lib.i64s(*sq, *sk, *sv, *so)
+    rc = lib.flw_fp8_swa_attention_forward(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, strides, B, H, T, D, int(window),
+        _lib.GRANULARITY[granularity], out.data_ptr(), None, ws.data_ptr(), ws.numel(),
+        _lib.stream_of(q))
+    _lib.check(rc, "fp8_swa_attention_forward")
+    return out
+
+
+def reference_swa_attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int
+) -> torch.Tensor:
+    """Dense fp32 reference for correctness testing. O(T^2) memory -- small shapes only.
+
+    softmax(mask(Q K^T / sqrt(D))) V with valid(i, j) <=> j <= i and i - j < window
+    (fp8_swa_attention.py:262-273); returns q's dtype.
+    """
+    B, H, T, D = q.shape
+    qf, kf, vf = q.float(), k.float(), v.float()
+    scores = (qf @ kf.transpose(-1, -2).contiguous()) / (D ** 0.5)
+    idx = torch.arange(T, device=q.device)
+    keep = (idx[:, None] >= idx[None, :]) & ((idx[:, None] - idx[None, :]) < window)
+    scores = scores.masked_fill(~keep, float("-inf"))
+    return (torch.softmax(scores, dim=-1) @ vf).to(q.dtype)

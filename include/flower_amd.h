@@ -1,0 +1,150 @@
+/*
+ * libflower_amd -- C ABI of the MI355X (gfx950) FP8 sliding-window-attention path.
+ *
+ * Plain pointers and sizes only. Every pointer argument is device memory owned by the caller
+ * (the library never allocates or frees). Every call is asynchronous on `stream` (a
+ * hipStream_t passed as void*; NULL = the default stream) and returns 0 on success or a
+ * FLW_E_* code, with a message available from flw_last_error() on the calling thread.
+ * Strides are in elements. The innermost (D / K) dimension must be contiguous.
+ *
+ * Reference interfaces each entry point replaces are cited as path:line in sims1253/flower.
+ */
+#ifndef FLOWER_AMD_H
+#define FLOWER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLW_ABI_VERSION 1
+
+enum flw_status {
+  FLW_OK = 0,
+  FLW_E_INVALID = 1,      /* bad shape / stride / alignment / null pointer */
+  FLW_E_UNSUPPORTED = 2,  /* valid request this build does not implement (e.g. head_dim 96) */
+  FLW_E_WORKSPACE = 3,    /* workspace too small */
+  FLW_E_LAUNCH = 4        /* HIP launch error */
+};
+
+enum flw_dtype { FLW_F32 = 0, FLW_BF16 = 1 };
+
+/* Scale granularity for a (B, H, T, D) tensor: one scale, one per head h (amax over B, T, D),
+ * or one per (b, h) slice (amax over T, D). Scale arrays hold 1, H or B*H floats. */
+enum flw_granularity { FLW_SCALE_TENSOR = 0, FLW_SCALE_HEAD = 1, FLW_SCALE_BH = 2 };
+
+/* Layout of e4m3 codes written by flw_quant_e4m3:
+ *   FLW_LAYOUT_BHTD  -- contiguous (B, H, T, D), one byte per element;
+ *   FLW_LAYOUT_VTILE -- the attention kernel's V operand: per (b, h) slice, ceil(T/64) tiles of
+ *     64 keys x D bytes (keys past T are zero). Inside a tile, element (key kk, dim d) sits at
+ *        (d/32)*2048 + (kk/32)*1024 + ((d%32) + 32*h)*16 + b,
+ *        r = kk%32, h = (r/4)%2, b = 4*(r/8) + r%4,
+ *     i.e. each 16-byte run is one lane's share of a 32x32x64 FP8 MFMA operand of V^T. */
+enum flw_layout { FLW_LAYOUT_BHTD = 0, FLW_LAYOUT_VTILE = 1 };
+
+/* GEMM modes. A8W8: activations quantised per row to e4m3, FP8 x FP8 MFMA (the _fp8_head
+ * recipe). W8A16: e4m3 weights widened to bf16 in the kernel, bf16 activations unquantised. */
+enum flw_gemm_mode { FLW_GEMM_A8W8 = 0, FLW_GEMM_W8A16 = 1 };
+
+const char* flw_last_error(void);
+int flw_abi_version(void);
+
+/* ---------------------------------------------------------------- quantisation */
+
+/* Workspace for flw_quant_e4m3 / flw_fake_quant_e4m3 on a (B, H, T, D) tensor (amax partials). */
+size_t flw_quant_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
+
+/* Bytes of a FLW_LAYOUT_VTILE buffer for a (B, H, T, D) tensor: B*H*ceil(T/64)*64*D. */
+size_t flw_vtile_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
+
+/* e4m3 quantisation with amax scales, replacing `_per_tensor_fp8`
+ * (flower/kernels/fp8_swa_attention.py:195-205) and extending it to per-head / per-(b,h):
+ *   scale = max(amax, 1e-12) / 448  (fp32),  code = e4m3_rne(clamp(x / scale, -448, 448)).
+ * The scale stays on the device (scale_out: 1, H or B*H floats); no host synchronisation.
+ * x: fp32 or bf16, strides in elements, D contiguous, 16-byte aligned rows. */
+int flw_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                   int64_t stride_b, int64_t stride_h, int64_t stride_t, int granularity,
+                   int layout, uint8_t* out, float* scale_out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Straight-through fake quantisation forward value, replacing `_fake_quant_e4m3`
+ * (flower/models/base.py:167-203): out = x + (e4m3(x / s) * s - x), every step rounded to the
+ * input dtype exactly as the reference's op sequence rounds (s itself in the input dtype).
+ * out: contiguous (B, H, T, D) of the input dtype. scale_out may be NULL. */
+int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                        int64_t stride_b, int64_t stride_h, int64_t stride_t, int granularity,
+                        void* out, float* scale_out, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Per-row e4m3 quantisation of a [rows, cols] matrix, replacing the scale / cast steps of
+ * `CausalLM._fp8_head` (flower/models/base.py:912-918), used for GEMM activation rows and for
+ * weight output channels (FP8 weight cache):
+ *   scale[r] = max(amax_r / 448, 1e-12),  code = e4m3_rne(x / scale[r])  (no clamp).
+ * out: contiguous [rows, cols]; scale_out: [rows]. */
+int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                        uint8_t* out, float* scale_out, void* stream);
+
+/* ---------------------------------------------------------------- attention */
+
+/* FP8 causal sliding-window attention forward on pre-quantised operands, replacing the launch
+ * of `_fp8_swa_fwd_kernel` (flower/kernels/fp8_swa_attention.py:249-258):
+ *   q8, k8: (B, H, T, D) e4m3 with element strides q_strides[3] / k_strides[3] = {b, h, t};
+ *   v_tiles: FLW_LAYOUT_VTILE e4m3 V;  scales: 1, H or B*H floats each (granularity);
+ *   out: (B, H, T, D) fp32 or bf16 with strides out_strides[3].
+ * Query i attends to keys j with j <= i and i - j < window; window <= 0 gives zeros.
+ * D in {32, 64, 128}. */
+int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                    const int64_t* k_strides, const uint8_t* v_tiles, const float* q_scale,
+                    const float* k_scale, const float* v_scale, int granularity, void* out,
+                    int out_dtype, const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
+                    int64_t D, int64_t window, void* stream);
+
+/* Workspace of flw_fp8_swa_attention_forward (e4m3 Q, K, tiled V, scales, amax partials). */
+size_t flw_fp8_swa_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
+
+/* The whole `fp8_swa_attention_forward(q, k, v, window)` of
+ * flower/kernels/fp8_swa_attention.py:208-259: quantise Q, K, V (granularity as above), then
+ * the fused FP8 attention; output in the input dtype. strides: 12 values, {b, h, t} of q, k, v,
+ * out. scales_out (3 x 1|H|B*H floats: q, k, v) may be NULL. */
+int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, int dtype,
+                                  const int64_t* strides, int64_t B, int64_t H, int64_t T,
+                                  int64_t D, int64_t window, int granularity, void* out,
+                                  float* scales_out, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/* ---------------------------------------------------------------- GEMM */
+
+/* Workspace of flw_fp8_linear (the per-row e4m3 activations and their scales in A8W8 mode). */
+size_t flw_fp8_linear_workspace_bytes(int64_t M, int64_t K, int mode);
+
+/* y[M, N] (bf16) = x[M, K] (bf16) @ dequant(w8[N, K])^T, replacing the FP8 GEMM of
+ * torchao Float8Linear / `torch._scaled_mm` (flower/models/base.py:919-923,
+ * flower/precision.py:304-324). w_scale: N floats (per output channel) or 1 float
+ * (w_scale_count = 1, per tensor). A8W8 quantises x per row (flw_quant_rows_e4m3 semantics)
+ * into the workspace first. Requires K % 64 == 0, N % 16 == 0. */
+int flw_fp8_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride, const uint8_t* w8,
+                   int64_t N, const float* w_scale, int64_t w_scale_count, int mode, void* y,
+                   int64_t y_row_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The scaled FP8 GEMM alone: y[M, N] (bf16) = (x8[M, K] . w8[N, K]) * x_scale[m] * w_scale[n],
+ * fp32 accumulation (`torch._scaled_mm(x8, w8.t(), scale_a, scale_b, out_dtype=bf16)`,
+ * flower/models/base.py:919-923). Scale counts: M or 1, and N or 1. */
+int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
+                      const float* x_scale, int64_t x_scale_count, const float* w_scale,
+                      int64_t w_scale_count, void* y, int64_t y_row_stride, void* stream);
+
+/* ---------------------------------------------------------------- diagnostics */
+
+/* No counterpart in the reference. Converts n fp32 values to e4m3 codes on the device, with the
+ * hardware instruction the attention kernel uses for P (hardware = 1, v_cvt_pk_fp8_f32, n even)
+ * or with the library's exact software rounding (hardware = 0), so a test can check the two
+ * agree bit for bit on the values the kernel feeds it. */
+int flw_diag_cvt_e4m3(const float* x, uint8_t* out, int64_t n, int hardware, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLOWER_AMD_H */

@@ -1,0 +1,72 @@
+"""CPU: the C-ABI library loads and exports exactly what include/flower_amd.h declares."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flower_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(flw_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_path_entry_points():
+    names = declared_functions()
+    for must in ("flw_quant_e4m3", "flw_fake_quant_e4m3", "flw_quant_rows_e4m3", "flw_fp8_swa_fwd",
+                 "flw_fp8_swa_attention_forward", "flw_fp8_linear", "flw_fp8_scaled_mm",
+                 "flw_last_error", "flw_abi_version"):
+        assert must in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/flower_amd.h but not exported"
+    # the Python binding types exactly the declared set
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def test_host_only_calls_work_without_a_gpu():
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = _lib.load()
+    assert lib.flw_abi_version() == 1
+    assert lib.flw_vtile_bytes(2, 3, 100, 64) == 2 * 3 * 128 * 64
+    assert lib.flw_quant_workspace_bytes(1, 1, 1000, 64) == 4 * 4          # 4 chunks of 256 rows
+    assert lib.flw_fp8_swa_workspace_bytes(4, 16, 8192, 64) >= 3 * 4 * 16 * 8192 * 64
+    # argument validation happens on the host, before any device work
+    rc = lib.flw_fp8_swa_fwd(None, None, None, None, None, None, None, None, 0, None, 0, None,
+                             1, 1, 64, 64, 16, None)
+    assert rc == 1 and b"null" in lib.flw_last_error()
+    s = _lib.i64s(0, 0, 0)
+    rc = lib.flw_fp8_swa_fwd(16, s, 16, s, 16, 16, 16, 16, 0, 16, 1, s, 1, 1, 64, 96, 16, None)
+    assert rc == 2 and b"head_dim" in lib.flw_last_error()
+    rc = lib.flw_fp8_linear(16, 8, 64, 64, 16, 16, 16, 16, 1, 16, 16, 16, 1 << 20, None)
+    assert rc == 2 and b"not implemented" in lib.flw_last_error()
+
+
+def test_operators_refuse_cpu_tensors():
+    """No silent CPU fallback: the product path raises on host tensors."""
+    import torch
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    from flower_amd.kernels.fp8_swa_attention import _per_tensor_fp8, fp8_swa_attention_forward
+    from flower_amd.attention import _fake_quant_e4m3
+    x = torch.randn(1, 2, 64, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        fp8_swa_attention_forward(x, x, x, 16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        _per_tensor_fp8(x)
+    with pytest.raises(RuntimeError, match="GPU"):
+        _fake_quant_e4m3(x)

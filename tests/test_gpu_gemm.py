@@ -1,0 +1,176 @@
+"""GPU parity: FP8 GEMM and the FP8 weight cache (C ABI via flower_amd) vs the CPU oracle.
+
+Gate: against the float64 closed form on the same e4m3 codes and scales, every output within
+one bf16 rounding step plus fp32-accumulation slack: |d| <= 2^-7 * |ref| + 1e-3 * rms(ref).
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from gpu_util import seeded, to_np
+from oracle.gemm import fp8_linear_a8w8, scaled_mm
+from oracle.quant import rowwise_fp8
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_gemm_close(got, ref):
+    got = got.astype(np.float64)
+    ref = ref.astype(np.float64)
+    tol = 2.0 ** -7 * np.abs(ref) + 1e-3 * np.sqrt(np.mean(ref ** 2))
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance; max |d| {np.abs(got - ref).max()}"
+
+
+def codes(shape, seed):
+    """Random finite e4m3 codes (no NaN)."""
+    c = np.random.default_rng(seed).integers(0, 256, size=shape, dtype=np.uint8)
+    c[(c & 0x7F) == 0x7F] = 0x38
+    return c
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 256, 512), (100, 36, 80), (257, 132, 1040), (1, 16, 16)])
+@pytest.mark.parametrize("sx_per_row,sw_per_col", [(True, True), (False, False), (True, False)])
+def test_scaled_mm_matches_closed_form(M, N, K, sx_per_row, sw_per_col):
+    from flower_amd import _lib as L
+    lb = L.load()
+    x8, w8 = codes((M, K), 1), codes((N, K), 2)
+    rng = np.random.default_rng(3)
+    sx = rng.uniform(0.001, 0.01, M if sx_per_row else 1).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N if sw_per_col else 1).astype(np.float32)
+    tx8, tw8 = torch.from_numpy(x8).cuda(), torch.from_numpy(w8).cuda()
+    tsx, tsw = torch.from_numpy(sx).cuda(), torch.from_numpy(sw).cuda()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    L.check(lb.flw_fp8_scaled_mm(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), sx.size,
+                                 tsw.data_ptr(), sw.size, y.data_ptr(), N, L.stream_of(y)), "scaled_mm")
+    ref = scaled_mm(x8, w8, np.broadcast_to(sx, (M,)), np.broadcast_to(sw, (N,)))
+    assert_gemm_close(to_np(y), ref)
+
+
+def test_config2_fp8_linear_full_size():
+    """W [4096 x 1024] ~ N(0, 0.02) bf16 per-channel e4m3; X [8192 x 1024]
+    ~ N(0, 1) bf16 with 0.1% outliers x20; A8W8 output checked on sampled rows against the
+    closed form, activation codes bit-exact."""
+    from flower_amd.precision import fp8_linear_forward, quantize_weight
+    g = torch.Generator().manual_seed(7)
+    W = (torch.randn(4096, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    X = torch.randn(8192, 1024, generator=g)
+    idx = torch.randperm(X.numel(), generator=g)[: X.numel() // 1000]
+    X.view(-1)[idx] *= 20
+    X = X.to(torch.bfloat16)
+    w8, ws = quantize_weight(W.cuda(), "rowwise")
+    want_w8, want_ws = rowwise_fp8(W.float().numpy())
+    np.testing.assert_array_equal(to_np(w8), want_w8)
+    np.testing.assert_array_equal(to_np(ws), want_ws.reshape(-1))
+    y = to_np(fp8_linear_forward(X.cuda(), w8, ws))
+    rows = np.random.default_rng(0).choice(8192, 256, replace=False)
+    ref, _, _ = fp8_linear_a8w8(X.float().numpy()[rows], want_w8, want_ws.reshape(-1))
+    assert_gemm_close(y[rows], ref)
+    # vs the unquantised bf16 product: the reference's FP8-head acceptance bounds
+    # (tests/test_training_speedups.py:375-389)
+    full = (X.float().numpy()[rows] @ W.float().numpy().T)
+    rel = np.linalg.norm(y[rows] - full) / np.linalg.norm(full)
+    assert rel < 0.05 and 0.9 < np.linalg.norm(y[rows]) / np.linalg.norm(full) < 1.1, rel
+
+
+def test_fp8_linear_module_matches_bf16_linear_and_backprops():
+    from flower_amd.precision import Fp8Linear
+    torch.manual_seed(0)
+    lin = nn.Linear(256, 512, bias=True).cuda().to(torch.bfloat16)
+    f8 = Fp8Linear.from_linear(lin)
+    x = torch.randn(4, 32, 256, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    y = f8(x)
+    ref = lin(x.detach())
+    rel = ((y.float() - ref.float()).norm() / ref.float().norm()).item()
+    assert y.shape == (4, 32, 512) and y.dtype == torch.bfloat16 and rel < 0.05, rel
+    y.float().square().mean().backward()
+    assert x.grad is not None and lin.weight.grad is not None and torch.isfinite(x.grad).all()
+
+
+# ---------------------------------------------------------------- fp8_weight_cache (test_fp8_weight_cache.py)
+
+def _fp8_model(d: int = 256, hid: int = 512) -> nn.Module:
+    from flower_amd.precision import Fp8Linear
+    torch.manual_seed(0)
+    m = nn.Sequential(nn.Linear(d, hid, bias=False), nn.Linear(hid, d, bias=False))
+    m = m.cuda().to(torch.bfloat16)
+    return nn.Sequential(*(Fp8Linear.from_linear(l) for l in m))
+
+
+@pytest.mark.parametrize("recipe", ["rowwise", "tensorwise"])
+def test_cached_is_bit_identical_to_uncached(recipe):
+    from flower_amd.precision import fp8_weight_cache
+    accum = 3
+    xs = [torch.randn(128, 256, device="cuda", dtype=torch.bfloat16) for _ in range(accum)]
+
+    def run(use_cache: bool):
+        m = _fp8_model()
+        for mod in m:
+            mod.recipe = recipe
+        opt = torch.optim.SGD(m.parameters(), lr=0.01)
+        for _ in range(2):
+            opt.zero_grad(set_to_none=True)
+            if use_cache:
+                with fp8_weight_cache(m):
+                    for x in xs:
+                        m(x).float().square().mean().backward()
+            else:
+                for x in xs:
+                    m(x).float().square().mean().backward()
+            opt.step()
+        return [p.detach().float().clone() for p in m.parameters()]
+
+    for a, b in zip(run(False), run(True)):
+        assert torch.equal(a, b), "cached path diverged from uncached"
+
+
+def test_raises_when_a_weight_changes_while_cache_is_live():
+    from flower_amd.precision import fp8_weight_cache
+    m = _fp8_model()
+    x = torch.randn(128, 256, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="stale"):
+        with fp8_weight_cache(m):
+            m(x).float().sum().backward()
+            with torch.no_grad():
+                m[0].weight.data -= 0.1
+            m(x).float().sum().backward()
+
+
+def test_forwards_are_restored_after_exit_and_after_exception():
+    from flower_amd.precision import fp8_weight_cache
+    m = _fp8_model()
+    before = [mod.forward for mod in m]
+    with fp8_weight_cache(m):
+        pass
+    assert all(mod.forward == orig for mod, orig in zip(m, before))
+    with pytest.raises(ValueError):
+        with fp8_weight_cache(m):
+            raise ValueError("boom")
+    assert all(mod.forward == orig for mod, orig in zip(m, before))
+
+
+def test_cache_uses_one_quantisation_per_enter():
+    """Inside the cache the layer must not re-quantise its weight on each microstep."""
+    from flower_amd.precision import Fp8Linear, fp8_weight_cache
+    m = _fp8_model()
+    calls = {"n": 0}
+    orig = Fp8Linear.quantize_weight
+
+    def counting(self):
+        calls["n"] += 1
+        return orig(self)
+
+    Fp8Linear.quantize_weight = counting
+    try:
+        x = torch.randn(64, 256, device="cuda", dtype=torch.bfloat16)
+        with fp8_weight_cache(m):
+            for _ in range(4):
+                m(x)
+        assert calls["n"] == 2
+        m(x)
+        assert calls["n"] == 4
+    finally:
+        Fp8Linear.quantize_weight = orig
+

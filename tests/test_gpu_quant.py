@@ -1,0 +1,215 @@
+"""GPU parity: e4m3 quantisers (C ABI via flower_amd) vs the CPU oracle, bit-exact."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import seeded, to_np, vtile_permute
+from oracle.e4m3 import f32_to_e4m3
+from oracle.quant import fake_quant_e4m3, per_tensor_fp8, rowwise_fp8
+
+pytestmark = pytest.mark.gpu
+
+
+def lib():
+    from flower_amd import _lib
+    return _lib
+
+
+def near_ties(shape, seed, amax=3.0):
+    from test_oracle_quant import near_tie_input
+    return torch.from_numpy(near_tie_input(shape, seed, amax))
+
+
+# ------------------------------------------------------------------ the hardware P conversion
+
+def test_hw_fp8_convert_is_exact_on_the_attention_P_range():
+    """v_cvt_pk_fp8_f32 (used for P * 448 in the attention kernel) against the library's exact
+    rounding, on EVERY fp32 value in [0, 448 * (1 + 2^-20)], compared on the device."""
+    L = lib()
+    lb = L.load()
+    hi = int(np.array([448.0], np.float32).view(np.int32)[0]) + 16
+    chunk = 1 << 26
+    bad = 0
+    for start in range(0, hi + 1, chunk):
+        n = min(chunk, hi + 1 - start)
+        n += n % 2
+        x = torch.arange(start, start + n, dtype=torch.int64, device="cuda").to(torch.int32).view(torch.float32)
+        hw = torch.empty(n, dtype=torch.uint8, device="cuda")
+        sw = torch.empty(n, dtype=torch.uint8, device="cuda")
+        s = L.stream_of(x)
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), hw.data_ptr(), n, 1, s), "hw")
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), sw.data_ptr(), n, 0, s), "sw")
+        bad += int((hw != sw).sum())
+    assert bad == 0, f"{bad} hardware conversions differ from exact RNE"
+
+
+def test_device_exact_rounding_matches_oracle():
+    """The device's software e4m3 rounding (used by the quantisers) vs the oracle, on random
+    bit patterns, every e4m3 midpoint +-4 ulp, NaN and inf."""
+    L = lib()
+    lb = L.load()
+    from test_oracle_e4m3 import _boundaries
+    pts = _boundaries()
+    u = pts.view(np.int32).astype(np.int64)
+    cand = (u[:, None] + np.arange(-4, 5)[None, :]).reshape(-1)
+    cand = cand[(cand >= -(2 ** 31)) & (cand < 2 ** 31)].astype(np.int32).view(np.float32)
+    rnd = np.random.default_rng(0).integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([cand, rnd, np.array([np.nan, -np.nan, np.inf, -np.inf], np.float32)])
+    xt = torch.from_numpy(x).cuda()
+    out = torch.empty(x.size, dtype=torch.uint8, device="cuda")
+    L.check(lb.flw_diag_cvt_e4m3(xt.data_ptr(), out.data_ptr(), x.size, 0, L.stream_of(xt)), "sw")
+    np.testing.assert_array_equal(out.cpu().numpy(), f32_to_e4m3(x))
+
+
+# ------------------------------------------------------------------ _per_tensor_fp8
+
+CASES = [
+    # (shape, dtype, maker)
+    ((2, 4, 256, 64), torch.float32, "randn"),
+    ((2, 4, 256, 64), torch.bfloat16, "randn"),
+    ((1, 8, 1024, 64), torch.float32, "randn"),          # BASELINE config 1 shape
+    ((2, 3, 100, 32), torch.bfloat16, "randn"),          # ragged T
+    ((2, 4, 64, 32), torch.float32, "ties"),
+    ((2, 4, 64, 32), torch.float32, "zeros"),
+    ((1, 2, 300, 128), torch.bfloat16, "lognormal_heads"),
+    ((3, 5, 257, 64), torch.float32, "tiny"),
+]
+
+
+def make(shape, dtype, kind, seed=0):
+    if kind == "randn":
+        x = seeded(shape, seed, torch.float32, "cpu")
+    elif kind == "ties":
+        x = near_ties(shape, seed)
+    elif kind == "zeros":
+        x = torch.zeros(shape)
+    elif kind == "lognormal_heads":
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(*shape, generator=g) * torch.randn(1, shape[1], 1, 1, generator=g).exp()
+    elif kind == "tiny":
+        x = seeded(shape, seed, torch.float32, "cpu") * 1e-30
+    else:
+        raise ValueError(kind)
+    return x.to(dtype).cuda()
+
+
+@pytest.mark.parametrize("shape,dtype,kind", CASES)
+@pytest.mark.parametrize("granularity", ["tensor", "head", "bh"])
+def test_per_tensor_fp8_codes_and_scales_bit_exact(shape, dtype, kind, granularity):
+    from flower_amd.kernels.fp8_swa_attention import _per_tensor_fp8
+    x = make(shape, dtype, kind)
+    q8, scale = _per_tensor_fp8(x, granularity)
+    torch.cuda.synchronize()
+    want_codes, want_scale = per_tensor_fp8(to_np(x), granularity)
+    np.testing.assert_array_equal(to_np(q8), want_codes)
+    np.testing.assert_array_equal(to_np(scale).view(np.uint32), want_scale.reshape(-1).view(np.uint32))
+
+
+def test_per_tensor_fp8_strided_input():
+    """q as the model produces it: x.view(B, T, H, D).transpose(1, 2) (base.py:612-614)."""
+    from flower_amd.kernels.fp8_swa_attention import _per_tensor_fp8
+    B, T, H, D = 2, 192, 4, 64
+    x = seeded((B, T, H * D), 3, torch.bfloat16).view(B, T, H, D).transpose(1, 2)
+    assert not x.is_contiguous()
+    q8, scale = _per_tensor_fp8(x, "head")
+    want_codes, want_scale = per_tensor_fp8(to_np(x.contiguous()), "head")
+    np.testing.assert_array_equal(to_np(q8), want_codes)
+    np.testing.assert_array_equal(to_np(scale), want_scale.reshape(-1))
+
+
+def test_nan_input_gives_nan_scale_and_codes_like_the_reference():
+    from flower_amd.kernels.fp8_swa_attention import _per_tensor_fp8
+    x = seeded((1, 2, 64, 32), 4, torch.float32, "cpu")
+    x[0, 1, 5, 7] = float("nan")
+    q8, scale = _per_tensor_fp8(x.cuda(), "head")
+    want_codes, want_scale = per_tensor_fp8(x.numpy(), "head")
+    np.testing.assert_array_equal(to_np(q8), want_codes)
+    s = to_np(scale)
+    assert np.isnan(s[1]) and s[0] == want_scale.reshape(-1)[0]
+
+
+@pytest.mark.parametrize("shape,dtype", [((2, 3, 100, 64), torch.bfloat16), ((1, 2, 64, 32), torch.float32),
+                                         ((1, 1, 257, 128), torch.bfloat16)])
+def test_vtile_layout_is_the_documented_permutation(shape, dtype):
+    L = lib()
+    lb = L.load()
+    x = make(shape, dtype, "randn", seed=5)
+    B, H, T, D = shape
+    out = torch.empty(lb.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(H, dtype=torch.float32, device="cuda")
+    ws = L.workspace(lb.flw_quant_workspace_bytes(B, H, T, D), "cuda")
+    sb, sh, st, _ = x.stride()
+    L.check(lb.flw_quant_e4m3(x.data_ptr(), L.dtype_code(dtype), B, H, T, D, sb, sh, st, L.SCALE_HEAD,
+                              L.LAYOUT_VTILE, out.data_ptr(), sc.data_ptr(), ws.data_ptr(), ws.numel(),
+                              L.stream_of(x)), "vtile")
+    want_codes, want_scale = per_tensor_fp8(to_np(x), "head")
+    np.testing.assert_array_equal(out.cpu().numpy(), vtile_permute(want_codes))
+    np.testing.assert_array_equal(to_np(sc), want_scale.reshape(-1))
+
+
+# ------------------------------------------------------------------ _fake_quant_e4m3
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["randn", "ties", "zeros", "tiny"])
+def test_fake_quant_matches_reference_sequence_bit_exact(dtype, kind):
+    from flower_amd.attention import _fake_quant_e4m3
+    x = make((2, 2, 96, 64), dtype, kind, seed=6)
+    y = _fake_quant_e4m3(x)
+    want, _, _ = fake_quant_e4m3(to_np(x), "f32" if dtype == torch.float32 else "bf16")
+    assert y.dtype == dtype and y.shape == x.shape
+    np.testing.assert_array_equal(to_np(y).view(np.uint32), want.view(np.uint32))
+
+
+def test_fake_quant_gradient_passes_straight_through():      # test_fp8_attention_sim.py:40-52
+    from flower_amd.attention import _fake_quant_e4m3
+    x = seeded((2, 2, 8, 16), 0).requires_grad_(True)
+    y = _fake_quant_e4m3(x)
+    g = seeded((2, 2, 8, 16), 1)
+    y.backward(g)
+    assert torch.equal(x.grad, g)
+
+
+def test_fake_quant_is_actually_quantized_and_zero_safe():     # :23-29, :69-74
+    from flower_amd.attention import _fake_quant_e4m3
+    x = seeded((2, 2, 32, 16), 0) * 0.5
+    y = _fake_quant_e4m3(x)
+    assert not torch.equal(y, x) and (y - x).abs().mean() > 0
+    z = torch.zeros(2, 2, 8, 16, device="cuda")
+    assert torch.equal(_fake_quant_e4m3(z), z)
+
+
+# ------------------------------------------------------------------ per-row (GEMM / weight cache)
+
+@pytest.mark.parametrize("rows,cols,dtype,skew", [(128, 512, torch.bfloat16, 0.0), (100, 1024, torch.bfloat16, -2.5),
+                                                  (37, 64, torch.float32, 0.0), (4096, 1024, torch.bfloat16, 0.0)])
+def test_rowwise_quant_bit_exact(rows, cols, dtype, skew):
+    from flower_amd import _lib as L
+    lb = L.load()
+    x = (seeded((rows, cols), 7, torch.float32) + skew).to(dtype)
+    out = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(rows, dtype=torch.float32, device="cuda")
+    L.check(lb.flw_quant_rows_e4m3(x.data_ptr(), L.dtype_code(dtype), rows, cols, cols, out.data_ptr(),
+                                   sc.data_ptr(), L.stream_of(x)), "rows")
+    want_codes, want_scale = rowwise_fp8(to_np(x))
+    np.testing.assert_array_equal(to_np(out), want_codes)
+    np.testing.assert_array_equal(to_np(sc), want_scale.reshape(-1))
+
+
+def test_abi_rejects_bad_arguments():
+    L = lib()
+    lb = L.load()
+    x = torch.zeros(1, 1, 64, 60, device="cuda")       # D not a multiple of 4? 60 is; use 62 bf16
+    xb = torch.zeros(1, 1, 64, 62, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(64 * 62, dtype=torch.uint8, device="cuda")
+    sc = torch.empty(1, device="cuda")
+    ws = L.workspace(1024, "cuda")
+    rc = lb.flw_quant_e4m3(xb.data_ptr(), L.BF16, 1, 1, 64, 62, 64 * 62, 64 * 62, 62, 0, 0, out.data_ptr(),
+                           sc.data_ptr(), ws.data_ptr(), ws.numel(), None)
+    assert rc == 2 and b"multiple" in lb.flw_last_error()
+    rc = lb.flw_quant_e4m3(x.data_ptr(), L.F32, 1, 1, 64, 60, 64 * 60, 64 * 60, 60, 0, 0, out.data_ptr(),
+                           sc.data_ptr(), ws.data_ptr(), 0, None)
+    assert rc == 3 and b"workspace" in lb.flw_last_error()
+    assert ctypes.c_int(rc).value == 3
