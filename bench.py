@@ -37,6 +37,7 @@ sys.path.insert(0, ROOT)
 METRIC = "FP8 SWA attn fwd TFLOPS + % FP8 MFMA peak at T=8192,W=1024; quant GB/s"
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
 HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E
+COPY_PROBE_BYTES = 256 << 20
 
 WORKLOADS = {
     "c3": dict(B=4, H=16, T=8192, D=64, W=1024, granularity="head", inputs="lognormal_heads"),
@@ -189,6 +190,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first run one plain 256 MiB device copy, the reference point that scales "
+                         "the HBM byte counters of a rocprofv3 --pmc run")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU (every box here has one); the "
@@ -198,6 +202,11 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     cfg = WORKLOADS[args.workload]
+    if args.copy_probe:
+        src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     r = bench_attention(cfg, args.steps, args.warmup)
     value = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
     attn_tflops = r["flops"] / (r["attn_ms"] * 1e-3) / 1e12

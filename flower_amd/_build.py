@@ -3,7 +3,8 @@
     python -m flower_amd._build          # compile all HIP sources into flower_amd/libflower_amd.so
 
 One shared object, C ABI only (include/flower_amd.h). Every HIP source is compiled with packed
-FP32 instructions disabled (``-target-feature -packed-fp32-ops``).
+FP32 instructions disabled (``-target-feature -packed-fp32-ops``); sources compile in parallel
+into ``_build/`` and are linked with ``hipcc -shared``.
 """
 
 from __future__ import annotations
@@ -16,9 +17,23 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
+OBJDIR = os.path.join(ROOT, "_build")
 LIB = os.path.join(HERE, "libflower_amd.so")
 SOURCES = ["flw_error.hip", "flw_quant.hip", "flw_swa.hip", "flw_gemm.hip", "flw_selftest.hip"]
 ARCH = os.environ.get("FLW_OFFLOAD_ARCH", "gfx950")
+
+COMMON = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the attention rescale and the GEMM epilogue then
+    # work on them in place instead of copying through AGPRs.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    "-Wno-unused-result", "-I", os.path.join(ROOT, "include"),
+]
+# The attention kernel's max reductions run on MFMA results; in IEEE mode every fmax operand is
+# first re-quietened (one extra VALU op per score). NaN inputs still give NaN rows without it.
+PER_SOURCE = {"flw_swa.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
+NOISE = "'-packed-fp32-ops' is not a recognized feature"
 
 
 def hipcc() -> str:
@@ -28,25 +43,36 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain (ROCm) is required to build libflower_amd")
 
 
+def _run_all(cmds, verbose):
+    procs = []
+    for cmd in cmds:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    errors = []
+    for cmd, pr in procs:
+        _, err = pr.communicate()
+        err = "\n".join(l for l in err.splitlines() if NOISE not in l)
+        if pr.returncode != 0:
+            errors.append(f"{cmd[-3] if len(cmd) > 3 else cmd}: hipcc failed ({pr.returncode}):\n{err}")
+        elif verbose and err.strip():
+            print(err, file=sys.stderr)
+    if errors:
+        raise RuntimeError("\n".join(errors))
+
+
 def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    os.makedirs(OBJDIR, exist_ok=True)
+    cc = hipcc()
+    objs, cmds = [], []
+    for s in SOURCES:
+        src = os.path.join(CSRC, s)
+        obj = os.path.join(OBJDIR, s.replace(".hip", ".o"))
+        objs.append(obj)
+        cmds.append([cc, *COMMON, *PER_SOURCE.get(s, []), "-c", src, "-o", obj])
+    _run_all(cmds, verbose)
     tmp = LIB + ".tmp"
-    cmd = [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-Wno-unused-result", "-I", os.path.join(ROOT, "include"),
-        *srcs, "-o", tmp,
-    ]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass warns that it does not know the packed-fp32 feature; that is expected.
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    errs = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{errs}")
-    if verbose and errs.strip():
-        print(errs, file=sys.stderr)
+    _run_all([[cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]], verbose)
     os.replace(tmp, LIB)
     return LIB
 

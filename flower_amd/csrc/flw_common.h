@@ -26,11 +26,12 @@ constexpr float kEps = 1e-12f;   // the reference's amax / scale floor
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (quiet).
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (quiet). The NaN test is on the bit
+// pattern so it holds in translation units built with relaxed NaN handling.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
   uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-  return (f != f) ? 0x7FC0u : r;
+  return (u & 0x7FFFFFFFu) > 0x7F800000u ? 0x7FC0u : r;
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
 

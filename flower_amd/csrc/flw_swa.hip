@@ -1,19 +1,27 @@
 // FP8 causal sliding-window attention forward for gfx950 (CDNA4).
 //
 // Work decomposition: one workgroup = 4 waves = 128 queries of one (b, h) slice; each wave owns
-// 32 queries. The workgroup walks 64-key tiles over the band [m0 - W + 1, m0 + 127] only (tiles
-// wholly outside the window are never visited); a wave skips the tiles that miss its own
+// 32 queries. The workgroup walks 64-key tiles over its band [m0 - W + 1, m0 + 127] only (tiles
+// wholly outside the window are never visited); a wave computes only the tiles that meet its own
 // 32-query band. Per tile a wave computes S^T = K Q^T with two v_mfma_f32_32x32x64_f8f6f4 (keys
 // are the MFMA rows, queries the columns, so every lane holds 32 scores of ONE query and the row
-// max / sum are lane-local plus one exchange with lane^32), runs the online softmax in base 2
-// with the softmax scale, log2(e) and the x448 P pre-scale folded into one FMA, packs P to
-// e4m3 in registers (v_cvt_pk_fp8_f32) straight into the B operand of O^T += V^T P^T
-// (D/32 more MFMAs). K tiles are staged in LDS in MFMA-fragment order (a permutation of 16-byte
-// chunks of the row-major tile); V arrives already in that order from the quantiser
-// (FLW_LAYOUT_VTILE), so every fragment read is a conflict-free linear ds_read_b128.
-// Tiles are double-buffered in LDS with one barrier per tile; the next tile's global loads are
-// issued before the current tile's MFMAs. Workgroups are dealt to the 8 XCDs so that each XCD
-// works through contiguous query tiles of the same heads and re-reads K/V from its own L2.
+// max / sum are lane-local plus one v_permlane32_swap with lane^32), runs the online softmax in
+// base 2 with the softmax scale, log2(e) and the x448 P pre-scale folded into one FMA, packs P to
+// e4m3 in registers (v_cvt_pk_fp8_f32) straight into the B operand of O^T += V^T P^T (D/32 more
+// MFMAs, accumulators kept in VGPRs so the rescale is one multiply per element).
+//
+// The softmax is VALU-bound (per score: one FMA, one v_exp_f32 at half rate, half a max3, half a
+// convert, one add; per tile D/64 rescale multiplies per score) while the MFMA work per tile is
+// about a third of that, so the loop is arranged to keep the VALU fed: the QK^T MFMAs of tile
+// j+1 are issued before the softmax of tile j, whose PV MFMAs then run under the next tile's
+// VALU work; two workgroups per CU give every SIMD a second wave to interleave.
+//
+// K tiles are staged in LDS in MFMA-fragment order (a permutation of 16-byte chunks of the
+// row-major tile); V arrives already in that order from the quantiser (FLW_LAYOUT_VTILE), so every
+// fragment read is a conflict-free linear ds_read_b128. Three LDS stages, one barrier per tile:
+// the global loads of tile j+2 are in flight while tile j is consumed. Workgroups are dealt to
+// the 8 XCDs so that each XCD works through contiguous query tiles of the same heads and re-reads
+// K/V from its own L2.
 #include <math.h>
 
 #include "flw_common.h"
@@ -31,6 +39,7 @@ __device__ __forceinline__ v16f mfma_32x32x64_f8(v8i a, v8i b, v16f c) {
 constexpr int kWaves = 4;
 constexpr int kBM = 32 * kWaves;   // queries per workgroup
 constexpr int kBN = 64;            // keys per tile
+constexpr int kStages = 3;         // LDS ring of K/V tiles
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLog2_448 = 8.807354922057604f;   // log2(448): P is produced pre-scaled by 448
 
@@ -47,7 +56,7 @@ struct SwaParams {
   int gran;
   void* out;
   int64_t osb, osh, ost;      // element strides of out
-  int H, T, W, nM;
+  int H, T, W, nM, nwg;
 };
 
 template <typename OutT> struct Store4;
@@ -74,6 +83,23 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* lds, int off) {
   return r;
 }
 
+// x combined with its value in lane ^ 32 (the other half of the same query's keys).
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Scores of one 64-key tile for one wave: S^T blocks of keys n0 .. n0+31 and n0+32 .. n0+63.
+// Lane (qcol = lane % 32, hh = lane / 32), element v of block blk holds key
+// n0 + 32 blk + 8 (v / 4) + 4 hh + v % 4 of query q0 + qcol.
+struct Scores {
+  v16f s0, s1;
+};
+
 template <int D, typename OutT>
 __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
   constexpr int NDC = D >= 64 ? D / 64 : 1;   // 64-deep K chunks of the QK^T product
@@ -83,12 +109,15 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
   constexpr int CPR = D / 16;                  // 16-byte chunks per K row
   constexpr int KCH = 64 * CPR;                // chunks per K tile (== V tile chunks)
   constexpr int CPT = (KCH + 255) / 256;       // chunks per thread
-  __shared__ __align__(16) uint8_t lds_k[2][KT_BYTES];
-  __shared__ __align__(16) uint8_t lds_v[2][VT_BYTES];
+  __shared__ __align__(16) uint8_t lds_k[kStages][KT_BYTES];
+  __shared__ __align__(16) uint8_t lds_v[kStages][VT_BYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nwg = gridDim.x;
-  int L = blockIdx.x;
+  // Work-item / group ids through the builtins (this file is built without IEEE mode, and the
+  // device-library accessors are not inlined across that mode difference).
+  const int tid = (int)__builtin_amdgcn_workitem_id_x(), lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
+  const int nwg = p.nwg;
+  int L = (int)__builtin_amdgcn_workgroup_id_x();
   if ((nwg & 7) == 0) L = (L & 7) * (nwg >> 3) + (L >> 3);   // contiguous work per XCD
   const int bh = L / p.nM, mt = L % p.nM;
   const int b = bh / p.H, h = bh % p.H;
@@ -129,9 +158,9 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
       const int i = tid + 256 * j;
       if (i < KCH) {
         const int kk = i / CPR, g = i % CPR;
-        const int row = n0 + kk;
-        kreg[j] = row < T ? *reinterpret_cast<const uint4*>(kbase + (int64_t)row * p.kst + 16 * g)
-                          : make_uint4(0, 0, 0, 0);
+        // Rows past T repeat row T-1: such keys only meet queries past T (masked or not stored).
+        const int row = min(n0 + kk, T - 1);
+        kreg[j] = *reinterpret_cast<const uint4*>(kbase + (int64_t)row * p.kst + 16 * g);
         vreg[j] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(n0 >> 6) * VT_BYTES + 16 * i);
       }
     }
@@ -151,100 +180,125 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
     }
   };
 
-  // Key range of the workgroup, tile-aligned; and of this wave.
+  // Key range of the workgroup, tile-aligned, and this wave's tiles [ta, tb] inside it.
   const int lo_raw = m0 - W + 1;
   const int lo = lo_raw <= 0 ? 0 : (lo_raw & ~(kBN - 1));
   const int hi = min(T, m0 + kBM);
-  const int wlo = q0 - W + 1, whi = q0 + 31;
+  const int nt = hi > lo ? (hi - lo + kBN - 1) / kBN : 0;
+  const int wk0 = max(0, q0 - W + 1), wk1 = min(q0 + 31, T - 1);
+  const int ta = q0 < T ? (wk0 - lo) / kBN : 1;
+  const int tb = q0 < T ? (wk1 - lo) / kBN : 0;
 
   v16f o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = v16f{};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  if (lo < hi) {
-    load_tile(lo);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int n0 = lo, it = 0; n0 < hi; n0 += kBN, ++it) {
-    const int buf = it & 1;
-    const bool more = n0 + kBN < hi;
-    if (more) load_tile(n0 + kBN);
-
-    if (n0 <= whi && n0 + kBN - 1 >= wlo) {
-      const uint8_t* lk = lds_k[buf];
-      const uint8_t* lv = lds_v[buf];
-      v16f s0 = v16f{}, s1 = v16f{};
+  auto qk = [&](Scores& s, int buf) {
+    const uint8_t* lk = lds_k[buf];
+    s.s0 = v16f{};
+    s.s1 = v16f{};
 #pragma unroll
-      for (int dc = 0; dc < NDC; ++dc) {
-        v8i k0 = load_frag(lk, ((0 * NDC + dc) * 2 * 64 + lane) * 16);
-        v8i k1 = load_frag(lk, ((1 * NDC + dc) * 2 * 64 + lane) * 16);
-        if (D == 32 && hh) { k0 = v8i{0, 0, 0, 0, 0, 0, 0, 0}; k1 = k0; }
-        s0 = mfma_32x32x64_f8(k0, qf[dc], s0);
-        s1 = mfma_32x32x64_f8(k1, qf[dc], s1);
+    for (int dc = 0; dc < NDC; ++dc) {
+      v8i k0 = load_frag(lk, ((0 * NDC + dc) * 2 * 64 + lane) * 16);
+      v8i k1 = load_frag(lk, ((1 * NDC + dc) * 2 * 64 + lane) * 16);
+      if (D == 32 && hh) { k0 = v8i{0, 0, 0, 0, 0, 0, 0, 0}; k1 = k0; }
+      s.s0 = mfma_32x32x64_f8(k0, qf[dc], s.s0);
+      s.s1 = mfma_32x32x64_f8(k1, qf[dc], s.s1);
+    }
+  };
+
+  auto softmax_pv = [&](Scores& s, int n0, int buf) {
+    // Mask only where the tile crosses the diagonal or the window start: valid <=> 0 <= i-j < W,
+    // one unsigned compare. Keys past T only meet queries past T, whose rows are not stored.
+    const bool interior = (n0 + kBN - 1 <= q0) && (q0 + 31 - n0 < W);
+    if (!interior) {
+      const int base = q0 + qcol - n0 - 4 * hh;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int kv = 8 * (v >> 2) + (v & 3);
+        s.s0[v] = (unsigned)(base - kv) < (unsigned)W ? s.s0[v] : -INFINITY;
+        s.s1[v] = (unsigned)(base - kv - 32) < (unsigned)W ? s.s1[v] : -INFINITY;
       }
-
-      // Mask only where the tile crosses the diagonal, the window start or T.
-      const bool interior = (n0 + kBN - 1 <= q0) && (q0 + 31 - n0 < W) && (n0 + kBN <= T);
-      if (!interior) {
-        const int qi = q0 + qcol;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int kj = n0 + 8 * (v >> 2) + 4 * hh + (v & 3);
-          const int kj1 = kj + 32;
-          const bool ok0 = kj <= qi && qi - kj < W && kj < T;
-          const bool ok1 = kj1 <= qi && qi - kj1 < W && kj1 < T;
-          s0[v] = ok0 ? s0[v] : -INFINITY;
-          s1[v] = ok1 ? s1[v] : -INFINITY;
-        }
-      }
-
-      float tmax = fmaxf(s0[0], s1[0]);
-#pragma unroll
-      for (int v = 1; v < 16; ++v) tmax = fmaxf(tmax, fmaxf(s0[v], s1[v]));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run, tmax);
-      const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_safe) * c);
-      const float nb = kLog2_448 - m_safe * c;
-
-      float lsum = 0.0f;
-      int pk[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a0 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 0], c, nb));
-        const float a1 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 1], c, nb));
-        const float a2 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 2], c, nb));
-        const float a3 = __builtin_amdgcn_exp2f(fmaf(s0[4 * j + 3], c, nb));
-        const float b0 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 0], c, nb));
-        const float b1 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 1], c, nb));
-        const float b2 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 2], c, nb));
-        const float b3 = __builtin_amdgcn_exp2f(fmaf(s1[4 * j + 3], c, nb));
-        lsum += (a0 + a1) + (a2 + a3) + ((b0 + b1) + (b2 + b3));
-        int wa = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
-        pk[j] = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, wa, true);
-        int wb = __builtin_amdgcn_cvt_pk_fp8_f32(b0, b1, 0, false);
-        pk[4 + j] = __builtin_amdgcn_cvt_pk_fp8_f32(b2, b3, wb, true);
-      }
-      l_run = l_run * alpha + lsum;
-      const v8i pf = v8i{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        o[db] *= alpha;
-        const v8i vf = load_frag(lv, (db * 2 * 64 + lane) * 16);
-        o[db] = mfma_32x32x64_f8(vf, pf, o[db]);
-      }
-      m_run = m_new;
     }
 
-    if (more) store_tile(buf ^ 1);
+    // Row max: four independent chains of v_max3 over 8 scores each.
+    float mx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float m = fmaxf(fmaxf(s.s0[4 * j], s.s0[4 * j + 1]), s.s0[4 * j + 2]);
+      m = fmaxf(fmaxf(m, s.s0[4 * j + 3]), s.s1[4 * j]);
+      m = fmaxf(fmaxf(m, s.s1[4 * j + 1]), s.s1[4 * j + 2]);
+      mx[j] = fmaxf(m, s.s1[4 * j + 3]);
+    }
+    const float tmax = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_safe) * c);
+    const float nb = kLog2_448 - m_safe * c;
+    m_run = m_new;
+
+    float ls[4];
+    int pk[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a0 = __builtin_amdgcn_exp2f(fmaf(s.s0[4 * j + 0], c, nb));
+      const float a1 = __builtin_amdgcn_exp2f(fmaf(s.s0[4 * j + 1], c, nb));
+      const float a2 = __builtin_amdgcn_exp2f(fmaf(s.s0[4 * j + 2], c, nb));
+      const float a3 = __builtin_amdgcn_exp2f(fmaf(s.s0[4 * j + 3], c, nb));
+      const float b0 = __builtin_amdgcn_exp2f(fmaf(s.s1[4 * j + 0], c, nb));
+      const float b1 = __builtin_amdgcn_exp2f(fmaf(s.s1[4 * j + 1], c, nb));
+      const float b2 = __builtin_amdgcn_exp2f(fmaf(s.s1[4 * j + 2], c, nb));
+      const float b3 = __builtin_amdgcn_exp2f(fmaf(s.s1[4 * j + 3], c, nb));
+      ls[j] = ((a0 + a1) + (a2 + a3)) + ((b0 + b1) + (b2 + b3));
+      const int wa = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
+      pk[j] = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, wa, true);
+      const int wb = __builtin_amdgcn_cvt_pk_fp8_f32(b0, b1, 0, false);
+      pk[4 + j] = __builtin_amdgcn_cvt_pk_fp8_f32(b2, b3, wb, true);
+    }
+    l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
+    const v8i pf = v8i{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
+    const uint8_t* lv = lds_v[buf];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const v8i vf = load_frag(lv, (db * 2 * 64 + lane) * 16);
+      o[db] *= alpha;
+      o[db] = mfma_32x32x64_f8(vf, pf, o[db]);
+    }
+  };
+
+  // Prologue: stage tiles 0 and 1; scores of tile 0 if this wave starts there.
+  if (nt > 0) { load_tile(lo); store_tile(0); }
+  if (nt > 1) { load_tile(lo + kBN); store_tile(1); }
+  // Retire every global load so far (Q fragments included) on all paths: the wait-count pass
+  // then knows Q is resident inside the loop and does not drain the tile prefetch before each
+  // QK^T MFMA. 0x0F70 = vmcnt(0), expcnt / lgkmcnt unconstrained.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+
+  Scores sa, sb;
+  if (ta == 0 && ta <= tb) qk(sa, 0);
+
+  // One tile: prefetch tile j+2 (global -> registers), issue the QK^T MFMAs of tile j+1, then the
+  // softmax + PV of tile j, then park tile j+2 in the free LDS stage.
+  auto step = [&](int j, int buf, Scores& cur, Scores& nxt) {
+    const bool pre = j + 2 < nt;
+    if (pre) load_tile(lo + (j + 2) * kBN);
+    const int nbuf = buf == kStages - 1 ? 0 : buf + 1;
+    if (j + 1 >= ta && j + 1 <= tb) qk(nxt, nbuf);
+    if (j >= ta && j <= tb) softmax_pv(cur, lo + j * kBN, buf);
+    if (pre) store_tile(nbuf == kStages - 1 ? 0 : nbuf + 1);
     __syncthreads();
+    return nbuf;
+  };
+  int buf = 0;
+  for (int j = 0; j < nt; j += 2) {
+    buf = step(j, buf, sa, sb);
+    if (j + 1 < nt) buf = step(j + 1, buf, sb, sa);
   }
 
   // Epilogue: out = O * v_scale / l   (l carries the x448 of P, matching pv_scale = v_s / 448)
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = pair_sum(l_run);
   const float inv = l_tot == 0.0f ? 0.0f : v_s / l_tot;
   const int qi = q0 + qcol;
   if (qi < T) {
@@ -303,7 +357,8 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.qs = qs; p.ks = ks; p.vs = vs; p.gran = gran;
   p.out = out; p.osb = ost[0]; p.osh = ost[1]; p.ost = ost[2];
   p.H = (int)H; p.T = (int)T; p.W = (int)W; p.nM = (int)nM;
-  dim3 grid((unsigned)(B * H * nM));
+  p.nwg = (int)(B * H * nM);
+  dim3 grid((unsigned)p.nwg);
   if (D == 32) launch_d<32>(p, out_dtype, grid, stream);
   else if (D == 64) launch_d<64>(p, out_dtype, grid, stream);
   else launch_d<128>(p, out_dtype, grid, stream);
