@@ -58,7 +58,7 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
   uint32_t m = c & 7u;
   float v = e == 0 ? (float)m * 0.001953125f                        // m * 2^-9
                    : __uint_as_float(((e + 120u) << 23) | (m << 20));
-  v = ((c & 0x7Fu) == 0x7Fu) ? __builtin_nanf("") : v;
+  v = ((c & 0x7Fu) == 0x7Fu) ? __uint_as_float(0x7FC00000u) : v;   // NaN, by its bit pattern
   return __uint_as_float(__float_as_uint(v) | s);
 }
 

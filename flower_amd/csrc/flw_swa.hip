@@ -24,6 +24,8 @@
 // K/V from its own L2.
 #include <math.h>
 
+#include <type_traits>
+
 #include "flw_common.h"
 
 namespace flw {
@@ -65,11 +67,14 @@ template <> struct Store4<float> {
     *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
   }
 };
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 template <> struct Store4<uint16_t> {
+  // v_cvt_pk_bf16_f32: round to nearest even, two values per instruction.
   __device__ __forceinline__ static void st(uint16_t* p, float a, float b, float c, float d) {
     uint2 w;
-    w.x = f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
-    w.y = f32_to_bf16_bits(c) | (f32_to_bf16_bits(d) << 16);
+    w.x = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+    w.y = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{c, d}), bf16x2));
     *reinterpret_cast<uint2*>(p) = w;
   }
 };
@@ -100,8 +105,9 @@ struct Scores {
   v16f s0, s1;
 };
 
+// Three workgroups (12 waves) per CU for D <= 64, two for D = 128 (its O^T needs 64 VGPRs).
 template <int D, typename OutT>
-__global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
+__global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParams p) {
   constexpr int NDC = D >= 64 ? D / 64 : 1;   // 64-deep K chunks of the QK^T product
   constexpr int NDB = D / 32;                  // 32-row blocks of O^T
   constexpr int KT_BYTES = 2 * NDC * 2048;     // one K tile in fragment order
@@ -148,33 +154,47 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
     }
   }
 
+  // K rows: scalar tile base + a fixed 32-bit offset per thread; V tiles are contiguous.
   const uint8_t* kbase = p.k8 + b * p.ksb + h * p.ksh;
   const uint8_t* vbase = p.vt + (int64_t)bh * p.vt_slice;
+  uint32_t koff[CPT], ldsk[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int i = min(tid + 256 * j, KCH - 1);
+    const int kk = i / CPR, g = i % CPR;
+    const int d0 = 16 * g;
+    const int blk = kk >> 5, krow = kk & 31, dc = d0 >> 6, h2 = (d0 >> 5) & 1, cc = (d0 >> 4) & 1;
+    koff[j] = (uint32_t)(kk * p.kst + 16 * g);
+    ldsk[j] = (uint32_t)((((blk * NDC + dc) * 2 + cc) * 64 + krow + 32 * h2) * 16);
+  }
   uint4 kreg[CPT], vreg[CPT];
 
-  auto load_tile = [&](int n0) {
+  auto load_tile = [&](int n0) __attribute__((always_inline)) {
+    const uint8_t* kt = kbase + (int64_t)n0 * p.kst;
+    const uint8_t* vtile = vbase + (int64_t)(n0 >> 6) * VT_BYTES;
+    const bool full = n0 + kBN <= T;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int i = tid + 256 * j;
-      if (i < KCH) {
-        const int kk = i / CPR, g = i % CPR;
-        // Rows past T repeat row T-1: such keys only meet queries past T (masked or not stored).
-        const int row = min(n0 + kk, T - 1);
-        kreg[j] = *reinterpret_cast<const uint4*>(kbase + (int64_t)row * p.kst + 16 * g);
-        vreg[j] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(n0 >> 6) * VT_BYTES + 16 * i);
+      if (KCH % 256 == 0 || i < KCH) {
+        if (full) {
+          kreg[j] = *reinterpret_cast<const uint4*>(kt + koff[j]);
+        } else {
+          // Rows past T repeat row T-1: such keys only meet queries past T (not stored).
+          const int kk = i / CPR, g = i % CPR;
+          const int row = min(n0 + kk, T - 1);
+          kreg[j] = *reinterpret_cast<const uint4*>(kbase + (int64_t)row * p.kst + 16 * g);
+        }
+        vreg[j] = *reinterpret_cast<const uint4*>(vtile + 16 * i);
       }
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int i = tid + 256 * j;
-      if (i < KCH) {
-        const int kk = i / CPR, g = i % CPR;
-        const int d0 = 16 * g;
-        const int blk = kk >> 5, krow = kk & 31, dc = d0 >> 6, h2 = (d0 >> 5) & 1, cc = (d0 >> 4) & 1;
-        const int off = (((blk * NDC + dc) * 2 + cc) * 64 + krow + 32 * h2) * 16;
-        *reinterpret_cast<uint4*>(&lds_k[buf][off]) = kreg[j];
+      if (KCH % 256 == 0 || i < KCH) {
+        *reinterpret_cast<uint4*>(&lds_k[buf][ldsk[j]]) = kreg[j];
         *reinterpret_cast<uint4*>(&lds_v[buf][16 * i]) = vreg[j];
       }
     }
@@ -193,8 +213,10 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = v16f{};
   float m_run = -INFINITY, l_run = 0.0f;
+  int pk[8] = {0, 0, 0, 0, 0, 0, 0, 0};     // e4m3 P of the current tile, packed 4 per word
 
-  auto qk = [&](Scores& s, int buf) {
+  // S^T = K Q^T for the tile in LDS stage `buf`.
+  auto qk = [&](Scores& s, int buf) __attribute__((always_inline)) {
     const uint8_t* lk = lds_k[buf];
     s.s0 = v16f{};
     s.s1 = v16f{};
@@ -208,19 +230,48 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
     }
   };
 
-  auto softmax_pv = [&](Scores& s, int n0, int buf) {
-    // Mask only where the tile crosses the diagonal or the window start: valid <=> 0 <= i-j < W,
-    // one unsigned compare. Keys past T only meet queries past T, whose rows are not stored.
-    const bool interior = (n0 + kBN - 1 <= q0) && (q0 + 31 - n0 < W);
-    if (!interior) {
-      const int base = q0 + qcol - n0 - 4 * hh;
+  // Band masking per 32-key block of a tile. d0 = q0 - (first key of the block) is a multiple
+  // of 32, so a block is partial under the causal condition only when d0 == 0, and then element
+  // v of lane (qcol, hh) is valid iff kv(v) <= qcol - 4 hh (kv(v) = 8 (v / 4) + v % 4 is the
+  // key's offset inside the block). When W is a multiple of 32 a block is partial under the
+  // window condition only when d0 == W, with exactly the complementary pattern. Those 16
+  // per-element lane masks are formed once (held as SGPR pairs), so masking such a block is one
+  // v_cndmask per score. Blocks wholly outside the band become -inf; other windows fall back
+  // to one unsigned compare of i - j against W per score.
+  const bool w32 = (W & 31) == 0;
+  bool diag[16];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int kv = 8 * (v >> 2) + (v & 3);
-        s.s0[v] = (unsigned)(base - kv) < (unsigned)W ? s.s0[v] : -INFINITY;
-        s.s1[v] = (unsigned)(base - kv - 32) < (unsigned)W ? s.s1[v] : -INFINITY;
-      }
+  for (int v = 0; v < 16; ++v) diag[v] = 8 * (v >> 2) + (v & 3) <= qcol - 4 * hh;
+
+  auto mask_block = [&](v16f& sb, int blk, int n0) __attribute__((always_inline)) {
+    const int d0 = q0 - n0 - 32 * blk;            // query q0 minus the block's first key
+    const bool causal = d0 < 31;                   // some key of the block is after some query
+    const bool window = d0 + 31 >= W;              // some pair is W or more apart
+    if (!causal && !window) return;
+    if (d0 < 0 || d0 - W > 30) {                   // no pair of the block is in the band
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sb[v] = -INFINITY;
+    } else if (causal && !window && d0 == 0) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sb[v] = diag[v] ? sb[v] : -INFINITY;
+    } else if (window && !causal && w32 && d0 == W) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sb[v] = diag[v] ? -INFINITY : sb[v];
+    } else {
+      const int base = d0 + qcol - 4 * hh;         // i - j for element kv = 0 of this lane
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        sb[v] = (unsigned)(base - (8 * (v >> 2) + (v & 3))) < (unsigned)W ? sb[v] : -INFINITY;
     }
+  };
+
+  // Online softmax of one tile (the reference's update: m_new = max(m, rowmax S),
+  // p = exp(S - m_new), alpha = exp(m - m_new), l = l alpha + sum p, O = O alpha + e4m3(448 p) V),
+  // in base 2 with the scale folded in, then O^T += V^T P^T.
+  auto softmax_pv = [&](Scores& s, int n0, int buf) __attribute__((always_inline)) {
+    // Keys past T only meet queries past T, whose rows are not stored.
+    mask_block(s.s0, 0, n0);
+    mask_block(s.s1, 1, n0);
 
     // Row max: four independent chains of v_max3 over 8 scores each.
     float mx[4];
@@ -238,8 +289,9 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
     const float nb = kLog2_448 - m_safe * c;
     m_run = m_new;
 
+    // P = 448 exp(S - m) as one FMA + exp2 per score, packed to e4m3 two at a time (the old
+    // half of each packed word is overwritten, so last tile's codes serve as the old value).
     float ls[4];
-    int pk[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float a0 = __builtin_amdgcn_exp2f(fmaf(s.s0[4 * j + 0], c, nb));
@@ -251,10 +303,10 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
       const float b2 = __builtin_amdgcn_exp2f(fmaf(s.s1[4 * j + 2], c, nb));
       const float b3 = __builtin_amdgcn_exp2f(fmaf(s.s1[4 * j + 3], c, nb));
       ls[j] = ((a0 + a1) + (a2 + a3)) + ((b0 + b1) + (b2 + b3));
-      const int wa = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
-      pk[j] = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, wa, true);
-      const int wb = __builtin_amdgcn_cvt_pk_fp8_f32(b0, b1, 0, false);
-      pk[4 + j] = __builtin_amdgcn_cvt_pk_fp8_f32(b2, b3, wb, true);
+      pk[j] = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, pk[j], false);
+      pk[j] = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, pk[j], true);
+      pk[4 + j] = __builtin_amdgcn_cvt_pk_fp8_f32(b0, b1, pk[4 + j], false);
+      pk[4 + j] = __builtin_amdgcn_cvt_pk_fp8_f32(b2, b3, pk[4 + j], true);
     }
     l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
     const v8i pf = v8i{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
@@ -267,7 +319,7 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
     }
   };
 
-  // Prologue: stage tiles 0 and 1; scores of tile 0 if this wave starts there.
+  // Prologue: stage tiles 0 and 1.
   if (nt > 0) { load_tile(lo); store_tile(0); }
   if (nt > 1) { load_tile(lo + kBN); store_tile(1); }
   // Retire every global load so far (Q fragments included) on all paths: the wait-count pass
@@ -276,25 +328,25 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(SwaParams p) {
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
-  Scores sa, sb;
-  if (ta == 0 && ta <= tb) qk(sa, 0);
-
-  // One tile: prefetch tile j+2 (global -> registers), issue the QK^T MFMAs of tile j+1, then the
-  // softmax + PV of tile j, then park tile j+2 in the free LDS stage.
-  auto step = [&](int j, int buf, Scores& cur, Scores& nxt) {
+  // One tile: prefetch tile j+2 (global -> registers), QK^T + softmax + PV of tile j from LDS
+  // stage BUF (a compile-time constant, so LDS offsets are immediates), then park tile j+2 in
+  // the stage tile j-1 used.
+  Scores sc;
+  auto step = [&](int j, auto bufc) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(bufc)::value;
     const bool pre = j + 2 < nt;
     if (pre) load_tile(lo + (j + 2) * kBN);
-    const int nbuf = buf == kStages - 1 ? 0 : buf + 1;
-    if (j + 1 >= ta && j + 1 <= tb) qk(nxt, nbuf);
-    if (j >= ta && j <= tb) softmax_pv(cur, lo + j * kBN, buf);
-    if (pre) store_tile(nbuf == kStages - 1 ? 0 : nbuf + 1);
+    if (j >= ta && j <= tb) {
+      qk(sc, BUF);
+      softmax_pv(sc, lo + j * kBN, BUF);
+    }
+    if (pre) store_tile((BUF + 2) % kStages);
     __syncthreads();
-    return nbuf;
   };
-  int buf = 0;
-  for (int j = 0; j < nt; j += 2) {
-    buf = step(j, buf, sa, sb);
-    if (j + 1 < nt) buf = step(j + 1, buf, sb, sa);
+  for (int j = 0; j < nt; j += kStages) {
+    step(j, std::integral_constant<int, 0>{});
+    if (j + 1 < nt) step(j + 1, std::integral_constant<int, 1>{});
+    if (j + 2 < nt) step(j + 2, std::integral_constant<int, 2>{});
   }
 
   // Epilogue: out = O * v_scale / l   (l carries the x448 of P, matching pv_scale = v_s / 448)
