@@ -90,7 +90,7 @@ class AttentionStep:
         self.vt = torch.empty(self.lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device=dev)
         self.sc = torch.empty(3 * G, dtype=torch.float32, device=dev)
         self.G = G
-        self.ws = _lib.workspace(self.lib.flw_quant_workspace_bytes(B, H, T, D), dev)
+        self.ws = _lib.workspace(3 * self.lib.flw_quant_workspace_bytes(B, H, T, D), dev)
         self.out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
         self.dt = _lib.dtype_code(q.dtype)
         self.s8 = _lib.i64s(H * T * D, T * D, D)
@@ -98,14 +98,12 @@ class AttentionStep:
 
     def quant(self, stream):
         B, H, T, D = self.shape
-        L, lib = self.L, self.lib
-        for x, dst, layout, i in ((self.q, self.q8, L.LAYOUT_BHTD, 0), (self.k, self.k8, L.LAYOUT_BHTD, 1),
-                                  (self.v, self.vt, L.LAYOUT_VTILE, 2)):
-            sb, sh, st, _ = x.stride()
-            rc = lib.flw_quant_e4m3(x.data_ptr(), self.dt, B, H, T, D, sb, sh, st, self.gran, layout,
-                                    dst.data_ptr(), self.sc.data_ptr() + 4 * i * self.G, self.ws.data_ptr(),
-                                    self.ws.numel(), stream)
-            L.check(rc, "quant")
+        strides = self.L.i64s(*self.q.stride()[:3], *self.k.stride()[:3], *self.v.stride()[:3])
+        rc = self.lib.flw_quant_qkv_e4m3(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
+                                         B, H, T, D, strides, self.gran, self.q8.data_ptr(),
+                                         self.k8.data_ptr(), self.vt.data_ptr(), self.sc.data_ptr(),
+                                         self.ws.data_ptr(), self.ws.numel(), stream)
+        self.L.check(rc, "quant")
 
     def attend(self, stream):
         B, H, T, D = self.shape

@@ -32,6 +32,9 @@ SIGNATURES = {
     "flw_vtile_bytes": (c_size_t, [c_int64] * 4),
     "flw_quant_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                                c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "flw_quant_qkv_e4m3": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
+                                   c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   c_void_p, c_size_t, c_void_p]),
     "flw_fake_quant_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64,
                                     c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_size_t,
                                     c_void_p]),
@@ -50,6 +53,7 @@ SIGNATURES = {
     "flw_fp8_scaled_mm": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "flw_diag_cvt_e4m3": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p]),
+    "flw_diag_quotient": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p]),
 }
 
 _lib = None

@@ -1,28 +1,47 @@
 // e4m3 quantisers (HBM-bound): amax partials -> quantise, and the per-row quantiser.
 //
-// A (B, H, T, D) tensor is handled as B*H slices of T rows x D contiguous elements. Pass 1
-// (amax_partial_kernel) reduces |x| over chunks of kRowsPerChunk rows of one slice into a
-// partials array; pass 2 (quant_kernel) lets every workgroup fold the partials of its scale group
-// (whole tensor / head / slice) itself -- no atomics, no zero-initialised buffer, no host sync --
-// then quantises its chunk. Chunks are processed one tensor at a time, so on MI355X the second
-// read of a 64 MiB Q/K/V tensor is served largely from the 256 MB Infinity Cache.
+// A (B, H, T, D) tensor is handled as B*H slices of T rows x D contiguous elements, cut into
+// chunks of kRowsPerChunk rows. Pass 1 (amax_kernel) reduces |x| over each chunk into a partials
+// array; pass 2 (quant_kernel) lets every workgroup fold the partials of its scale group (whole
+// tensor / head / slice) itself -- no atomics, no zero-initialised buffer, no host sync -- then
+// quantises its chunk. Up to three tensors of one shape (Q, K, V) go through each pass in ONE
+// launch (grid.z = tensor), and every thread keeps kUnroll 16-byte loads in flight. The second
+// read of each tensor is largely served by the MI355X Infinity Cache (256 MB).
+//
+// Rounding. The reference computes e4m3(clamp(x / s, -448, 448)) with an IEEE fp32 division
+// and round-to-nearest-even. For a scale group whose amax is finite, every |x / s| is at most
+// 448 (s = max(amax, eps) / 448), so the clamp is inert and the quotient goes through
+//   q0 = x * r,  e = fma(-q0, s, x),  q = fma(e, r, q0)       with r = RN(1 / s)
+// (the reciprocal-then-correct sequence of Markstein, correctly rounded when r is the correctly
+// rounded reciprocal) and the hardware RNE converter v_cvt_pk_fp8_f32, two values per
+// instruction. Both are checked bit for bit on the device against the exact division and the
+// exact software rounding (flw_diag_* entry points and their tests). A group whose amax is NaN or
+// infinite takes the exact path (IEEE division, clamp, software rounding) so that NaN and inf
+// propagate exactly as in the reference.
 #include "flw_common.h"
 
 namespace flw {
 
 constexpr int kThreads = 256;
 constexpr int64_t kRowsPerChunk = 256;   // multiple of 64: VTILE chunks hold whole key tiles
+constexpr int kUnroll = 8;               // 16-byte loads in flight per thread
 
-struct SliceParams {
+struct QTensor {
   const void* x;
-  int64_t d0, d1, d2, d3;      // B, H, T, D
   int64_t s0, s1, s2;          // element strides of b, h, t
-  int64_t nchunks;             // chunks per slice
-  uint32_t* partials;          // [d0*d1*nchunks] |x| max bit patterns
-  int granularity;
   uint8_t* out8;               // codes (BHTD or VTILE)
   void* outx;                  // fake-quant output (input dtype, contiguous BHTD)
   float* scale_out;            // 1 | d1 | d0*d1
+  int layout;
+  int rows_packed;             // s2 == D: a chunk is one contiguous run of memory
+};
+
+struct QuantParams {
+  QTensor t[3];
+  int64_t d0, d1, d2, d3;      // B, H, T, D
+  int64_t nchunks;             // chunks per slice
+  uint32_t* partials;          // [tensor][d0*d1][nchunks] |x| max bit patterns
+  int granularity;
 };
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t m, uint32_t* lds4) {
@@ -36,60 +55,80 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t m, uint32_t* lds4) {
   return r;
 }
 
+// Element offset of the 16-byte vector v of chunk rows [r0, ...) inside a slice.
+__device__ __forceinline__ int64_t vec_offset(const QTensor& t, int64_t r0, int64_t v, int64_t vpr,
+                                              int n, int64_t d3) {
+  if (t.rows_packed) return r0 * d3 + v * n;
+  const int64_t row = r0 + v / vpr, cv = v % vpr;
+  return row * t.s2 + cv * n;
+}
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void amax_partial_kernel(SliceParams p) {
+__global__ __launch_bounds__(kThreads) void amax_kernel(QuantParams p) {
   using V = Vec16<T>;
   __shared__ uint32_t red[kThreads / 64];
+  const QTensor& t = p.t[blockIdx.z];
   const int64_t slice = blockIdx.y;
   const int64_t i0 = slice / p.d1, i1 = slice % p.d1;
   const int64_t r0 = (int64_t)blockIdx.x * kRowsPerChunk;
   const int64_t r1 = min(p.d2, r0 + kRowsPerChunk);
-  const T* base = static_cast<const T*>(p.x) + i0 * p.s0 + i1 * p.s1;
+  const T* base = static_cast<const T*>(t.x) + i0 * t.s0 + i1 * t.s1;
   const int64_t vpr = p.d3 / V::N;
   const int64_t nvec = (r1 - r0) * vpr;
   uint32_t m = 0;
-  for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
-    const int64_t row = r0 + v / vpr, cv = v % vpr;
-    float f[V::N];
-    V::load(base + row * p.s2 + cv * V::N, f);
+  for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kThreads * kUnroll) {
+    float f[kUnroll][V::N];
 #pragma unroll
-    for (int i = 0; i < V::N; ++i) { uint32_t a = abs_bits(f[i]); m = m > a ? m : a; }
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t v = v0 + (int64_t)u * kThreads;
+      if (v < nvec) {
+        V::load(base + vec_offset(t, r0, v, vpr, V::N, p.d3), f[u]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V::N; ++i) f[u][i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int i = 0; i < V::N; ++i) { const uint32_t a = abs_bits(f[u][i]); m = m > a ? m : a; }
   }
   m = block_max_u32(m, red);
-  if (threadIdx.x == 0) p.partials[slice * p.nchunks + blockIdx.x] = m;
+  if (threadIdx.x == 0)
+    p.partials[((int64_t)blockIdx.z * p.d0 * p.d1 + slice) * p.nchunks + blockIdx.x] = m;
 }
 
 // Fold the partials of this workgroup's scale group.
-__device__ __forceinline__ uint32_t group_amax(const SliceParams& p, int64_t slice, int64_t i1,
-                                               uint32_t* red) {
+__device__ __forceinline__ uint32_t group_amax(const QuantParams& p, const uint32_t* part,
+                                               int64_t slice, int64_t i1, uint32_t* red) {
   uint32_t m = 0;
   if (p.granularity == FLW_SCALE_TENSOR) {
     const int64_t n = p.d0 * p.d1 * p.nchunks;
-    for (int64_t i = threadIdx.x; i < n; i += kThreads) { uint32_t a = p.partials[i]; m = m > a ? m : a; }
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) { uint32_t a = part[i]; m = m > a ? m : a; }
   } else if (p.granularity == FLW_SCALE_HEAD) {
     const int64_t n = p.d0 * p.nchunks;
     for (int64_t i = threadIdx.x; i < n; i += kThreads) {
       const int64_t b = i / p.nchunks, c = i % p.nchunks;
-      uint32_t a = p.partials[(b * p.d1 + i1) * p.nchunks + c];
+      uint32_t a = part[(b * p.d1 + i1) * p.nchunks + c];
       m = m > a ? m : a;
     }
   } else {
     for (int64_t i = threadIdx.x; i < p.nchunks; i += kThreads) {
-      uint32_t a = p.partials[slice * p.nchunks + i];
+      uint32_t a = part[slice * p.nchunks + i];
       m = m > a ? m : a;
     }
   }
   return block_max_u32(m, red);
 }
 
-__device__ __forceinline__ int64_t group_index(const SliceParams& p, int64_t slice, int64_t i1) {
-  return p.granularity == FLW_SCALE_TENSOR ? 0 : (p.granularity == FLW_SCALE_HEAD ? i1 : slice);
+__device__ __forceinline__ int64_t group_index(int gran, int64_t slice, int64_t i1) {
+  return gran == FLW_SCALE_TENSOR ? 0 : (gran == FLW_SCALE_HEAD ? i1 : slice);
 }
 
-__device__ __forceinline__ bool writes_scale(const SliceParams& p, int64_t slice, int64_t i0) {
+__device__ __forceinline__ bool writes_scale(int gran, int64_t slice, int64_t i0) {
   if (blockIdx.x != 0 || threadIdx.x != 0) return false;
-  if (p.granularity == FLW_SCALE_TENSOR) return slice == 0;
-  if (p.granularity == FLW_SCALE_HEAD) return i0 == 0;
+  if (gran == FLW_SCALE_TENSOR) return slice == 0;
+  if (gran == FLW_SCALE_HEAD) return i0 == 0;
   return true;
 }
 
@@ -97,6 +136,15 @@ __device__ __forceinline__ float clamp448(float y) {
   // torch.clamp semantics: NaN stays NaN (both comparisons are false)
   y = y > kE4m3Max ? kE4m3Max : y;
   return y < -kE4m3Max ? -kE4m3Max : y;
+}
+
+// x / s from r = RN(1 / s): one product and two FMAs, the correctly rounded quotient whenever
+// |x / s| >= 2^-20 (below that the correction can underflow, but every such quotient is an e4m3
+// zero); the sign is copied from x so that -0 and tiny negatives keep the reference's sign.
+__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
+  const float q0 = x * r;
+  const float e = fmaf(-q0, s, x);
+  return __builtin_copysignf(fmaf(e, r, q0), x);
 }
 
 // Byte offset of element (key kk, dim d) inside a 64 x D VTILE tile.
@@ -107,17 +155,43 @@ __device__ __forceinline__ uint32_t vtile_offset(uint32_t kk, uint32_t d) {
   return (d >> 5) * 2048u + (kk >> 5) * 1024u + ((d & 31u) + 32u * h) * 16u + b;
 }
 
+// e4m3 codes of N values, packed little-endian (N = 4 or 8), on the fast or the exact path.
+template <int N>
+__device__ __forceinline__ void codes_of(const float* f, float s, float r, bool fast, uint32_t* w) {
+  if (fast) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      int c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * i], s, r),
+                                              div_by_scale(f[4 * i + 1], s, r), 0, false);
+      c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * i + 2], s, r),
+                                          div_by_scale(f[4 * i + 3], s, r), c, true);
+      w[i] = (uint32_t)c;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        c |= (f32_to_e4m3(clamp448(f[4 * i + j] / s)) & 0xFFu) << (8 * j);   // IEEE division
+      w[i] = c;
+    }
+  }
+}
+
 // MODE 0: e4m3 codes with the _per_tensor_fp8 recipe. MODE 1: _fake_quant_e4m3 forward value.
-template <typename T, int LAYOUT, int MODE>
-__global__ __launch_bounds__(kThreads) void quant_kernel(SliceParams p) {
+template <typename T, int MODE>
+__global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
   using V = Vec16<T>;
   constexpr bool kBf16 = sizeof(T) == 2;
   __shared__ uint32_t red[kThreads / 64];
   extern __shared__ __align__(16) uint8_t tile_lds[];   // VTILE staging: kRowsPerChunk x D
+  const QTensor& t = p.t[blockIdx.z];
   const int64_t slice = blockIdx.y;
   const int64_t i0 = slice / p.d1, i1 = slice % p.d1;
+  const uint32_t* part = p.partials + (int64_t)blockIdx.z * p.d0 * p.d1 * p.nchunks;
 
-  const float amax = __uint_as_float(group_amax(p, slice, i1, red));
+  const float amax = __uint_as_float(group_amax(p, part, slice, i1, red));
   float scale;
   if (MODE == 1 && kBf16) {
     // base.py:198-199 under bf16: clamp and /448 are bf16 tensor ops
@@ -126,87 +200,90 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(SliceParams p) {
   } else {
     scale = (amax < kEps ? kEps : amax) / kE4m3Max;     // IEEE fp32 division
   }
-  if (writes_scale(p, slice, i0)) p.scale_out[group_index(p, slice, i1)] = scale;
+  if (writes_scale(p.granularity, slice, i0)) t.scale_out[group_index(p.granularity, slice, i1)] = scale;
+  const bool fast = MODE == 0 && __builtin_isfinite(amax);   // uniform over the workgroup
+  const float rcp = 1.0f / scale;                            // IEEE: correctly rounded
 
   const int64_t r0 = (int64_t)blockIdx.x * kRowsPerChunk;
   const int64_t r1 = min(p.d2, r0 + kRowsPerChunk);
+  const bool vtile = MODE == 0 && t.layout == FLW_LAYOUT_VTILE;
   // VTILE: cover whole 64-row tiles, padding rows past T become code 0.
-  const int64_t r1p = LAYOUT == FLW_LAYOUT_VTILE ? min(r0 + kRowsPerChunk, (p.d2 + 63) & ~int64_t(63)) : r1;
-  const T* base = static_cast<const T*>(p.x) + i0 * p.s0 + i1 * p.s1;
+  const int64_t r1p = vtile ? min(r0 + kRowsPerChunk, (p.d2 + 63) & ~int64_t(63)) : r1;
+  const T* base = static_cast<const T*>(t.x) + i0 * t.s0 + i1 * t.s1;
   const int64_t vpr = p.d3 / V::N;
-  const int64_t nvec = (r1p - r0) * vpr;
+  const int64_t nvec = (r1 - r0) * vpr;        // vectors of real rows
+  const int64_t nvec_p = (r1p - r0) * vpr;     // including VTILE padding rows
 
-  for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
-    const int64_t row = r0 + v / vpr, cv = v % vpr;
-    float f[V::N];
-    if (row < p.d2) {
-      V::load(base + row * p.s2 + cv * V::N, f);
-    } else {
+  for (int64_t v0 = threadIdx.x; v0 < nvec_p; v0 += (int64_t)kThreads * kUnroll) {
+    float f[kUnroll][V::N];
 #pragma unroll
-      for (int i = 0; i < V::N; ++i) f[i] = 0.0f;
-    }
-    uint32_t codes[V::N];
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t v = v0 + (int64_t)u * kThreads;
+      if (v < nvec) {
+        V::load(base + vec_offset(t, r0, v, vpr, V::N, p.d3), f[u]);
+      } else {
 #pragma unroll
-    for (int i = 0; i < V::N; ++i) {
-      float y = f[i] / scale;                      // IEEE division, as the reference's CPU path
-      if (MODE == 1 && kBf16) y = round_bf16(y);
-      codes[i] = f32_to_e4m3(clamp448(y)) & 0xFFu;
-      if (row >= p.d2) codes[i] = 0;
+        for (int i = 0; i < V::N; ++i) f[u][i] = 0.0f;
+      }
     }
-    if (MODE == 0) {
-      if (LAYOUT == FLW_LAYOUT_BHTD) {
-        uint8_t* dst = p.out8 + (slice * p.d2 + row) * p.d3 + cv * V::N;
-        if (V::N == 8) {
-          uint2 w;
-          w.x = codes[0] | (codes[1] << 8) | (codes[2] << 16) | (codes[3] << 24);
-          w.y = codes[4] | (codes[5] << 8) | (codes[6] << 16) | (codes[7] << 24);
-          *reinterpret_cast<uint2*>(dst) = w;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t v = v0 + (int64_t)u * kThreads;
+      if (v >= nvec_p) continue;
+      if (MODE == 0) {
+        uint32_t w[V::N / 4];
+        codes_of<V::N>(f[u], scale, rcp, fast, w);
+        if (!vtile) {
+          uint8_t* dst = t.out8 + (slice * p.d2 + r0) * p.d3 + v * V::N;
+          if (V::N == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+          else *reinterpret_cast<uint32_t*>(dst) = w[0];
         } else {
-          *reinterpret_cast<uint32_t*>(dst) =
-              codes[0] | (codes[1] << 8) | (codes[2] << 16) | (codes[3] << 24);
+          const uint32_t lrow = (uint32_t)(v / vpr), d = (uint32_t)((v % vpr) * V::N);
+          uint8_t* tl = tile_lds + (lrow >> 6) * (64u * (uint32_t)p.d3);
+          const bool pad = v >= nvec;
+#pragma unroll
+          for (int i = 0; i < V::N; ++i)
+            tl[vtile_offset(lrow & 63u, d + i)] = pad ? 0 : (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
         }
       } else {
-        const uint32_t lrow = (uint32_t)(row - r0);
-        uint8_t* t = tile_lds + (lrow >> 6) * (64u * (uint32_t)p.d3);
+        // out = x + (dq - x), each step rounded to T (base.py:200-203)
+        float o[V::N];
 #pragma unroll
-        for (int i = 0; i < V::N; ++i)
-          t[vtile_offset(lrow & 63u, (uint32_t)(cv * V::N + i))] = (uint8_t)codes[i];
-      }
-    } else {
-      // out = x + (dq - x), each step rounded to T (base.py:200-203)
-      float o[V::N];
-#pragma unroll
-      for (int i = 0; i < V::N; ++i) {
-        float dq = e4m3_to_f32(codes[i] | 0u) * scale;
-        if (kBf16) dq = round_bf16(dq);
-        float d = dq - f[i];
-        if (kBf16) d = round_bf16(d);
-        o[i] = f[i] + d;
-      }
-      T* dst = static_cast<T*>(p.outx) + (slice * p.d2 + row) * p.d3 + cv * V::N;
-      if (kBf16) {
-        uint4 w;
-        w.x = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
-        w.y = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
-        w.z = f32_to_bf16_bits(o[4]) | (f32_to_bf16_bits(o[5]) << 16);
-        w.w = f32_to_bf16_bits(o[6]) | (f32_to_bf16_bits(o[7]) << 16);
-        *reinterpret_cast<uint4*>(dst) = w;
-      } else {
-        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        for (int i = 0; i < V::N; ++i) {
+          float y = f[u][i] / scale;                 // IEEE division, as the reference's CPU path
+          if (kBf16) y = round_bf16(y);
+          float dq = e4m3_to_f32(f32_to_e4m3(clamp448(y)) & 0xFFu) * scale;
+          if (kBf16) dq = round_bf16(dq);
+          float d = dq - f[u][i];
+          if (kBf16) d = round_bf16(d);
+          o[i] = f[u][i] + d;
+        }
+        T* dst = static_cast<T*>(t.outx) + (slice * p.d2 + r0) * p.d3 + v * V::N;
+        if (kBf16) {
+          uint4 w;
+          w.x = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
+          w.y = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
+          w.z = f32_to_bf16_bits(o[4]) | (f32_to_bf16_bits(o[5]) << 16);
+          w.w = f32_to_bf16_bits(o[6]) | (f32_to_bf16_bits(o[7]) << 16);
+          *reinterpret_cast<uint4*>(dst) = w;
+        } else {
+          *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        }
       }
     }
   }
-  if (LAYOUT == FLW_LAYOUT_VTILE && MODE == 0) {
+  if (vtile) {
     __syncthreads();
     const int64_t ntiles = (p.d2 + 63) >> 6;
     const int64_t nbytes = (r1p - r0) * p.d3;
-    uint8_t* dst = p.out8 + (slice * ntiles + (r0 >> 6)) * 64 * p.d3;
+    uint8_t* dst = t.out8 + (slice * ntiles + (r0 >> 6)) * 64 * p.d3;
     for (int64_t o = threadIdx.x * 16; o < nbytes; o += kThreads * 16)
       *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(tile_lds + o);
   }
 }
 
-// One wave per row: amax, scale = max(amax / 448, 1e-12), codes = e4m3(x / scale).
+// One wave per row: amax, scale = max(amax / 448, 1e-12), codes = e4m3(x / scale) (no clamp:
+// |x / scale| <= 448 whenever amax is finite).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rows_quant_kernel(const T* __restrict__ x, int64_t rows,
                                                               int64_t cols, int64_t rs,
@@ -226,24 +303,30 @@ __global__ __launch_bounds__(kThreads) void rows_quant_kernel(const T* __restric
     for (int i = 0; i < V::N; ++i) { uint32_t a = abs_bits(f[i]); m = m > a ? m : a; }
   }
   m = wave_max_u32(m);
-  float s = __uint_as_float(m) / kE4m3Max;
+  const float amax = __uint_as_float(m);
+  float s = amax / kE4m3Max;
   s = s < kEps ? kEps : s;
   if (lane == 0) scale_out[row] = s;
+  const bool fast = __builtin_isfinite(amax);
+  const float rcp = 1.0f / s;
   uint8_t* dst = out + row * cols;
   for (int64_t v = lane; v < nvec; v += 64) {
     float f[V::N];
     V::load(src + v * V::N, f);
-    uint32_t c[V::N];
-#pragma unroll
-    for (int i = 0; i < V::N; ++i) c[i] = f32_to_e4m3(f[i] / s) & 0xFFu;
-    if (V::N == 8) {
-      uint2 w;
-      w.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-      w.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-      *reinterpret_cast<uint2*>(dst + v * 8) = w;
+    uint32_t w[V::N / 4];
+    if (fast) {
+      codes_of<V::N>(f, s, rcp, true, w);
     } else {
-      *reinterpret_cast<uint32_t*>(dst + v * 4) = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+#pragma unroll
+      for (int i = 0; i < V::N / 4; ++i) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c |= (f32_to_e4m3(f[4 * i + j] / s) & 0xFFu) << (8 * j);
+        w[i] = c;
+      }
     }
+    if (V::N == 8) *reinterpret_cast<uint2*>(dst + v * 8) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t*>(dst + v * 4) = w[0];
   }
 }
 
@@ -270,42 +353,76 @@ static size_t partial_bytes(int64_t B, int64_t H, int64_t T) {
   return (size_t)(B * H * nchunks_of(T)) * sizeof(uint32_t);
 }
 
-template <int LAYOUT, int MODE>
-static int launch_slice(const SliceParams& p, int dtype, hipStream_t s, const char* name) {
-  dim3 grid((unsigned)p.nchunks, (unsigned)(p.d0 * p.d1));
-  size_t lds = LAYOUT == FLW_LAYOUT_VTILE ? (size_t)(kRowsPerChunk * p.d3) : 0;
+template <int MODE>
+static int launch_quant(const QuantParams& p, int ntensors, int dtype, hipStream_t s, const char* name) {
+  dim3 grid((unsigned)p.nchunks, (unsigned)(p.d0 * p.d1), (unsigned)ntensors);
+  bool any_vtile = false;
+  for (int i = 0; i < ntensors; ++i) any_vtile |= p.t[i].layout == FLW_LAYOUT_VTILE;
+  const size_t lds = MODE == 0 && any_vtile ? (size_t)(kRowsPerChunk * p.d3) : 0;
   if (dtype == FLW_F32) {
-    hipLaunchKernelGGL(amax_partial_kernel<float>, grid, dim3(kThreads), 0, s, p);
-    hipLaunchKernelGGL((quant_kernel<float, LAYOUT, MODE>), grid, dim3(kThreads), lds, s, p);
+    hipLaunchKernelGGL(amax_kernel<float>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((quant_kernel<float, MODE>), grid, dim3(kThreads), lds, s, p);
   } else {
-    hipLaunchKernelGGL(amax_partial_kernel<uint16_t>, grid, dim3(kThreads), 0, s, p);
-    hipLaunchKernelGGL((quant_kernel<uint16_t, LAYOUT, MODE>), grid, dim3(kThreads), lds, s, p);
+    hipLaunchKernelGGL(amax_kernel<uint16_t>, grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((quant_kernel<uint16_t, MODE>), grid, dim3(kThreads), lds, s, p);
   }
   return check_launch(name);
+}
+
+static void set_tensor(QTensor& t, const void* x, int64_t sb, int64_t sh, int64_t st, int64_t D,
+                       int layout, uint8_t* out8, void* outx, float* scale_out) {
+  t.x = x; t.s0 = sb; t.s1 = sh; t.s2 = st; t.layout = layout; t.out8 = out8; t.outx = outx;
+  t.scale_out = scale_out; t.rows_packed = st == D ? 1 : 0;
+}
+
+// Quantise n (1..3) tensors of one shape, dtype and granularity in two launches.
+int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
+                 int64_t D, const int64_t* strides, int granularity, const int* layouts,
+                 uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
+                 hipStream_t stream) {
+  FLW_REQUIRE(n >= 1 && n <= 3, FLW_E_INVALID, "1 to 3 tensors per call");
+  FLW_REQUIRE(granularity >= FLW_SCALE_TENSOR && granularity <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", granularity);
+  FLW_REQUIRE(ws != nullptr && ws_bytes >= (size_t)n * partial_bytes(B, H, T), FLW_E_WORKSPACE,
+              "workspace needs %zu bytes", (size_t)n * partial_bytes(B, H, T));
+  QuantParams p{};
+  for (int i = 0; i < n; ++i) {
+    int rc = check_tensor(xs[i], dtype, B, H, T, D, strides[3 * i], strides[3 * i + 1], strides[3 * i + 2]);
+    if (rc) return rc;
+    FLW_REQUIRE(layouts[i] == FLW_LAYOUT_BHTD || layouts[i] == FLW_LAYOUT_VTILE, FLW_E_INVALID, "bad layout %d", layouts[i]);
+    FLW_REQUIRE(outs[i] != nullptr && scale_outs[i] != nullptr, FLW_E_INVALID, "null output pointer");
+    if (layouts[i] == FLW_LAYOUT_VTILE) {
+      FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "VTILE layout needs D in {32, 64, 128}");
+      FLW_REQUIRE(((uintptr_t)outs[i] & 15) == 0, FLW_E_INVALID, "VTILE output must be 16-byte aligned");
+    } else {
+      FLW_REQUIRE(((uintptr_t)outs[i] & 7) == 0, FLW_E_INVALID, "output must be 8-byte aligned");
+    }
+    set_tensor(p.t[i], xs[i], strides[3 * i], strides[3 * i + 1], strides[3 * i + 2], D, layouts[i], outs[i],
+               nullptr, scale_outs[i]);
+  }
+  p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D;
+  p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(ws); p.granularity = granularity;
+  return launch_quant<0>(p, n, dtype, stream, "flw_quant_e4m3");
 }
 
 int quant_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
                int64_t sh, int64_t st, int granularity, int layout, uint8_t* out, float* scale_out,
                void* ws, size_t ws_bytes, hipStream_t stream) {
-  int rc = check_tensor(x, dtype, B, H, T, D, sb, sh, st);
-  if (rc) return rc;
-  FLW_REQUIRE(granularity >= FLW_SCALE_TENSOR && granularity <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", granularity);
-  FLW_REQUIRE(layout == FLW_LAYOUT_BHTD || layout == FLW_LAYOUT_VTILE, FLW_E_INVALID, "bad layout %d", layout);
-  FLW_REQUIRE(out != nullptr && scale_out != nullptr, FLW_E_INVALID, "null output pointer");
-  FLW_REQUIRE(ws != nullptr && ws_bytes >= partial_bytes(B, H, T), FLW_E_WORKSPACE,
-              "workspace needs %zu bytes", partial_bytes(B, H, T));
-  if (layout == FLW_LAYOUT_VTILE) {
-    FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "VTILE layout needs D in {32, 64, 128}");
-    FLW_REQUIRE(((uintptr_t)out & 15) == 0, FLW_E_INVALID, "VTILE output must be 16-byte aligned");
-  } else {
-    FLW_REQUIRE(((uintptr_t)out & 7) == 0, FLW_E_INVALID, "output must be 8-byte aligned");
-  }
-  SliceParams p{};
-  p.x = x; p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D; p.s0 = sb; p.s1 = sh; p.s2 = st;
-  p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(ws); p.granularity = granularity;
-  p.out8 = out; p.scale_out = scale_out;
-  if (layout == FLW_LAYOUT_BHTD) return launch_slice<FLW_LAYOUT_BHTD, 0>(p, dtype, stream, "flw_quant_e4m3");
-  return launch_slice<FLW_LAYOUT_VTILE, 0>(p, dtype, stream, "flw_quant_e4m3(vtile)");
+  const int64_t strides[3] = {sb, sh, st};
+  return quant_bhtd_n(1, &x, dtype, B, H, T, D, strides, granularity, &layout, &out, &scale_out, ws,
+                      ws_bytes, stream);
+}
+
+// ---------------------------------------------------------------- diagnostics
+
+// mode 0: IEEE x / s;  mode 1: the quantiser's reciprocal-and-correct quotient.
+__global__ __launch_bounds__(256) void quotient_kernel(const float* __restrict__ x, int64_t n,
+                                                       const float* __restrict__ s, int64_t ns,
+                                                       uint32_t* __restrict__ out, int mode) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n * ns) return;
+  const float xv = x[i % n], sv = s[i / n];
+  const float q = mode == 0 ? xv / sv : div_by_scale(xv, sv, 1.0f / sv);
+  out[i] = __float_as_uint(q);
 }
 
 }  // namespace flw
@@ -329,6 +446,21 @@ extern "C" int flw_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, in
                     scale_out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int flw_quant_qkv_e4m3(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                                  int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                                  int granularity, uint8_t* q8, uint8_t* k8, uint8_t* v_tiles,
+                                  float* scales_out, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  FLW_REQUIRE(strides != nullptr && scales_out != nullptr, FLW_E_INVALID, "null strides / scales");
+  const int64_t G = granularity == FLW_SCALE_TENSOR ? 1 : (granularity == FLW_SCALE_HEAD ? H : B * H);
+  const void* xs[3] = {q, k, v};
+  const int layouts[3] = {FLW_LAYOUT_BHTD, FLW_LAYOUT_BHTD, FLW_LAYOUT_VTILE};
+  uint8_t* outs[3] = {q8, k8, v_tiles};
+  float* sc[3] = {scales_out, scales_out + G, scales_out + 2 * G};
+  return quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, sc, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T,
                                    int64_t D, int64_t stride_b, int64_t stride_h, int64_t stride_t,
                                    int granularity, void* out, float* scale_out, void* workspace,
@@ -339,17 +471,17 @@ extern "C" int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t 
   FLW_REQUIRE(out != nullptr && ((uintptr_t)out & 15) == 0, FLW_E_INVALID, "output must be non-null and 16-byte aligned");
   FLW_REQUIRE(workspace != nullptr && workspace_bytes >= partial_bytes(B, H, T), FLW_E_WORKSPACE,
               "workspace needs %zu bytes", partial_bytes(B, H, T));
-  SliceParams p{};
-  p.x = x; p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D; p.s0 = stride_b; p.s1 = stride_h; p.s2 = stride_t;
-  p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(workspace); p.granularity = granularity;
-  p.outx = out;
-  p.scale_out = scale_out;
-  if (scale_out == nullptr) {   // optional: park the scales in the tail of the workspace
+  QuantParams p{};
+  float* sc = scale_out;
+  if (sc == nullptr) {   // optional: park the scales in the tail of the workspace
     const size_t need = partial_bytes(B, H, T) + sizeof(float) * (size_t)(B * H);
     FLW_REQUIRE(workspace_bytes >= need, FLW_E_WORKSPACE, "workspace needs %zu bytes without scale_out", need);
-    p.scale_out = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + partial_bytes(B, H, T));
+    sc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + partial_bytes(B, H, T));
   }
-  return launch_slice<FLW_LAYOUT_BHTD, 1>(p, dtype, static_cast<hipStream_t>(stream), "flw_fake_quant_e4m3");
+  set_tensor(p.t[0], x, stride_b, stride_h, stride_t, D, FLW_LAYOUT_BHTD, nullptr, out, sc);
+  p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D;
+  p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(workspace); p.granularity = granularity;
+  return launch_quant<1>(p, 1, dtype, static_cast<hipStream_t>(stream), "flw_fake_quant_e4m3");
 }
 
 extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64_t cols,
@@ -371,4 +503,15 @@ extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64
     hipLaunchKernelGGL(rows_quant_kernel<uint16_t>, grid, dim3(kThreads), 0, s,
                        static_cast<const uint16_t*>(x), rows, cols, row_stride, out, scale_out);
   return check_launch("flw_quant_rows_e4m3");
+}
+
+extern "C" int flw_diag_quotient(const float* x, int64_t n, const float* scales, int64_t n_scales,
+                                 uint32_t* out, int mode, void* stream) {
+  FLW_REQUIRE(x && scales && out && n > 0 && n_scales > 0, FLW_E_INVALID, "bad arguments");
+  FLW_REQUIRE(mode == 0 || mode == 1, FLW_E_INVALID, "mode must be 0 (IEEE) or 1 (reciprocal + correction)");
+  const int64_t total = n * n_scales;
+  FLW_REQUIRE((total + 255) / 256 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many quotients");
+  hipLaunchKernelGGL(quotient_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, n, scales, n_scales, out, mode);
+  return check_launch("flw_diag_quotient");
 }

@@ -367,9 +367,10 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   }
 }
 
-int quant_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
-               int64_t sh, int64_t st, int granularity, int layout, uint8_t* out, float* scale_out,
-               void* ws, size_t ws_bytes, hipStream_t stream);
+int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
+                 int64_t D, const int64_t* strides, int granularity, const int* layouts,
+                 uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
+                 hipStream_t stream);
 
 template <int D>
 static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s) {
@@ -431,7 +432,7 @@ static SwaWorkspace swa_ws_layout(int64_t B, int64_t H, int64_t T, int64_t D) {
   w.vt = w.k8 + align256(n);
   w.scales = w.vt + align256(flw_vtile_bytes(B, H, T, D));
   w.partials = w.scales + align256(3 * sizeof(float) * (size_t)(B * H));
-  w.total = w.partials + align256(flw_quant_workspace_bytes(B, H, T, D));
+  w.total = w.partials + align256(3 * flw_quant_workspace_bytes(B, H, T, D));
   return w;
 }
 
@@ -471,16 +472,12 @@ extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const
   uint8_t* q8 = ws + w.q8;
   uint8_t* k8 = ws + w.k8;
   uint8_t* vt = ws + w.vt;
-  void* part = ws + w.partials;
-  const size_t pbytes = w.total - w.partials;
-  int rc = quant_bhtd(q, dtype, B, H, T, D, strides[0], strides[1], strides[2], granularity,
-                      FLW_LAYOUT_BHTD, q8, sc, part, pbytes, s);
-  if (rc) return rc;
-  rc = quant_bhtd(k, dtype, B, H, T, D, strides[3], strides[4], strides[5], granularity,
-                  FLW_LAYOUT_BHTD, k8, sc + G, part, pbytes, s);
-  if (rc) return rc;
-  rc = quant_bhtd(v, dtype, B, H, T, D, strides[6], strides[7], strides[8], granularity,
-                  FLW_LAYOUT_VTILE, vt, sc + 2 * G, part, pbytes, s);
+  const void* xs[3] = {q, k, v};
+  const int layouts[3] = {FLW_LAYOUT_BHTD, FLW_LAYOUT_BHTD, FLW_LAYOUT_VTILE};
+  uint8_t* outs[3] = {q8, k8, vt};
+  float* scs[3] = {sc, sc + G, sc + 2 * G};
+  int rc = quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, scs,
+                        ws + w.partials, w.total - w.partials, s);
   if (rc) return rc;
   const int64_t s8[3] = {H * T * D, T * D, D};
   return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, granularity, out, dtype, strides + 9,

@@ -69,6 +69,15 @@ int flw_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T, in
                    int layout, uint8_t* out, float* scale_out, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* flw_quant_e4m3 on three tensors of one shape in one pass pair (the three `_per_tensor_fp8`
+ * calls of flower/kernels/fp8_swa_attention.py:242-244): q and k to FLW_LAYOUT_BHTD codes (q8,
+ * k8), v to FLW_LAYOUT_VTILE (v_tiles). strides: 9 values, {b, h, t} of q, k, v. scales_out:
+ * 3 x (1 | H | B*H) floats in the order q, k, v. workspace: 3 * flw_quant_workspace_bytes. */
+int flw_quant_qkv_e4m3(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                       int64_t H, int64_t T, int64_t D, const int64_t* strides, int granularity,
+                       uint8_t* q8, uint8_t* k8, uint8_t* v_tiles, float* scales_out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Straight-through fake quantisation forward value, replacing `_fake_quant_e4m3`
  * (flower/models/base.py:167-203): out = x + (e4m3(x / s) * s - x), every step rounded to the
  * input dtype exactly as the reference's op sequence rounds (s itself in the input dtype).
@@ -142,6 +151,12 @@ int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8
  * or with the library's exact software rounding (hardware = 0), so a test can check the two
  * agree bit for bit on the values the kernel feeds it. */
 int flw_diag_cvt_e4m3(const float* x, uint8_t* out, int64_t n, int hardware, void* stream);
+
+/* No counterpart in the reference. The quotient x[i] / scale[j] for every pair (i, j), as raw
+ * fp32 bits in out[j * n + i]: mode 0 with the IEEE division, mode 1 with the quantisers'
+ * reciprocal-and-correct sequence, so a test can check the two agree bit for bit. */
+int flw_diag_quotient(const float* x, int64_t n, const float* scales, int64_t n_scales,
+                      uint32_t* out, int mode, void* stream);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,91 @@ def test_hw_fp8_convert_is_exact_on_the_attention_P_range():
     assert bad == 0, f"{bad} hardware conversions differ from exact RNE"
 
 
+def test_hw_fp8_convert_is_exact_on_negative_quantiser_range():
+    """The quantisers feed v_cvt_pk_fp8_f32 quotients in [-448 (1 + 2^-20), 448 (1 + 2^-20)]:
+    the negative half, EVERY fp32 value, against the exact rounding."""
+    L = lib()
+    lb = L.load()
+    hi = int(np.array([448.0], np.float32).view(np.int32)[0]) + 16
+    chunk = 1 << 26
+    bad = 0
+    for start in range(0, hi + 1, chunk):
+        n = min(chunk, hi + 1 - start)
+        n += n % 2
+        u = torch.arange(start, start + n, dtype=torch.int64, device="cuda") | (1 << 31)
+        x = u.to(torch.int32).view(torch.float32)          # sign bit set: -|x|
+        hw = torch.empty(n, dtype=torch.uint8, device="cuda")
+        sw = torch.empty(n, dtype=torch.uint8, device="cuda")
+        s = L.stream_of(x)
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), hw.data_ptr(), n, 1, s), "hw")
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), sw.data_ptr(), n, 0, s), "sw")
+        bad += int((hw != sw).sum())
+    assert bad == 0, f"{bad} hardware conversions differ from exact RNE"
+
+
+def _quotients(x, scales, mode):
+    L = lib()
+    lb = L.load()
+    xt = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    st = torch.from_numpy(np.ascontiguousarray(scales, np.float32)).cuda()
+    out = torch.empty(x.size * scales.size, dtype=torch.int32, device="cuda")
+    L.check(lb.flw_diag_quotient(xt.data_ptr(), x.size, st.data_ptr(), scales.size, out.data_ptr(),
+                                 mode, L.stream_of(xt)), "quotient")
+    return out
+
+
+def _scale_set(seed=0):
+    """Scales the quantisers form: max(amax, 1e-12) / 448 for random and adversarial amax
+    (all-ones and all-zeros mantissas, powers of two, tiny, huge), plus raw random mantissas."""
+    rng = np.random.default_rng(seed)
+    amax = np.concatenate([
+        rng.standard_normal(700).astype(np.float32) ** 2 * 10,
+        np.exp(rng.uniform(-30, 30, 300)).astype(np.float32),
+        np.array([1.0, 2.0, 448.0, 3.0, 1e-12, 1e-30, 3e38, 65504.0], np.float32),
+        (np.uint32(0x3FFFFFFF) - np.arange(32, dtype=np.uint32)).view(np.float32),   # 1.999..
+        (np.uint32(0x3F800000) + np.arange(32, dtype=np.uint32)).view(np.float32),   # 1.000..
+    ])
+    s = (np.maximum(amax, np.float32(1e-12)) / np.float32(448.0)).astype(np.float32)
+    raw = ((rng.integers(0, 1 << 23, 256, dtype=np.uint32)) | np.uint32(0x3F800000)).view(np.float32)
+    return np.concatenate([s, raw]).astype(np.float32)
+
+
+def test_reciprocal_correction_equals_ieee_division_on_every_bf16_input():
+    """The quantisers' x / s (RN(1/s), one product, two FMAs) is the IEEE quotient bit for bit,
+    for all 65,536 bf16 values x against ~1,300 scales, wherever |x / s| <= 2^9 (the quantiser
+    never sees larger quotients: |x| <= amax and s >= amax / 448)."""
+    bits = np.arange(1 << 16, dtype=np.uint32) << 16
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    scales = _scale_set()
+    for lo in range(0, scales.size, 256):
+        sc = scales[lo:lo + 256]
+        ref = _quotients(x, sc, 0)
+        got = _quotients(x, sc, 1)
+        _check_quotients(ref, got, f"scales {lo}..{lo + sc.size}")
+
+
+def _check_quotients(ref, got, what):
+    """Bit-identical where 2^-20 <= |q| <= 2^9; below 2^-20 (an e4m3 zero) the sign must agree."""
+    q = ref.view(torch.float32).abs()
+    inside = q <= 512.0
+    exact = inside & (q >= 2.0 ** -20)
+    bad = int(((ref != got) & exact).sum())
+    assert bad == 0, f"{bad} quotients differ ({what})"
+    sign_bad = int((((ref ^ got) < 0) & inside).sum())
+    assert sign_bad == 0, f"{sign_bad} quotient signs differ ({what})"
+
+
+def test_reciprocal_correction_equals_ieee_division_on_random_fp32():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(1 << 18) * np.exp(rng.uniform(-20, 20, 1 << 18))).astype(np.float32)
+    scales = _scale_set(2)[::5]
+    x[:64] = np.float32(-0.0)
+    ref = _quotients(x, scales, 0)
+    got = _quotients(x, scales, 1)
+    _check_quotients(ref, got, "random fp32")
+
+
 def test_device_exact_rounding_matches_oracle():
     """The device's software e4m3 rounding (used by the quantisers) vs the oracle, on random
     bit patterns, every e4m3 midpoint +-4 ulp, NaN and inf."""
@@ -91,6 +176,7 @@ def make(shape, dtype, kind, seed=0):
         x = torch.randn(*shape, generator=g) * torch.randn(1, shape[1], 1, 1, generator=g).exp()
     elif kind == "tiny":
         x = seeded(shape, seed, torch.float32, "cpu") * 1e-30
+        x.view(-1)[::7] = -0.0                                  # the sign of zero is kept
     else:
         raise ValueError(kind)
     return x.to(dtype).cuda()
@@ -148,6 +234,34 @@ def test_vtile_layout_is_the_documented_permutation(shape, dtype):
     want_codes, want_scale = per_tensor_fp8(to_np(x), "head")
     np.testing.assert_array_equal(out.cpu().numpy(), vtile_permute(want_codes))
     np.testing.assert_array_equal(to_np(sc), want_scale.reshape(-1))
+
+
+@pytest.mark.parametrize("granularity", ["tensor", "head", "bh"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_qkv_entry_point_bit_exact(granularity, dtype):
+    """flw_quant_qkv_e4m3: Q, K codes (BHTD), V codes (VTILE) and all scales in one call."""
+    L = lib()
+    lb = L.load()
+    B, H, T, D = 2, 3, 200, 64
+    xs = [make((B, H, T, D), dtype, kind, seed=s) for s, kind in ((7, "randn"), (8, "ties"), (9, "lognormal_heads"))]
+    G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+    q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device="cuda")
+    k8 = torch.empty_like(q8)
+    vt = torch.empty(lb.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(3 * G, dtype=torch.float32, device="cuda")
+    ws = L.workspace(3 * lb.flw_quant_workspace_bytes(B, H, T, D), "cuda")
+    strides = L.i64s(*xs[0].stride()[:3], *xs[1].stride()[:3], *xs[2].stride()[:3])
+    L.check(lb.flw_quant_qkv_e4m3(xs[0].data_ptr(), xs[1].data_ptr(), xs[2].data_ptr(), L.dtype_code(dtype),
+                                  B, H, T, D, strides, L.GRANULARITY[granularity], q8.data_ptr(),
+                                  k8.data_ptr(), vt.data_ptr(), sc.data_ptr(), ws.data_ptr(), ws.numel(),
+                                  L.stream_of(q8)), "qkv")
+    want = [per_tensor_fp8(to_np(x), granularity) for x in xs]
+    np.testing.assert_array_equal(q8.cpu().numpy(), want[0][0])
+    np.testing.assert_array_equal(k8.cpu().numpy(), want[1][0])
+    np.testing.assert_array_equal(vt.cpu().numpy(), vtile_permute(want[2][0]))
+    got_sc = to_np(sc).view(np.uint32)
+    for i in range(3):
+        np.testing.assert_array_equal(got_sc[i * G:(i + 1) * G], want[i][1].reshape(-1).view(np.uint32))
 
 
 # ------------------------------------------------------------------ _fake_quant_e4m3
