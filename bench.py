@@ -1,23 +1,29 @@
 """Benchmark of the FP8 sliding-window-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|gemm_c2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2]
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
 lognormal(0, 1) factor (seeded), per-head e4m3 scales. One step = the whole operator: amax +
-e4m3 quantisation of Q, K and V (V into the MFMA tile layout) and the fused FP8 attention
-kernel, on inputs already resident in HBM. Everything runs through the C ABI of
-libflower_amd.so on torch's current stream.
+e4m3 quantisation of Q, K and V (V into the MFMA tile layout, one launch pair for the three) and
+the fused FP8 attention kernel, on inputs already resident in HBM. Everything runs through the
+C ABI of libflower_amd.so on torch's current stream.
 
 Printed (one JSON line):
   value      -- in-window attention FLOP/s of the whole step, TFLOP/s (4*D per in-window pair)
-  roofline   -- the attention kernel alone (HIP events around its launches): achieved TFLOP/s
-                against MI355X dense FP8 MFMA peak (5.0 PFLOP/s)
-  quant      -- the three quantise launches: algorithmic bytes (two passes: 2 reads + 1 write
-                per element) / their event time, against 8 TB/s HBM
+  roofline   -- the attention kernel alone (HIP events around each of its launches, on the
+                stream it runs on): achieved TFLOP/s against MI355X dense FP8 MFMA peak
+                (5.0 PFLOP/s); traffic = its measured HBM bytes per launch (TRAFFIC below)
+  quant      -- the quantise launch pair: algorithmic bytes (2 reads + 1 write per element) /
+                their event time, against 8 TB/s HBM
   cpu_baseline -- the CPU oracle of the FP8-simulated reference path (e4m3 quantise, dequantise,
                 banded fp32 softmax attention) on a bounded sample of the same workload, host
                 cores, scaled linearly to the same unit.
+
+--workload c2 measures the FP8 weight-cache linear of BASELINE.json config 2 instead (bf16
+x[8192, 1024] with 0.1 % outliers at 20x, cached e4m3 weight [4096, 1024] with per-output-channel
+scales; one step = per-row activation quantisation + the scaled FP8 GEMM), in GEMM TFLOP/s.
+Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
 """
 
 from __future__ import annotations
@@ -43,6 +49,20 @@ WORKLOADS = {
     "c3": dict(B=4, H=16, T=8192, D=64, W=1024, granularity="head", inputs="lognormal_heads"),
     "c4": dict(B=1, H=16, T=32768, D=64, W=4096, granularity="head", inputs="student_t_channels"),
     "c1": dict(B=1, H=8, T=1024, D=64, W=256, granularity="tensor", inputs="randn_fp32"),
+    "c2": dict(M=8192, N=4096, K=1024, outlier_frac=0.001, outlier_scale=20.0, w_std=0.02),
+}
+DATA = {
+    "lognormal_heads": "synthetic (seeded; bf16 N(0,1) x a lognormal(0,1) factor per head)",
+    "student_t_channels": "synthetic (seeded; bf16 N(0,1), 4 of 64 channels Student-t nu=4)",
+    "randn_fp32": "synthetic (seeded; fp32 N(0,1))",
+    "c2": "synthetic (seeded; bf16 x N(0,1) with 0.1% outliers x20; weight N(0,0.02), random init)",
+}
+
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload
+# (profiles/swa_fwd_c3.md). FETCH_SIZE is scaled by 2.0: a plain 256 MiB device copy reads back
+# 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0).
+TRAFFIC = {
+    "c3": {"swa_fwd": 167_979_008, "quant": 503_929_856},
 }
 
 
@@ -67,13 +87,30 @@ def make_inputs(cfg, seed=0):
     return out
 
 
+def make_gemm_inputs(cfg, seed=0):
+    """bf16 activations with 0.1 % outliers at 20x, bf16 weight N(0, 0.02)."""
+    M, N, K = cfg["M"], cfg["N"], cfg["K"]
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    n_out = int(round(cfg["outlier_frac"] * M * K))
+    pos = torch.randperm(M * K, generator=g)[:n_out]
+    x.view(-1)[pos] *= cfg["outlier_scale"]
+    w = torch.randn(N, K, generator=g) * cfg["w_std"]
+    return x.to(torch.bfloat16), w.to(torch.bfloat16)
+
+
 def in_window_pairs(T, W):
     ramp = min(T, W)
     return ramp * (ramp + 1) // 2 + max(0, T - W) * W
 
 
+def _events(n):
+    return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+             torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+
+
 class AttentionStep:
-    """The operator as four C-ABI launches with HIP events around the attention kernel."""
+    """The operator as C-ABI launches: one quantise pair for Q/K/V, then the attention kernel."""
 
     def __init__(self, q, k, v, cfg):
         from flower_amd import _lib
@@ -95,12 +132,12 @@ class AttentionStep:
         self.dt = _lib.dtype_code(q.dtype)
         self.s8 = _lib.i64s(H * T * D, T * D, D)
         self.so = _lib.i64s(*self.out.stride()[:3])
+        self.sx = _lib.i64s(*q.stride()[:3], *k.stride()[:3], *v.stride()[:3])
 
     def quant(self, stream):
         B, H, T, D = self.shape
-        strides = self.L.i64s(*self.q.stride()[:3], *self.k.stride()[:3], *self.v.stride()[:3])
         rc = self.lib.flw_quant_qkv_e4m3(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
-                                         B, H, T, D, strides, self.gran, self.q8.data_ptr(),
+                                         B, H, T, D, self.sx, self.gran, self.q8.data_ptr(),
                                          self.k8.data_ptr(), self.vt.data_ptr(), self.sc.data_ptr(),
                                          self.ws.data_ptr(), self.ws.numel(), stream)
         self.L.check(rc, "quant")
@@ -121,8 +158,7 @@ def bench_attention(cfg, steps, warmup):
     for _ in range(warmup):
         step.quant(stream)
         step.attend(stream)
-    torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    ev = _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
@@ -136,30 +172,78 @@ def bench_attention(cfg, steps, warmup):
     quant_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
     attn_ms = np.array([e[1].elapsed_time(e[2]) for e in ev])
     B, H, T, D = q.shape
-    flops = 4 * D * B * H * in_window_pairs(T, cfg["W"])
-    n = B * H * T * D
-    qbytes = 3 * n * (2 * q.element_size() + 1)
     return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, quant_ms=float(np.mean(quant_ms)),
-                attn_ms=float(np.mean(attn_ms)), attn_ms_min=float(np.min(attn_ms)), flops=flops,
-                quant_bytes=qbytes, out=step.out, inputs=(q, k, v))
+                attn_ms=float(np.mean(attn_ms)), attn_ms_min=float(np.min(attn_ms)),
+                flops=4 * D * B * H * in_window_pairs(T, cfg["W"]),
+                quant_bytes=3 * B * H * T * D * (2 * q.element_size() + 1), dtype=q.dtype)
+
+
+def bench_gemm(cfg, steps, warmup):
+    """BASELINE config 2 through the C ABI: weight quantised once (the FP8 weight cache), then per
+    step per-row activation quantisation + the scaled FP8 GEMM, events around the GEMM."""
+    from flower_amd import _lib
+    lib = _lib.load()
+    x, w = (t.cuda() for t in make_gemm_inputs(cfg))
+    M, N, K = cfg["M"], cfg["N"], cfg["K"]
+    stream = torch.cuda.current_stream().cuda_stream
+    w8 = torch.empty((N, K), dtype=torch.uint8, device="cuda")
+    ws_ = torch.empty(N, dtype=torch.float32, device="cuda")
+    _lib.check(lib.flw_quant_rows_e4m3(w.data_ptr(), _lib.BF16, N, K, K, w8.data_ptr(), ws_.data_ptr(), stream), "w")
+    x8 = torch.empty((M, K), dtype=torch.uint8, device="cuda")
+    sx = torch.empty(M, dtype=torch.float32, device="cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+
+    def quant():
+        _lib.check(lib.flw_quant_rows_e4m3(x.data_ptr(), _lib.BF16, M, K, K, x8.data_ptr(), sx.data_ptr(), stream), "x")
+
+    def gemm():
+        _lib.check(lib.flw_fp8_scaled_mm(x8.data_ptr(), M, K, w8.data_ptr(), N, sx.data_ptr(), M,
+                                         ws_.data_ptr(), N, y.data_ptr(), N, stream), "gemm")
+
+    for _ in range(warmup):
+        quant()
+        gemm()
+    ev = _events(steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        quant()
+        ev[i][1].record()
+        gemm()
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    q_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
+    g_ms = np.array([e[1].elapsed_time(e[2]) for e in ev])
+    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, quant_ms=float(q_ms.mean()),
+                gemm_ms=float(g_ms.mean()), gemm_ms_min=float(g_ms.min()), flops=2 * M * N * K,
+                quant_bytes=M * K * (2 * 2 + 1) + 4 * M, gemm_bytes=M * K + N * K + 2 * M * N,
+                x=x, w=w)
 
 
 def cpu_baseline(cfg, budget_s=20.0):
-    """Oracle of the FP8-simulated reference path on the host: per-head e4m3 quantise, dequantise,
-    banded fp32 attention; a sample of heads (all B of each), scaled linearly."""
+    """Oracle of the FP8-simulated reference path on the host: e4m3 quantise, dequantise, banded
+    fp32 attention, head by head (all B of each) until the time budget, scaled linearly."""
     from threadpoolctl import threadpool_limits
     from oracle.quant import dequant, per_tensor_fp8
     from oracle.swa import swa_banded
     cores = min(16, os.cpu_count() or 1)
     B, H, T, D, W = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["W"]
     q, k, v = (t.float().numpy() for t in make_inputs(cfg))
+    gran = cfg["granularity"]
     done_heads, t_total = 0, 0.0
     with threadpool_limits(cores):
+        if gran == "tensor":                     # one scale over all heads: quantise once, timed
+            t0 = time.perf_counter()
+            full = [dequant(*per_tensor_fp8(x, "tensor")) for x in (q, k, v)]
+            t_total += time.perf_counter() - t0
         for h in range(H):
             t0 = time.perf_counter()
-            sl = [x[:, h:h + 1] for x in (q, k, v)]
-            deq = [dequant(*per_tensor_fp8(x, cfg["granularity"] if cfg["granularity"] != "bh" else "bh"))
-                   for x in sl]
+            if gran == "tensor":
+                deq = [x[:, h:h + 1] for x in full]
+            else:
+                deq = [dequant(*per_tensor_fp8(x[:, h:h + 1], gran)) for x in (q, k, v)]
             swa_banded(*deq, W, chunk=512)
             t_total += time.perf_counter() - t0
             done_heads += 1
@@ -168,17 +252,33 @@ def cpu_baseline(cfg, budget_s=20.0):
     flops = 4 * D * B * done_heads * in_window_pairs(T, W)
     return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"{done_heads} of {H} heads (all {B} batches each) of the same workload in "
-                      f"{t_total:.1f} s: oracle per-head e4m3 quantise + dequantise + banded fp32 "
-                      f"softmax attention (numpy/BLAS), FLOPs counted as in-window 4*D per pair"}
+                      f"{t_total:.1f} s: oracle e4m3 quantise + dequantise + banded fp32 softmax "
+                      f"attention (numpy / multithreaded BLAS), FLOPs counted as in-window 4*D per pair"}
 
 
-def load_traffic(name):
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    try:
-        with open(path) as f:
-            return json.load(f).get(name)
-    except (OSError, ValueError):
-        return None
+def cpu_baseline_gemm(x, w, budget_s=15.0):
+    """The oracle's _fp8_head recipe on the host: per-row e4m3 of x and W, closed-form GEMM,
+    on row blocks of x until the time budget."""
+    from threadpoolctl import threadpool_limits
+    from oracle.gemm import fp8_linear_a8w8
+    from oracle.quant import rowwise_fp8
+    cores = min(16, os.cpu_count() or 1)
+    xf, wf = x.float().cpu().numpy(), w.float().cpu().numpy()
+    w8, sw = rowwise_fp8(wf)
+    rows, t_total = 0, 0.0
+    with threadpool_limits(cores):
+        for r0 in range(0, xf.shape[0], 512):
+            t0 = time.perf_counter()
+            fp8_linear_a8w8(xf[r0:r0 + 512], w8, sw.reshape(-1))
+            t_total += time.perf_counter() - t0
+            rows += min(512, xf.shape[0] - r0)
+            if t_total > budget_s:
+                break
+    flops = 2 * rows * wf.shape[0] * wf.shape[1]
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{rows} of {xf.shape[0]} activation rows in {t_total:.1f} s: oracle per-row e4m3 "
+                      f"quantisation + float64 closed-form scaled GEMM (numpy / BLAS); weight "
+                      f"quantised once outside the timing, as the weight cache does"}
 
 
 def main():
@@ -193,8 +293,8 @@ def main():
                          "the HBM byte counters of a rocprofv3 --pmc run")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs on exactly one GPU (every box here has one); the "
-              "multi-GPU design is described in DESIGN.md. Use --gpus 1.", file=sys.stderr)
+        print("bench.py: this build runs on exactly one GPU (every box here has one); how the path "
+              "would shard across GPUs is described in DESIGN.md. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
@@ -205,10 +305,20 @@ def main():
         torch.empty_like(src).copy_(src)
         torch.cuda.synchronize()
         del src
+    if args.workload == "c2":
+        line = run_gemm(cfg, args)
+    else:
+        line = run_attention(cfg, args)
+    print(json.dumps(line), flush=True)
+
+
+def run_attention(cfg, args):
     r = bench_attention(cfg, args.steps, args.warmup)
     value = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
     attn_tflops = r["flops"] / (r["attn_ms"] * 1e-3) / 1e12
     quant_gbps = r["quant_bytes"] / (r["quant_ms"] * 1e-3) / 1e9
+    traffic = TRAFFIC.get(args.workload, {})
+    dt = {torch.bfloat16: "bf16", torch.float32: "fp32"}[r["dtype"]]
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -221,25 +331,55 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8_e4m3 (fp32 accumulate)",
-        "data": "synthetic (seeded; bf16 N(0,1) x lognormal per-head factor)",
-        "config": {"workload": f"fp8_swa_attention_forward BASELINE {args.workload.upper()}",
+        "data": DATA[cfg["inputs"]],
+        "config": {"workload": f"fp8_swa_attention_forward, BASELINE {args.workload.upper()}",
                    "B": cfg["B"], "H": cfg["H"], "T": cfg["T"], "D": cfg["D"], "window": cfg["W"],
-                   "causal": True, "scales": cfg["granularity"],
-                   "input_dtype": str(r["inputs"][0].dtype).replace("torch.", "")},
+                   "causal": True, "scales": cfg["granularity"], "input_dtype": dt},
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / FP8_PEAK_TFLOPS, 4),
-                     "traffic": load_traffic(f"swa_fwd_{args.workload}"),
-                     "kernel": "swa_fwd_kernel<64, bf16>", "kernel_ms": round(r["attn_ms"], 4),
-                     "kernel_ms_min": round(r["attn_ms_min"], 4)},
+                     "traffic": traffic.get("swa_fwd"),
+                     "kernel": f"swa_fwd_kernel<{cfg['D']}, {dt}>", "kernel_ms": round(r["attn_ms"], 4),
+                     "kernel_ms_min": round(r["attn_ms_min"], 4), "flop_per_launch": r["flops"]},
         "quant": {"bound": "hbm", "achieved": round(quant_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                   "frac": round(quant_gbps / HBM_PEAK_GBPS, 4), "ms": round(r["quant_ms"], 4),
-                  "algorithmic_bytes": r["quant_bytes"],
-                  "traffic": load_traffic(f"quant_{args.workload}")},
+                  "algorithmic_bytes": r["quant_bytes"], "traffic": traffic.get("quant")},
         "attention_pct_fp8_peak": round(100 * attn_tflops / FP8_PEAK_TFLOPS, 2),
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg)
-    print(json.dumps(line), flush=True)
+    return line
+
+
+def run_gemm(cfg, args):
+    r = bench_gemm(cfg, args.steps, args.warmup)
+    value = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
+    g_tflops = r["flops"] / (r["gemm_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": "FP8 weight-cache linear (per-row x per-channel e4m3) TFLOPS, BASELINE config 2",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate)",
+        "data": DATA["c2"],
+        "config": {"workload": "fp8 linear from the weight cache, BASELINE C2", "M": cfg["M"],
+                   "N": cfg["N"], "K": cfg["K"], "scales": "per-row x per-output-channel"},
+        "roofline": {"bound": "mfma", "achieved": round(g_tflops, 2), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(g_tflops / FP8_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "fp8_gemm_kernel", "kernel_ms": round(r["gemm_ms"], 4),
+                     "kernel_ms_min": round(r["gemm_ms_min"], 4), "flop_per_launch": r["flops"]},
+        "quant": {"bound": "hbm", "achieved": round(r["quant_bytes"] / (r["quant_ms"] * 1e-3) / 1e9, 1),
+                  "peak": HBM_PEAK_GBPS, "unit": "GB/s", "ms": round(r["quant_ms"], 4),
+                  "algorithmic_bytes": r["quant_bytes"]},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_gemm(r["x"], r["w"])
+    return line
 
 
 if __name__ == "__main__":

@@ -24,7 +24,7 @@ namespace flw {
 
 constexpr int kThreads = 256;
 constexpr int64_t kRowsPerChunk = 256;   // multiple of 64: VTILE chunks hold whole key tiles
-constexpr int kUnroll = 8;               // 16-byte loads in flight per thread
+constexpr int kUnroll = 2;               // 16-byte loads in flight per thread (swept: 2..16)
 
 struct QTensor {
   const void* x;
