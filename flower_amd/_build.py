@@ -25,14 +25,13 @@ ARCH = os.environ.get("FLW_OFFLOAD_ARCH", "gfx950")
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in ordinary VGPRs: the attention rescale and the GEMM epilogue then
-    # work on them in place instead of copying through AGPRs.
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-result", "-I", os.path.join(ROOT, "include"),
 ]
-# The attention kernel's max reductions run on MFMA results; in IEEE mode every fmax operand is
-# first re-quietened (one extra VALU op per score). NaN inputs still give NaN rows without it.
-PER_SOURCE = {"flw_swa.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
+# Attention: MFMA accumulators in ordinary VGPRs (the online-softmax rescale works on them in
+# place instead of copying through AGPRs), and no IEEE mode, since in IEEE mode every fmax operand
+# of the row max is first re-quietened (one extra VALU op per score); NaN inputs still give NaN
+# rows without it. The GEMM keeps the default form: its 256 accumulators per lane live in AGPRs.
+PER_SOURCE = {"flw_swa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans", "-mno-amdgpu-ieee"]}
 NOISE = "'-packed-fp32-ops' is not a recognized feature"
 
 

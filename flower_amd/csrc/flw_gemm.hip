@@ -9,6 +9,9 @@
 // ds_read_b128), the next stage's global loads overlapping the current stage's MFMAs.
 #include "flw_common.h"
 
+// m0 is clobbered by the direct-to-LDS loads below; nothing else here uses it.
+#pragma clang diagnostic ignored "-Winline-asm"
+
 namespace flw {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -34,7 +37,8 @@ struct GemmParams {
   uint16_t* y;         // [M, N] bf16
   int64_t ys;          // row stride of y (elements)
   int M, N, K;
-  int tiles_n;         // ceil(N / 128)
+  int tiles_n;         // output tiles along N
+  int tiles_m;         // output tiles along M
 };
 
 __device__ __forceinline__ v8i gfrag(const uint8_t* lds, int off) {
@@ -139,6 +143,214 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------- 256 x 256 tile, direct-to-LDS
+//
+// For K % 128 == 0 (every model shape). Workgroup tile 256 (n) x 256 (m), 8 waves (two per SIMD)
+// in a 2 x 4 grid of 128 (n) x 64 (m) wave tiles: per 64-deep K chunk a wave reads 4 + 2
+// fragments (12 KB of LDS) for 8 v_mfma_f32_32x32x64_f8f6f4 (512 MFMA cycles), and the two waves
+// of a SIMD interleave one's LDS reads with the other's MFMAs.
+// Operand tiles move global -> LDS with global_load_lds_dwordx4 (no staging registers), 128 K
+// bytes of each row per stage so that one instruction reads 8 whole 128-byte lines (8 lanes per
+// row). In LDS a tile is row-major, 128 bytes per row, with the 16-byte chunk c of row r stored
+// at position c ^ ((r >> 1) & 7): a lane's DMA slot is fixed (base + 16 lane), so the swizzle is
+// applied by choosing which global chunk each lane fetches, and it makes the fragment reads (16
+// consecutive rows, one chunk each) hit 16 distinct bank groups. Two LDS stages of 64 KB, one
+// barrier per stage. Rows past M / N load a clamped valid row (their outputs are not stored).
+constexpr int kFBN = 256, kFBM = 256, kFBK = 128;
+constexpr int kFThreads = 512;
+constexpr int kGroupM = 4;                        // m-tiles per tile group (L2 locality)
+constexpr int kFOpBytes = 256 * kFBK;             // one operand tile per stage (32 KB)
+constexpr int kFStageBytes = 2 * kFOpBytes;       // W tile then X tile
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
+// (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt / lgkmcnt left free).
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// Workgroup barrier without the release fence __syncthreads() carries (which would drain every
+// outstanding global load, i.e. the whole prefetch, at each K step). Callers wait for the loads
+// they need with an explicit vmcnt first; the empty asm statements keep the compiler from moving
+// memory operations across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
+
+// Byte offset of chunk c (16 bytes) of row r in a swizzled 128-byte-row tile.
+__device__ __forceinline__ int swz_off(int r, int c) { return r * 128 + 16 * (c ^ ((r >> 1) & 7)); }
+
+// A 32 x 64 MFMA fragment of row block rb, K chunk kc: lane (row 32 rb + lane % 32, half h)
+// takes the 32 bytes at K offset 64 kc + 32 h.
+__device__ __forceinline__ v8i swz_frag(const uint8_t* tile, int rb, int kc, int lane) {
+  const int r = 32 * rb + (lane & 31), c = 4 * kc + 2 * (lane >> 5);
+  const uint4 a = *reinterpret_cast<const uint4*>(tile + swz_off(r, c));
+  const uint4 b = *reinterpret_cast<const uint4*>(tile + swz_off(r, c + 1));
+  return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
+}
+
+// One 256 x 256 output tile: K loop over two LDS stages, then the scaled bf16 epilogue.
+__device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
+                                          int n0, int wave, int lane) {
+  const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
+  // Loads: a stage is 2 x 256 rows x 128 bytes = 512 rows; wave w fills rows 64 w .. 64 w + 63
+  // (waves 0-3: W, 4-7: X) with 8 instructions of 8 rows each. Lane i of instruction t covers
+  // row 8 t + i / 8 of the wave's range, LDS position i % 8, i.e. global chunk (i % 8) ^ swz.
+  const int op = wave >> 2;                       // uniform
+  const uint8_t* gsrc = op == 0 ? p.w8 : p.x8;
+  uint32_t goff[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int r = 64 * (wave & 3) + 8 * t + (lane >> 3);      // row within the operand tile
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int grow = op == 0 ? min(n0 + r, p.N - 1) : min(m0 + r, p.M - 1);
+    goff[t] = (uint32_t)grow * (uint32_t)p.K + 16u * (uint32_t)c;
+  }
+  const int lbase = op * kFOpBytes + (64 * (wave & 3)) * 128;
+  // Issued from inline assembly: the compiler then does not track these LDS writes and does not
+  // drain the prefetch before every fragment read; the kernel orders them itself (an explicit
+  // vmcnt wait for this wave's loads, then a workgroup barrier, before a stage is read).
+  auto issue = [&](uint8_t* stage, int s) __attribute__((always_inline)) {
+    const uint32_t k0 = (uint32_t)s * kFBK;
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8_t*)(stage + lbase);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :: "s"(lds + t * 1024), "v"(goff[t] + k0), "s"(gsrc) : "memory", "m0");
+  };
+
+  v16f acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+  const int nst = p.K / kFBK;
+  issue(st0, 0);
+
+  // Stage s in `cur`: prefetch stage s+1 into `nxt` (its readers finished at the end of step
+  // s-1, before the barrier below was passed by everyone... see the barrier at the step's end),
+  // wait for stage s, publish it, then two K chunks of fragments + MFMAs.
+  auto step = [&](int s, const uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+    if (s + 1 < nst) {
+      issue(nxt, s + 1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));   // this wave's loads of stage s landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    lds_barrier();                                // ... and every wave's
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      v8i a[4], b[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = swz_frag(cur, 4 * wn + i, kc, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = swz_frag(cur + kFOpBytes, 2 * wm + j, kc, lane);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = gemm_mfma(a[i], b[j], acc[i][j]);
+    }
+    // Everyone's fragment reads of `cur` are done before anyone refills it (next step + 1).
+    __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
+    lds_barrier();
+  };
+  for (int s = 0; s < nst; s += 2) {
+    step(s, st0, st1);
+    if (s + 1 < nst) step(s + 1, st1, st0);
+  }
+
+  // Epilogue: lane owns m = m0 + 64 wm + 32 j + lane % 32, n = n0 + 128 wn + 32 i + 8 g + 4 hh + 0..3
+  const int hh = lane >> 5;
+  float sxm[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int m = min(m0 + 64 * wm + 32 * j + (lane & 31), p.M - 1);
+    sxm[j] = p.sx[(int64_t)m * p.sx_step];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float swn[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = min(n0 + 128 * wn + 32 * i + 8 * g + 4 * hh, p.N - 4);
+      if (p.sw_step) {
+        const float4 v = *reinterpret_cast<const float4*>(p.sw + n);
+        swn[4 * g] = v.x; swn[4 * g + 1] = v.y; swn[4 * g + 2] = v.z; swn[4 * g + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) swn[4 * g + e] = p.sw[0];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = m0 + 64 * wm + 32 * j + (lane & 31);
+      if (m >= p.M) continue;
+      uint16_t* yrow = p.y + (int64_t)m * p.ys;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + 128 * wn + 32 * i + 8 * g + 4 * hh;
+        if (n >= p.N) continue;      // N % 4 == 0 is required on the host
+        const v16f& c = acc[i][j];
+        uint2 w;
+        w.x = pack_bf16x2(c[4 * g] * sxm[j] * swn[4 * g], c[4 * g + 1] * sxm[j] * swn[4 * g + 1]);
+        w.y = pack_bf16x2(c[4 * g + 2] * sxm[j] * swn[4 * g + 2], c[4 * g + 3] * sxm[j] * swn[4 * g + 3]);
+        *reinterpret_cast<uint2*>(yrow + n) = w;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p) {
+  // One array per stage: every LDS access below names its stage at compile time, so the
+  // compiler can see that the direct-to-LDS loads in flight write the other stage.
+  __shared__ __align__(16) uint8_t st0[kFStageBytes];
+  __shared__ __align__(16) uint8_t st1[kFStageBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
+
+  // Persistent over tiles: workgroup b takes tiles L, L + G, L + 2G, ... (G = grid size), so
+  // the output stores of one tile drain while the next tile computes. L = (b % 8) (G / 8) + b / 8
+  // gives the G/8 workgroups of XCD b % 8 consecutive tile numbers, and tiles are numbered in
+  // groups of kGroupM m-tiles (m fastest): the 32 tiles an XCD runs at once are a 4 x 8 block
+  // whose operands (3 MB) stay in its 4 MB L2.
+  const int G = gridDim.x;
+  const int L = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int ntiles = p.tiles_n * p.tiles_m;
+  const int lane_w = lane;   // (kept for the loops below)
+  (void)lane_w;
+
+  for (int t = L; t < ntiles; t += G) {
+    const int group = t / (kGroupM * p.tiles_n);
+    const int first_m = group * kGroupM;
+    const int gm = min(p.tiles_m - first_m, kGroupM);
+    const int tm = first_m + (t % (kGroupM * p.tiles_n)) % gm;
+    const int tn = (t % (kGroupM * p.tiles_n)) / gm;
+    gemm_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane);
+  }
+}
+
+// Compute units of the current device (queried once per device).
+static int compute_units() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
                      const float* sx, int64_t sx_count, const float* sw, int64_t sw_count,
                      void* y, int64_t ys, hipStream_t s) {
@@ -156,6 +368,16 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
   p.sx_step = sx_count == 1 ? 0 : 1; p.sw_step = sw_count == 1 ? 0 : 1;
   p.y = static_cast<uint16_t*>(y); p.ys = ys;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  if (K % kFBK == 0 && N * K < (1ll << 32) && M * K < (1ll << 32)) {
+    p.tiles_n = (int)((N + kFBN - 1) / kFBN);
+    p.tiles_m = (int)((M + kFBM - 1) / kFBM);
+    const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
+    FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
+    // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per tile.
+    const int64_t grid = tiles < compute_units() ? tiles : compute_units();
+    hipLaunchKernelGGL(fp8_gemm_256_kernel, dim3((unsigned)grid), dim3(kFThreads), 0, s, p);
+    return check_launch("flw_fp8_scaled_mm");
+  }
   p.tiles_n = (int)((N + kGBN - 1) / kGBN);
   const int64_t tiles = (int64_t)p.tiles_n * ((M + kGBM - 1) / kGBM);
   FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");

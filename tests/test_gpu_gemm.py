@@ -31,7 +31,8 @@ def codes(shape, seed):
     return c
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 256, 512), (100, 36, 80), (257, 132, 1040), (1, 16, 16)])
+@pytest.mark.parametrize("M,N,K", [(128, 256, 512), (100, 36, 80), (257, 132, 1040), (1, 16, 16),
+                                   (300, 132, 256), (1, 20, 128), (513, 260, 1024), (256, 512, 384)])
 @pytest.mark.parametrize("sx_per_row,sw_per_col", [(True, True), (False, False), (True, False)])
 def test_scaled_mm_matches_closed_form(M, N, K, sx_per_row, sw_per_col):
     from flower_amd import _lib as L
