@@ -1,6 +1,6 @@
 """Benchmark of the FP8 sliding-window-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5]
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
@@ -50,12 +50,14 @@ WORKLOADS = {
     "c4": dict(B=1, H=16, T=32768, D=64, W=4096, granularity="head", inputs="student_t_channels"),
     "c1": dict(B=1, H=8, T=1024, D=64, W=256, granularity="tensor", inputs="randn_fp32"),
     "c2": dict(M=8192, N=4096, K=1024, outlier_frac=0.001, outlier_scale=20.0, w_std=0.02),
+    "c5": dict(B=1, T=32768, d_model=1024, num_heads=16, ffn_dim=4096, W=4096, w_std=0.02),
 }
 DATA = {
     "lognormal_heads": "synthetic (seeded; bf16 N(0,1) x a lognormal(0,1) factor per head)",
     "student_t_channels": "synthetic (seeded; bf16 N(0,1), 4 of 64 channels Student-t nu=4)",
     "randn_fp32": "synthetic (seeded; fp32 N(0,1))",
     "c2": "synthetic (seeded; bf16 x N(0,1) with 0.1% outliers x20; weight N(0,0.02), random init)",
+    "c5": "synthetic (seeded; bf16 x N(0,1); every Linear weight N(0,0.02), random init)",
 }
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload
@@ -307,6 +309,8 @@ def main():
         del src
     if args.workload == "c2":
         line = run_gemm(cfg, args)
+    elif args.workload == "c5":
+        line = run_block(cfg, args)
     else:
         line = run_attention(cfg, args)
     print(json.dumps(line), flush=True)
@@ -380,6 +384,48 @@ def run_gemm(cfg, args):
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_gemm(r["x"], r["w"])
     return line
+
+
+def run_block(cfg, args):
+    """one FP8 decoder block forward (RMSNorm -> QKV -> per-head FP8 SWA -> O ->
+    residual -> RMSNorm -> GELU MLP -> residual), every Linear from the FP8 weight cache."""
+    from flower_amd.block import Fp8DecoderBlock, block_flops, init_block_
+    from flower_amd.precision import fp8_weight_cache
+    B, T, d = cfg["B"], cfg["T"], cfg["d_model"]
+    blk = Fp8DecoderBlock(d, cfg["num_heads"], cfg["ffn_dim"], cfg["W"])
+    init_block_(blk, std=cfg["w_std"], seed=0)
+    blk = blk.to("cuda", torch.bfloat16)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, T, d, generator=g).to("cuda", torch.bfloat16)
+    flops = block_flops(T, B, d, cfg["ffn_dim"], cfg["num_heads"], cfg["W"])
+    with fp8_weight_cache(blk):
+        for _ in range(args.warmup):
+            blk(x)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for a, b in ev:
+            a.record()
+            blk(x)
+            b.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    value = flops / (wall / args.steps) / 1e12
+    return {
+        "metric": "FP8 decoder block forward TFLOPS (linear + in-window attention FLOPs), BASELINE config 5",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3 (fp32 accumulate), bf16 activations",
+        "data": DATA["c5"],
+        "config": {"workload": "Fp8DecoderBlock forward, BASELINE C5", "B": B, "T": T, "d_model": d,
+                   "num_heads": cfg["num_heads"], "ffn_dim": cfg["ffn_dim"], "window": cfg["W"],
+                   "scales": "per-head attention, per-row x per-channel linears"},
+        "roofline": {"bound": "mfma", "achieved": round(flops / (ms * 1e-3) / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel": "whole block (HIP events around each forward)",
+                     "kernel_ms": round(ms, 4), "flop_per_launch": flops},
+    }
 
 
 if __name__ == "__main__":
