@@ -11,8 +11,8 @@ C ABI of libflower_amd.so on torch's current stream.
 
 Printed (one JSON line):
   value      -- in-window attention FLOP/s of the whole step, TFLOP/s (4*D per in-window pair)
-  roofline   -- the attention kernel alone (HIP events around each of its launches, on the
-                stream it runs on): achieved TFLOP/s against MI355X dense FP8 MFMA peak
+  roofline   -- the attention kernel alone (a HIP event pair per launch, recorded from the
+                kernel's own dispatch on the stream it runs on, via flw_time_next_launch): achieved TFLOP/s against MI355X dense FP8 MFMA peak
                 (5.0 PFLOP/s); traffic = its measured HBM bytes per launch (TRAFFIC below)
   quant      -- the quantise launch pair: algorithmic bytes (2 reads + 1 write per element) /
                 their event time, against 8 TB/s HBM
@@ -60,11 +60,12 @@ DATA = {
     "c5": "synthetic (seeded; bf16 x N(0,1); every Linear weight N(0,0.02), random init)",
 }
 
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload
-# (profiles/swa_fwd_c3.md). FETCH_SIZE is scaled by 2.0: a plain 256 MiB device copy reads back
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on each workload
+# (summaries under profiles/). FETCH_SIZE is scaled by 2.0: a plain 256 MiB device copy reads back
 # 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0).
 TRAFFIC = {
     "c3": {"swa_fwd": 167_979_008, "quant": 503_929_856},
+    "c2": {"gemm": 120_440_320},
 }
 
 
@@ -106,9 +107,21 @@ def in_window_pairs(T, W):
     return ramp * (ramp + 1) // 2 + max(0, T - W) * W
 
 
-def _events(n):
-    return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-             torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+def _events(n, per=2):
+    """n tuples of `per` timing events, created up front (torch creates an event lazily, on its
+    first record) so their handles can be passed to the library before the timed region."""
+    ev = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(per)) for _ in range(n)]
+    for t in ev:
+        for e in t:
+            e.record()
+    return ev
+
+
+def _arm(lib, pair):
+    """The next attention / GEMM launch records this event pair from its own dispatch
+    timestamps (flw_time_next_launch -> hipExtLaunchKernel): the kernel's duration alone."""
+    from flower_amd import _lib
+    _lib.check(lib.flw_time_next_launch(pair[0].cuda_event, pair[1].cuda_event), "timer")
 
 
 class AttentionStep:
@@ -160,19 +173,19 @@ def bench_attention(cfg, steps, warmup):
     for _ in range(warmup):
         step.quant(stream)
         step.attend(stream)
-    ev = _events(steps)
+    ev, kev = _events(steps), _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         ev[i][0].record()
         step.quant(stream)
         ev[i][1].record()
+        _arm(step.lib, kev[i])
         step.attend(stream)
-        ev[i][2].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     quant_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
-    attn_ms = np.array([e[1].elapsed_time(e[2]) for e in ev])
+    attn_ms = np.array([e[0].elapsed_time(e[1]) for e in kev])
     B, H, T, D = q.shape
     return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, quant_ms=float(np.mean(quant_ms)),
                 attn_ms=float(np.mean(attn_ms)), attn_ms_min=float(np.min(attn_ms)),
@@ -205,22 +218,22 @@ def bench_gemm(cfg, steps, warmup):
     for _ in range(warmup):
         quant()
         gemm()
-    ev = _events(steps)
+    ev, kev = _events(steps), _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         ev[i][0].record()
         quant()
         ev[i][1].record()
+        _arm(lib, kev[i])
         gemm()
-        ev[i][2].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     q_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
-    g_ms = np.array([e[1].elapsed_time(e[2]) for e in ev])
+    g_ms = np.array([e[0].elapsed_time(e[1]) for e in kev])
     return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, quant_ms=float(q_ms.mean()),
                 gemm_ms=float(g_ms.mean()), gemm_ms_min=float(g_ms.min()), flops=2 * M * N * K,
-                quant_bytes=M * K * (2 * 2 + 1) + 4 * M, gemm_bytes=M * K + N * K + 2 * M * N,
+                quant_bytes=M * K * (2 * 2 + 1) + 4 * M, gemm_bytes=M * K + N * K + 2 * M * N + 4 * (M + N),
                 x=x, w=w)
 
 
@@ -374,8 +387,9 @@ def run_gemm(cfg, args):
         "config": {"workload": "fp8 linear from the weight cache, BASELINE C2", "M": cfg["M"],
                    "N": cfg["N"], "K": cfg["K"], "scales": "per-row x per-output-channel"},
         "roofline": {"bound": "mfma", "achieved": round(g_tflops, 2), "peak": FP8_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(g_tflops / FP8_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "fp8_gemm_kernel", "kernel_ms": round(r["gemm_ms"], 4),
+                     "unit": "TFLOP/s", "frac": round(g_tflops / FP8_PEAK_TFLOPS, 4),
+                     "traffic": TRAFFIC["c2"]["gemm"], "algorithmic_bytes": r["gemm_bytes"],
+                     "kernel": "fp8_gemm_256_kernel", "kernel_ms": round(r["gemm_ms"], 4),
                      "kernel_ms_min": round(r["gemm_ms_min"], 4), "flop_per_launch": r["flops"]},
         "quant": {"bound": "hbm", "achieved": round(r["quant_bytes"] / (r["quant_ms"] * 1e-3) / 1e9, 1),
                   "peak": HBM_PEAK_GBPS, "unit": "GB/s", "ms": round(r["quant_ms"], 4),

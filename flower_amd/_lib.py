@@ -28,6 +28,7 @@ _P64 = POINTER(c_int64)
 SIGNATURES = {
     "flw_last_error": (c_char_p, []),
     "flw_abi_version": (c_int, []),
+    "flw_time_next_launch": (c_int, [c_void_p, c_void_p]),
     "flw_quant_workspace_bytes": (c_size_t, [c_int64] * 4),
     "flw_vtile_bytes": (c_size_t, [c_int64] * 4),
     "flw_quant_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,

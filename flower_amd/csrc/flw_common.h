@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
 
@@ -14,6 +15,19 @@ namespace flw {
 // the calling thread is kept here for flw_last_error().
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// Launch of a kernel taking one parameter struct. If flw_time_next_launch() armed an event pair
+// on this thread, the launch consumes it: hipExtLaunchKernel records the pair from the dispatch's
+// own start / end timestamps.
+void take_timer(hipEvent_t* start, hipEvent_t* stop);
+
+template <typename P>
+inline hipError_t launch_timed(const void* kernel, dim3 grid, dim3 block, hipStream_t stream, P p) {
+  void* args[] = {static_cast<void*>(&p)};
+  hipEvent_t start, stop;
+  take_timer(&start, &stop);
+  return hipExtLaunchKernel(kernel, grid, block, args, 0, stream, start, stop, 0);
+}
 
 #define FLW_REQUIRE(cond, code, ...)                      \
   do {                                                    \

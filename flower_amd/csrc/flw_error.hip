@@ -16,6 +16,14 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
+static thread_local hipEvent_t g_timer_start = nullptr, g_timer_stop = nullptr;
+
+void take_timer(hipEvent_t* start, hipEvent_t* stop) {
+  *start = g_timer_start;
+  *stop = g_timer_stop;
+  g_timer_start = g_timer_stop = nullptr;
+}
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FLW_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
@@ -26,3 +34,11 @@ int check_launch(const char* what) {
 
 extern "C" const char* flw_last_error(void) { return flw::g_last_error; }
 extern "C" int flw_abi_version(void) { return FLW_ABI_VERSION; }
+
+extern "C" int flw_time_next_launch(void* start_event, void* stop_event) {
+  FLW_REQUIRE((start_event == nullptr) == (stop_event == nullptr), FLW_E_INVALID,
+              "flw_time_next_launch: pass both events or neither");
+  flw::g_timer_start = static_cast<hipEvent_t>(start_event);
+  flw::g_timer_stop = static_cast<hipEvent_t>(stop_event);
+  return FLW_OK;
+}

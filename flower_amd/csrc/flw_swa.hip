@@ -374,10 +374,9 @@ int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, 
 
 template <int D>
 static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s) {
-  if (out_dtype == FLW_F32)
-    hipLaunchKernelGGL((swa_fwd_kernel<D, float>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((swa_fwd_kernel<D, uint16_t>), grid, dim3(256), 0, s, p);
+  const void* k = out_dtype == FLW_F32 ? reinterpret_cast<const void*>(&swa_fwd_kernel<D, float>)
+                                       : reinterpret_cast<const void*>(&swa_fwd_kernel<D, uint16_t>);
+  launch_timed(k, grid, dim3(256), s, p);
 }
 
 static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, const int64_t* kst,

@@ -51,6 +51,12 @@ enum flw_gemm_mode { FLW_GEMM_A8W8 = 0, FLW_GEMM_W8A16 = 1 };
 const char* flw_last_error(void);
 int flw_abi_version(void);
 
+/* Measurement hook, no counterpart in the reference: arms two hipEvent_t (created with timing
+ * enabled, passed as void*) on the calling thread. The next launch of the attention kernel or of
+ * the FP8 GEMM on this thread records them from its own dispatch (hipExtLaunchKernel), so
+ * hipEventElapsedTime(start, stop) is that kernel's duration alone. Both NULL disarms. */
+int flw_time_next_launch(void* start_event, void* stop_event);
+
 /* ---------------------------------------------------------------- quantisation */
 
 /* Workspace for flw_quant_e4m3 / flw_fake_quant_e4m3 on a (B, H, T, D) tensor (amax partials). */
