@@ -9,13 +9,15 @@ e4m3 quantisation of Q, K and V (V into the MFMA tile layout, one launch pair fo
 the fused FP8 attention kernel, on inputs already resident in HBM. Everything runs through the
 C ABI of libflower_amd.so on torch's current stream.
 
+Before the W warm-up steps, the step runs untimed for SPIN_UP_S seconds (clock spin-up).
+
 Printed (one JSON line):
   value      -- in-window attention FLOP/s of the whole step, TFLOP/s (4*D per in-window pair)
   roofline   -- the attention kernel alone (a HIP event pair per launch, recorded from the
                 kernel's own dispatch on the stream it runs on, via flw_time_next_launch): achieved TFLOP/s against MI355X dense FP8 MFMA peak
                 (5.0 PFLOP/s); traffic = its measured HBM bytes per launch (TRAFFIC below)
   quant      -- the quantise launch pair: algorithmic bytes (2 reads + 1 write per element) /
-                their event time, against 8 TB/s HBM
+                their time (event pair recorded by the pair's own dispatches), against 8 TB/s HBM
   cpu_baseline -- the CPU oracle of the FP8-simulated reference path (e4m3 quantise, dequantise,
                 banded fp32 softmax attention) on a bounded sample of the same workload, host
                 cores, scaled linearly to the same unit.
@@ -117,9 +119,25 @@ def _events(n, per=2):
     return ev
 
 
+SPIN_UP_S = 0.3
+
+
+def _spin_up(step, seconds=SPIN_UP_S):
+    """Run the step, untimed, until `seconds` of wall time have passed. An idle MI355X needs
+    ~20-30 ms of sustained work to leave its low clock state: the first ~100 attention launches
+    of a fresh process run ~15 % slower than the rest, so W short warm-up steps alone would time
+    the clock ramp rather than the kernels."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            step()
+        torch.cuda.synchronize()
+
+
 def _arm(lib, pair):
-    """The next attention / GEMM launch records this event pair from its own dispatch
-    timestamps (flw_time_next_launch -> hipExtLaunchKernel): the kernel's duration alone."""
+    """The next entry point called records this event pair from its own dispatches
+    (flw_time_next_launch -> hipExtLaunchKernel): start with its first kernel, stop with its last,
+    so the interval holds those kernels and no marker packets."""
     from flower_amd import _lib
     _lib.check(lib.flw_time_next_launch(pair[0].cuda_event, pair[1].cuda_event), "timer")
 
@@ -170,6 +188,7 @@ def bench_attention(cfg, steps, warmup):
     q, k, v = (t.cuda() for t in make_inputs(cfg))
     step = AttentionStep(q, k, v, cfg)
     stream = torch.cuda.current_stream().cuda_stream
+    _spin_up(lambda: (step.quant(stream), step.attend(stream)))
     for _ in range(warmup):
         step.quant(stream)
         step.attend(stream)
@@ -177,9 +196,8 @@ def bench_attention(cfg, steps, warmup):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        ev[i][0].record()
+        _arm(step.lib, ev[i])
         step.quant(stream)
-        ev[i][1].record()
         _arm(step.lib, kev[i])
         step.attend(stream)
     torch.cuda.synchronize()
@@ -215,22 +233,28 @@ def bench_gemm(cfg, steps, warmup):
         _lib.check(lib.flw_fp8_scaled_mm(x8.data_ptr(), M, K, w8.data_ptr(), N, sx.data_ptr(), M,
                                          ws_.data_ptr(), N, y.data_ptr(), N, stream), "gemm")
 
+    _spin_up(lambda: (quant(), gemm()))
     for _ in range(warmup):
         quant()
         gemm()
-    ev, kev = _events(steps), _events(steps)
+    kev = _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        ev[i][0].record()
         quant()
-        ev[i][1].record()
         _arm(lib, kev[i])
         gemm()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    q_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
     g_ms = np.array([e[0].elapsed_time(e[1]) for e in kev])
+    # the row quantiser alone, timed after the steps (it has no timing hook of its own)
+    qev = _events(steps)
+    for a, b in qev:
+        a.record()
+        quant()
+        b.record()
+    torch.cuda.synchronize()
+    q_ms = np.array([a.elapsed_time(b) for a, b in qev])
     return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, quant_ms=float(q_ms.mean()),
                 gemm_ms=float(g_ms.mean()), gemm_ms_min=float(g_ms.min()), flops=2 * M * N * K,
                 quant_bytes=M * K * (2 * 2 + 1) + 4 * M, gemm_bytes=M * K + N * K + 2 * M * N + 4 * (M + N),
@@ -342,7 +366,7 @@ def run_attention(cfg, args):
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": args.warmup, "spin_up_s": SPIN_UP_S,
         "ms_per_step": round(r["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -377,7 +401,7 @@ def run_gemm(cfg, args):
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": args.warmup, "spin_up_s": SPIN_UP_S,
         "ms_per_step": round(r["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -413,6 +437,7 @@ def run_block(cfg, args):
     x = torch.randn(B, T, d, generator=g).to("cuda", torch.bfloat16)
     flops = block_flops(T, B, d, cfg["ffn_dim"], cfg["num_heads"], cfg["W"])
     with fp8_weight_cache(blk):
+        _spin_up(lambda: blk(x))
         for _ in range(args.warmup):
             blk(x)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
@@ -429,7 +454,7 @@ def run_block(cfg, args):
     return {
         "metric": "FP8 decoder block forward TFLOPS (linear + in-window attention FLOPs), BASELINE config 5",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4), "higher_is_better": True,
+        "warmup": args.warmup, "spin_up_s": SPIN_UP_S, "ms_per_step": round(wall / args.steps * 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3 (fp32 accumulate), bf16 activations",
         "data": DATA["c5"],
         "config": {"workload": "Fp8DecoderBlock forward, BASELINE C5", "B": B, "T": T, "d_model": d,

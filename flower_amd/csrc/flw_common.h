@@ -16,17 +16,27 @@ namespace flw {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
-// Launch of a kernel taking one parameter struct. If flw_time_next_launch() armed an event pair
-// on this thread, the launch consumes it: hipExtLaunchKernel records the pair from the dispatch's
-// own start / end timestamps.
-void take_timer(hipEvent_t* start, hipEvent_t* stop);
+// Kernel timing: flw_time_next_launch() arms an event pair on the calling thread; the next entry
+// point takes it (take_timer disarms) and hands `start` to its first launch and `stop` to its last.
+// hipExtLaunchKernel records each event from that dispatch's own start / end timestamps.
+struct Timer {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+Timer take_timer();
 
+// Launch of a kernel taking one parameter struct, optionally recording start / stop events.
+template <typename P>
+inline hipError_t launch_ext(const void* kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                             P p, hipEvent_t start, hipEvent_t stop) {
+  void* args[] = {static_cast<void*>(&p)};
+  return hipExtLaunchKernel(kernel, grid, block, args, lds, stream, start, stop, 0);
+}
+
+// A single-kernel entry point: the whole armed pair goes to its one launch.
 template <typename P>
 inline hipError_t launch_timed(const void* kernel, dim3 grid, dim3 block, hipStream_t stream, P p) {
-  void* args[] = {static_cast<void*>(&p)};
-  hipEvent_t start, stop;
-  take_timer(&start, &stop);
-  return hipExtLaunchKernel(kernel, grid, block, args, 0, stream, start, stop, 0);
+  const Timer t = take_timer();
+  return launch_ext(kernel, grid, block, 0, stream, p, t.start, t.stop);
 }
 
 #define FLW_REQUIRE(cond, code, ...)                      \

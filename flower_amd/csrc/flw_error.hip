@@ -18,10 +18,12 @@ int set_error(int code, const char* fmt, ...) {
 
 static thread_local hipEvent_t g_timer_start = nullptr, g_timer_stop = nullptr;
 
-void take_timer(hipEvent_t* start, hipEvent_t* stop) {
-  *start = g_timer_start;
-  *stop = g_timer_stop;
+Timer take_timer() {
+  Timer t;
+  t.start = g_timer_start;
+  t.stop = g_timer_stop;
   g_timer_start = g_timer_stop = nullptr;
+  return t;
 }
 
 int check_launch(const char* what) {

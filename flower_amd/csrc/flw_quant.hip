@@ -354,18 +354,18 @@ static size_t partial_bytes(int64_t B, int64_t H, int64_t T) {
 }
 
 template <int MODE>
-static int launch_quant(const QuantParams& p, int ntensors, int dtype, hipStream_t s, const char* name) {
+static int launch_quant(const QuantParams& p, int ntensors, int dtype, hipStream_t s, const char* name,
+                        Timer tm) {
   dim3 grid((unsigned)p.nchunks, (unsigned)(p.d0 * p.d1), (unsigned)ntensors);
   bool any_vtile = false;
   for (int i = 0; i < ntensors; ++i) any_vtile |= p.t[i].layout == FLW_LAYOUT_VTILE;
   const size_t lds = MODE == 0 && any_vtile ? (size_t)(kRowsPerChunk * p.d3) : 0;
-  if (dtype == FLW_F32) {
-    hipLaunchKernelGGL(amax_kernel<float>, grid, dim3(kThreads), 0, s, p);
-    hipLaunchKernelGGL((quant_kernel<float, MODE>), grid, dim3(kThreads), lds, s, p);
-  } else {
-    hipLaunchKernelGGL(amax_kernel<uint16_t>, grid, dim3(kThreads), 0, s, p);
-    hipLaunchKernelGGL((quant_kernel<uint16_t, MODE>), grid, dim3(kThreads), lds, s, p);
-  }
+  const void* ka = dtype == FLW_F32 ? reinterpret_cast<const void*>(&amax_kernel<float>)
+                                    : reinterpret_cast<const void*>(&amax_kernel<uint16_t>);
+  const void* kq = dtype == FLW_F32 ? reinterpret_cast<const void*>(&quant_kernel<float, MODE>)
+                                    : reinterpret_cast<const void*>(&quant_kernel<uint16_t, MODE>);
+  launch_ext(ka, grid, dim3(kThreads), 0, s, p, tm.start, nullptr);
+  launch_ext(kq, grid, dim3(kThreads), lds, s, p, nullptr, tm.stop);
   return check_launch(name);
 }
 
@@ -379,7 +379,7 @@ static void set_tensor(QTensor& t, const void* x, int64_t sb, int64_t sh, int64_
 int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
                  int64_t D, const int64_t* strides, int granularity, const int* layouts,
                  uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
-                 hipStream_t stream) {
+                 hipStream_t stream, Timer tm) {
   FLW_REQUIRE(n >= 1 && n <= 3, FLW_E_INVALID, "1 to 3 tensors per call");
   FLW_REQUIRE(granularity >= FLW_SCALE_TENSOR && granularity <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", granularity);
   FLW_REQUIRE(ws != nullptr && ws_bytes >= (size_t)n * partial_bytes(B, H, T), FLW_E_WORKSPACE,
@@ -401,7 +401,7 @@ int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, 
   }
   p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D;
   p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(ws); p.granularity = granularity;
-  return launch_quant<0>(p, n, dtype, stream, "flw_quant_e4m3");
+  return launch_quant<0>(p, n, dtype, stream, "flw_quant_e4m3", tm);
 }
 
 int quant_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
@@ -409,7 +409,7 @@ int quant_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_
                void* ws, size_t ws_bytes, hipStream_t stream) {
   const int64_t strides[3] = {sb, sh, st};
   return quant_bhtd_n(1, &x, dtype, B, H, T, D, strides, granularity, &layout, &out, &scale_out, ws,
-                      ws_bytes, stream);
+                      ws_bytes, stream, take_timer());
 }
 
 // ---------------------------------------------------------------- diagnostics
@@ -458,7 +458,7 @@ extern "C" int flw_quant_qkv_e4m3(const void* q, const void* k, const void* v, i
   uint8_t* outs[3] = {q8, k8, v_tiles};
   float* sc[3] = {scales_out, scales_out + G, scales_out + 2 * G};
   return quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, sc, workspace,
-                      workspace_bytes, static_cast<hipStream_t>(stream));
+                      workspace_bytes, static_cast<hipStream_t>(stream), take_timer());
 }
 
 extern "C" int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T,
@@ -481,7 +481,7 @@ extern "C" int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t 
   set_tensor(p.t[0], x, stride_b, stride_h, stride_t, D, FLW_LAYOUT_BHTD, nullptr, out, sc);
   p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D;
   p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(workspace); p.granularity = granularity;
-  return launch_quant<1>(p, 1, dtype, static_cast<hipStream_t>(stream), "flw_fake_quant_e4m3");
+  return launch_quant<1>(p, 1, dtype, static_cast<hipStream_t>(stream), "flw_fake_quant_e4m3", take_timer());
 }
 
 extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64_t cols,

@@ -370,19 +370,19 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
 int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
                  int64_t D, const int64_t* strides, int granularity, const int* layouts,
                  uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
-                 hipStream_t stream);
+                 hipStream_t stream, Timer tm);
 
 template <int D>
-static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s) {
+static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s, Timer tm) {
   const void* k = out_dtype == FLW_F32 ? reinterpret_cast<const void*>(&swa_fwd_kernel<D, float>)
                                        : reinterpret_cast<const void*>(&swa_fwd_kernel<D, uint16_t>);
-  launch_timed(k, grid, dim3(256), s, p);
+  launch_ext(k, grid, dim3(256), 0, s, p, tm.start, tm.stop);
 }
 
 static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, const int64_t* kst,
                    const uint8_t* vt, const float* qs, const float* ks, const float* vs, int gran,
                    void* out, int out_dtype, const int64_t* ost, int64_t B, int64_t H, int64_t T,
-                   int64_t D, int64_t window, hipStream_t stream) {
+                   int64_t D, int64_t window, hipStream_t stream, Timer tm) {
   FLW_REQUIRE(q8 && k8 && vt && qs && ks && vs && out && qst && kst && ost, FLW_E_INVALID, "null pointer argument");
   FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
   FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
@@ -411,9 +411,9 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.H = (int)H; p.T = (int)T; p.W = (int)W; p.nM = (int)nM;
   p.nwg = (int)(B * H * nM);
   dim3 grid((unsigned)p.nwg);
-  if (D == 32) launch_d<32>(p, out_dtype, grid, stream);
-  else if (D == 64) launch_d<64>(p, out_dtype, grid, stream);
-  else launch_d<128>(p, out_dtype, grid, stream);
+  if (D == 32) launch_d<32>(p, out_dtype, grid, stream, tm);
+  else if (D == 64) launch_d<64>(p, out_dtype, grid, stream, tm);
+  else launch_d<128>(p, out_dtype, grid, stream, tm);
   return check_launch("flw_fp8_swa_fwd");
 }
 
@@ -446,7 +446,8 @@ extern "C" int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, cons
                                const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
                                int64_t D, int64_t window, void* stream) {
   return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, granularity,
-                 out, out_dtype, out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream));
+                 out, out_dtype, out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream),
+                 take_timer());
 }
 
 extern "C" size_t flw_fp8_swa_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
@@ -475,10 +476,13 @@ extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const
   const int layouts[3] = {FLW_LAYOUT_BHTD, FLW_LAYOUT_BHTD, FLW_LAYOUT_VTILE};
   uint8_t* outs[3] = {q8, k8, vt};
   float* scs[3] = {sc, sc + G, sc + 2 * G};
+  // An armed timer brackets the whole operator: start with the first quantiser launch, stop with
+  // the attention kernel.
+  const Timer tm = take_timer();
   int rc = quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, scs,
-                        ws + w.partials, w.total - w.partials, s);
+                        ws + w.partials, w.total - w.partials, s, Timer{tm.start, nullptr});
   if (rc) return rc;
   const int64_t s8[3] = {H * T * D, T * D, D};
   return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, granularity, out, dtype, strides + 9,
-                 B, H, T, D, window, s);
+                 B, H, T, D, window, s, Timer{nullptr, tm.stop});
 }

@@ -52,9 +52,11 @@ const char* flw_last_error(void);
 int flw_abi_version(void);
 
 /* Measurement hook, no counterpart in the reference: arms two hipEvent_t (created with timing
- * enabled, passed as void*) on the calling thread. The next launch of the attention kernel or of
- * the FP8 GEMM on this thread records them from its own dispatch (hipExtLaunchKernel), so
- * hipEventElapsedTime(start, stop) is that kernel's duration alone. Both NULL disarms. */
+ * enabled, passed as void*) on the calling thread. The next call on this thread of an entry point
+ * that launches the quantisers, the attention kernel or the FP8 GEMM takes them: its first kernel
+ * records `start` and its last kernel records `stop` from their own dispatch timestamps
+ * (hipExtLaunchKernel), so hipEventElapsedTime(start, stop) spans exactly that call's kernels.
+ * Both NULL disarms. */
 int flw_time_next_launch(void* start_event, void* stop_event);
 
 /* ---------------------------------------------------------------- quantisation */

@@ -264,6 +264,44 @@ def test_qkv_entry_point_bit_exact(granularity, dtype):
         np.testing.assert_array_equal(got_sc[i * G:(i + 1) * G], want[i][1].reshape(-1).view(np.uint32))
 
 
+def test_timing_hook_brackets_one_entry_point_call():
+    """flw_time_next_launch: the quantiser pair records the armed events from its own dispatches
+    (start with the first kernel, stop with the last), computes the same codes, and disarms."""
+    L = lib()
+    lb = L.load()
+    B, H, T, D = 1, 2, 512, 64
+    xs = [make((B, H, T, D), torch.bfloat16, "randn", seed=s) for s in (1, 2, 3)]
+    outs = []
+    for timed in (False, True):
+        q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device="cuda")
+        k8 = torch.empty_like(q8)
+        vt = torch.empty(lb.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device="cuda")
+        sc = torch.empty(3 * H, dtype=torch.float32, device="cuda")
+        ws = L.workspace(3 * lb.flw_quant_workspace_bytes(B, H, T, D), "cuda")
+        strides = L.i64s(*xs[0].stride()[:3], *xs[1].stride()[:3], *xs[2].stride()[:3])
+        if timed:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            b.record()
+            torch.cuda.synchronize()
+            L.check(lb.flw_time_next_launch(a.cuda_event, b.cuda_event), "arm")
+        for _ in range(2):              # the second call runs untimed: the hook is consumed
+            L.check(lb.flw_quant_qkv_e4m3(xs[0].data_ptr(), xs[1].data_ptr(), xs[2].data_ptr(), L.BF16,
+                                          B, H, T, D, strides, L.SCALE_HEAD, q8.data_ptr(), k8.data_ptr(),
+                                          vt.data_ptr(), sc.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          L.stream_of(q8)), "qkv")
+        torch.cuda.synchronize()
+        outs.append(torch.cat([q8.view(-1), k8.view(-1), vt.view(-1), sc.view(torch.uint8)]))
+        if timed:
+            ms = a.elapsed_time(b)
+            assert 0.0 < ms < 1000.0, ms
+    assert torch.equal(outs[0], outs[1])
+    assert lb.flw_time_next_launch(None, None) == 0
+    x = torch.cuda.Event(enable_timing=True)
+    x.record()
+    assert lb.flw_time_next_launch(x.cuda_event, None) == 1      # both or neither
+
+
 # ------------------------------------------------------------------ _fake_quant_e4m3
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
