@@ -6,7 +6,8 @@
 // tensor / head / slice) itself -- no atomics, no zero-initialised buffer, no host sync -- then
 // quantises its chunk. Up to three tensors of one shape (Q, K, V) go through each pass in ONE
 // launch (grid.z = tensor), and every thread keeps kUnroll 16-byte loads in flight. The second
-// read of each tensor is largely served by the MI355X Infinity Cache (256 MB).
+// read of each tensor is partly served by the MI355X Infinity Cache (256 MB); pass 2 walks the
+// chunks in the reverse of pass 1's order to make the most of it.
 //
 // Rounding. The reference computes e4m3(clamp(x / s, -448, 448)) with an IEEE fp32 division
 // and round-to-nearest-even. For a scale group whose amax is finite, every |x / s| is at most
@@ -186,10 +187,14 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
   constexpr bool kBf16 = sizeof(T) == 2;
   __shared__ uint32_t red[kThreads / 64];
   extern __shared__ __align__(16) uint8_t tile_lds[];   // VTILE staging: kRowsPerChunk x D
-  const QTensor& t = p.t[blockIdx.z];
-  const int64_t slice = blockIdx.y;
+  // Blocks walk the tensors in the reverse of amax_kernel's order, so the first chunks quantised
+  // are the ones the amax pass read last and that are most likely still in the Infinity Cache.
+  const int zi = (int)(gridDim.z - 1 - blockIdx.z);
+  const int64_t slice = (int64_t)(gridDim.y - 1 - blockIdx.y);
+  const int64_t bx = (int64_t)(gridDim.x - 1 - blockIdx.x);
+  const QTensor& t = p.t[zi];
   const int64_t i0 = slice / p.d1, i1 = slice % p.d1;
-  const uint32_t* part = p.partials + (int64_t)blockIdx.z * p.d0 * p.d1 * p.nchunks;
+  const uint32_t* part = p.partials + (int64_t)zi * p.d0 * p.d1 * p.nchunks;
 
   const float amax = __uint_as_float(group_amax(p, part, slice, i1, red));
   float scale;
@@ -204,7 +209,7 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
   const bool fast = MODE == 0 && __builtin_isfinite(amax);   // uniform over the workgroup
   const float rcp = 1.0f / scale;                            // IEEE: correctly rounded
 
-  const int64_t r0 = (int64_t)blockIdx.x * kRowsPerChunk;
+  const int64_t r0 = bx * kRowsPerChunk;
   const int64_t r1 = min(p.d2, r0 + kRowsPerChunk);
   const bool vtile = MODE == 0 && t.layout == FLW_LAYOUT_VTILE;
   // VTILE: cover whole 64-row tiles, padding rows past T become code 0.

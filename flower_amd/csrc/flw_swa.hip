@@ -42,6 +42,7 @@ constexpr int kWaves = 4;
 constexpr int kBM = 32 * kWaves;   // queries per workgroup
 constexpr int kBN = 64;            // keys per tile
 constexpr int kStages = 3;         // LDS ring of K/V tiles
+constexpr int kBufferFlags = 0x00020000;   // buffer descriptor word 3 for raw dword access (gfx9)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLog2_448 = 8.807354922057604f;   // log2(448): P is produced pre-scaled by 448
 
@@ -169,23 +170,23 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   }
   uint4 kreg[CPT], vreg[CPT];
 
+  // K and V tiles through buffer descriptors of the (b, h) slice: the per-thread offset is fixed,
+  // the tile offset is a scalar, and K rows past T read as zero (they only meet queries past T,
+  // whose rows are not stored). The host checks that the slice fits a 31-bit extent.
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(kbase), 0, (int)((int64_t)(T - 1) * p.kst + D), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(vbase), 0, (int)p.vt_slice, kBufferFlags);
   auto load_tile = [&](int n0) __attribute__((always_inline)) {
-    const uint8_t* kt = kbase + (int64_t)n0 * p.kst;
-    const uint8_t* vtile = vbase + (int64_t)(n0 >> 6) * VT_BYTES;
-    const bool full = n0 + kBN <= T;
+    const int ks = n0 * (int)p.kst, vs = (n0 >> 6) * VT_BYTES;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int i = tid + 256 * j;
       if (KCH % 256 == 0 || i < KCH) {
-        if (full) {
-          kreg[j] = *reinterpret_cast<const uint4*>(kt + koff[j]);
-        } else {
-          // Rows past T repeat row T-1: such keys only meet queries past T (not stored).
-          const int kk = i / CPR, g = i % CPR;
-          const int row = min(n0 + kk, T - 1);
-          kreg[j] = *reinterpret_cast<const uint4*>(kbase + (int64_t)row * p.kst + 16 * g);
-        }
-        vreg[j] = *reinterpret_cast<const uint4*>(vtile + 16 * i);
+        const auto kv = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)koff[j], ks, 0);
+        const auto vv = __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * i, vs, 0);
+        kreg[j] = make_uint4(kv[0], kv[1], kv[2], kv[3]);
+        vreg[j] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
       }
     }
   };
@@ -396,6 +397,8 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   FLW_REQUIRE(((uintptr_t)q8 & 15) == 0 && ((uintptr_t)k8 & 15) == 0 && ((uintptr_t)vt & 15) == 0,
               FLW_E_INVALID, "q8 / k8 / v tiles must be 16-byte aligned");
   FLW_REQUIRE(((uintptr_t)out & 15) == 0, FLW_E_INVALID, "output must be 16-byte aligned");
+  FLW_REQUIRE((T - 1) * kst[2] + D < ((int64_t)1 << 31) && (T + 63) / 64 * 64 * D < ((int64_t)1 << 31),
+              FLW_E_UNSUPPORTED, "one (b, h) slice of k8 / v tiles must span < 2^31 bytes");
   const int64_t nM = (T + kBM - 1) / kBM;
   FLW_REQUIRE(B * H * nM <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
   int64_t W = window;

@@ -264,6 +264,67 @@ def test_qkv_entry_point_bit_exact(granularity, dtype):
         np.testing.assert_array_equal(got_sc[i * G:(i + 1) * G], want[i][1].reshape(-1).view(np.uint32))
 
 
+def run_qkv(xs, granularity):
+    """flw_quant_qkv_e4m3 on the three tensors; returns (q8, k8, vtiles, scales)."""
+    L = lib()
+    lb = L.load()
+    B, H, T, D = xs[0].shape
+    G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+    q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device="cuda")
+    k8 = torch.empty_like(q8)
+    vt = torch.empty(lb.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(3 * G, dtype=torch.float32, device="cuda")
+    ws = L.workspace(3 * lb.flw_quant_workspace_bytes(B, H, T, D), "cuda")
+    strides = L.i64s(*xs[0].stride()[:3], *xs[1].stride()[:3], *xs[2].stride()[:3])
+    L.check(lb.flw_quant_qkv_e4m3(xs[0].data_ptr(), xs[1].data_ptr(), xs[2].data_ptr(),
+                                  L.dtype_code(xs[0].dtype), B, H, T, D, strides,
+                                  L.GRANULARITY[granularity], q8.data_ptr(), k8.data_ptr(),
+                                  vt.data_ptr(), sc.data_ptr(), ws.data_ptr(), ws.numel(),
+                                  L.stream_of(q8)), "qkv")
+    torch.cuda.synchronize()
+    return q8, k8, vt, sc
+
+
+def check_qkv_against_oracle(xs, granularity, got):
+    q8, k8, vt, sc = got
+    G = sc.numel() // 3
+    want = [per_tensor_fp8(to_np(x), granularity) for x in xs]
+    np.testing.assert_array_equal(q8.cpu().numpy(), want[0][0])
+    np.testing.assert_array_equal(k8.cpu().numpy(), want[1][0])
+    np.testing.assert_array_equal(vt.cpu().numpy(), vtile_permute(want[2][0]))
+    got_sc = to_np(sc).view(np.uint32)
+    for i in range(3):
+        np.testing.assert_array_equal(got_sc[i * G:(i + 1) * G], want[i][1].reshape(-1).view(np.uint32))
+
+
+def test_qkv_large_shape_repeated():
+    """A 21 M-element-per-tensor call (2 x 4 x 40960 x 64, per head) against the oracle, then five
+    more calls that must give the same bytes."""
+    shape = (2, 4, 40960, 64)
+    xs = [make(shape, torch.bfloat16, "lognormal_heads", seed=s) for s in (21, 22, 23)]
+    first = run_qkv(xs, "head")
+    check_qkv_against_oracle(xs, "head", first)
+    ref = torch.cat([t.view(torch.uint8).reshape(-1) for t in first])
+    for _ in range(5):
+        again = run_qkv(xs, "head")
+        assert torch.equal(torch.cat([t.view(torch.uint8).reshape(-1) for t in again]), ref)
+
+
+def test_qkv_nan_group_and_strided_views():
+    """A NaN in one head makes that head's scale and codes NaN exactly as the reference does; the
+    inputs are the strided head views of a packed qkv projection (read in place)."""
+    B, T, H, D = 2, 512, 4, 64
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(B, T, 3 * H * D, generator=g).to(torch.bfloat16)
+    qkv[1, 17, H * D + 2 * D + 5] = float("nan")            # K, head 2
+    qkv = qkv.cuda()
+    xs = [t.view(B, T, H, D).transpose(1, 2) for t in qkv.chunk(3, dim=-1)]
+    assert not xs[0].is_contiguous()
+    got = run_qkv(xs, "head")
+    check_qkv_against_oracle(xs, "head", got)
+    assert np.isnan(to_np(got[3])[H + 2]) and not np.isnan(to_np(got[3])[H + 1])
+
+
 def test_timing_hook_brackets_one_entry_point_call():
     """flw_time_next_launch: the quantiser pair records the armed events from its own dispatches
     (start with the first kernel, stop with the last), computes the same codes, and disarms."""
