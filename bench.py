@@ -24,7 +24,9 @@ Printed (one JSON line):
 
 --workload c2 measures the FP8 weight-cache linear of BASELINE.json config 2 instead (bf16
 x[8192, 1024] with 0.1 % outliers at 20x, cached e4m3 weight [4096, 1024] with per-output-channel
-scales; one step = per-row activation quantisation + the scaled FP8 GEMM), in GEMM TFLOP/s.
+scales): the headline is the weight-only GEMM (e4m3 weight x bf16 activations on bf16 MFMA, one
+kernel per step); the A8W8 recipe (per-row activation quantisation + FP8 GEMM) is reported
+beside it, in GEMM TFLOP/s.
 Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
 """
 
@@ -44,6 +46,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "FP8 SWA attn fwd TFLOPS + % FP8 MFMA peak at T=8192,W=1024; quant GB/s"
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E
 COPY_PROBE_BYTES = 256 << 20
 
@@ -67,7 +70,7 @@ DATA = {
 # 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0).
 TRAFFIC = {
     "c3": {"swa_fwd": 167_979_008, "quant": 503_929_856},
-    "c2": {"gemm": 120_440_320},
+    "c2": {"gemm": 120_440_320, "w8a16": 136_010_752},
 }
 
 
@@ -261,6 +264,40 @@ def bench_gemm(cfg, steps, warmup):
                 x=x, w=w)
 
 
+def bench_gemm_w8a16(cfg, steps, warmup):
+    """BASELINE config 2, weight-only: the cached per-channel e4m3 weight times the bf16
+    activations as they are (flw_fp8_linear, FLW_GEMM_W8A16: one kernel per step)."""
+    from flower_amd import _lib
+    lib = _lib.load()
+    x, w = (t.cuda() for t in make_gemm_inputs(cfg))
+    M, N, K = cfg["M"], cfg["N"], cfg["K"]
+    stream = torch.cuda.current_stream().cuda_stream
+    w8 = torch.empty((N, K), dtype=torch.uint8, device="cuda")
+    ws_ = torch.empty(N, dtype=torch.float32, device="cuda")
+    _lib.check(lib.flw_quant_rows_e4m3(w.data_ptr(), _lib.BF16, N, K, K, w8.data_ptr(), ws_.data_ptr(), stream), "w")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+
+    def gemm():
+        _lib.check(lib.flw_fp8_linear(x.data_ptr(), M, K, K, w8.data_ptr(), N, ws_.data_ptr(), N,
+                                      _lib.GEMM_W8A16, y.data_ptr(), N, None, 0, stream), "w8a16")
+
+    _spin_up(gemm)
+    for _ in range(warmup):
+        gemm()
+    kev = _events(steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        _arm(lib, kev[i])
+        gemm()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    g_ms = np.array([e[0].elapsed_time(e[1]) for e in kev])
+    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, gemm_ms=float(g_ms.mean()),
+                gemm_ms_min=float(g_ms.min()), flops=2 * M * N * K,
+                gemm_bytes=2 * M * K + N * K + 2 * M * N + 4 * N, x=x, w=w)
+
+
 def cpu_baseline(cfg, budget_s=20.0):
     """Oracle of the FP8-simulated reference path on the host: e4m3 quantise, dequantise, banded
     fp32 attention, head by head (all B of each) until the time budget, scaled linearly."""
@@ -295,11 +332,12 @@ def cpu_baseline(cfg, budget_s=20.0):
                       f"attention (numpy / multithreaded BLAS), FLOPs counted as in-window 4*D per pair"}
 
 
-def cpu_baseline_gemm(x, w, budget_s=15.0):
-    """The oracle's _fp8_head recipe on the host: per-row e4m3 of x and W, closed-form GEMM,
-    on row blocks of x until the time budget."""
+def cpu_baseline_gemm(x, w, budget_s=15.0, weight_only=False):
+    """The oracle on the host: per-row e4m3 of W (once, outside the timing, as the weight cache
+    does), then per row block of x either the _fp8_head recipe (per-row e4m3 of x, closed-form
+    scaled GEMM) or the weight-only product, until the time budget."""
     from threadpoolctl import threadpool_limits
-    from oracle.gemm import fp8_linear_a8w8
+    from oracle.gemm import fp8_linear_a8w8, fp8_linear_w8a16
     from oracle.quant import rowwise_fp8
     cores = min(16, os.cpu_count() or 1)
     xf, wf = x.float().cpu().numpy(), w.float().cpu().numpy()
@@ -308,16 +346,20 @@ def cpu_baseline_gemm(x, w, budget_s=15.0):
     with threadpool_limits(cores):
         for r0 in range(0, xf.shape[0], 512):
             t0 = time.perf_counter()
-            fp8_linear_a8w8(xf[r0:r0 + 512], w8, sw.reshape(-1))
+            if weight_only:
+                fp8_linear_w8a16(xf[r0:r0 + 512], w8, sw.reshape(-1))
+            else:
+                fp8_linear_a8w8(xf[r0:r0 + 512], w8, sw.reshape(-1))
             t_total += time.perf_counter() - t0
             rows += min(512, xf.shape[0] - r0)
             if t_total > budget_s:
                 break
     flops = 2 * rows * wf.shape[0] * wf.shape[1]
     return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{rows} of {xf.shape[0]} activation rows in {t_total:.1f} s: oracle per-row e4m3 "
-                      f"quantisation + float64 closed-form scaled GEMM (numpy / BLAS); weight "
-                      f"quantised once outside the timing, as the weight cache does"}
+            "sample": f"{rows} of {xf.shape[0]} activation rows in {t_total:.1f} s: oracle " +
+                      ("weight-only product (float64 x @ dequant(w8)^T, numpy / BLAS)" if weight_only else
+                       "per-row e4m3 quantisation + float64 closed-form scaled GEMM (numpy / BLAS)") +
+                      "; weight quantised once outside the timing, as the weight cache does"}
 
 
 def main():
@@ -392,11 +434,15 @@ def run_attention(cfg, args):
 
 
 def run_gemm(cfg, args):
-    r = bench_gemm(cfg, args.steps, args.warmup)
+    """BASELINE config 2. Headline: the weight-only FP8 linear (e4m3 cached weight x bf16
+    activations, bf16 MFMA); alongside: the A8W8 recipe (per-row e4m3 activations, FP8 MFMA)."""
+    r = bench_gemm_w8a16(cfg, args.steps, args.warmup)
     value = r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12
     g_tflops = r["flops"] / (r["gemm_ms"] * 1e-3) / 1e12
+    a = bench_gemm(cfg, args.steps, args.warmup)
+    a_tflops = a["flops"] / (a["gemm_ms"] * 1e-3) / 1e12
     line = {
-        "metric": "FP8 weight-cache linear (per-row x per-channel e4m3) TFLOPS, BASELINE config 2",
+        "metric": "FP8 weight-cache linear TFLOPS (e4m3 per-channel weight x bf16 activations), BASELINE config 2",
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -406,21 +452,28 @@ def run_gemm(cfg, args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8_e4m3 (fp32 accumulate)",
+        "dtype": "bf16 MFMA (e4m3 weight widened exactly to bf16), fp32 accumulate",
         "data": DATA["c2"],
-        "config": {"workload": "fp8 linear from the weight cache, BASELINE C2", "M": cfg["M"],
-                   "N": cfg["N"], "K": cfg["K"], "scales": "per-row x per-output-channel"},
-        "roofline": {"bound": "mfma", "achieved": round(g_tflops, 2), "peak": FP8_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(g_tflops / FP8_PEAK_TFLOPS, 4),
-                     "traffic": TRAFFIC["c2"]["gemm"], "algorithmic_bytes": r["gemm_bytes"],
-                     "kernel": "fp8_gemm_256_kernel", "kernel_ms": round(r["gemm_ms"], 4),
+        "config": {"workload": "fp8 weight-only linear from the weight cache, BASELINE C2", "M": cfg["M"],
+                   "N": cfg["N"], "K": cfg["K"], "scales": "per-output-channel weight"},
+        "roofline": {"bound": "mfma", "achieved": round(g_tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(g_tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": TRAFFIC["c2"].get("w8a16"), "algorithmic_bytes": r["gemm_bytes"],
+                     "kernel": "w8a16_gemm_kernel", "kernel_ms": round(r["gemm_ms"], 4),
                      "kernel_ms_min": round(r["gemm_ms_min"], 4), "flop_per_launch": r["flops"]},
-        "quant": {"bound": "hbm", "achieved": round(r["quant_bytes"] / (r["quant_ms"] * 1e-3) / 1e9, 1),
-                  "peak": HBM_PEAK_GBPS, "unit": "GB/s", "ms": round(r["quant_ms"], 4),
-                  "algorithmic_bytes": r["quant_bytes"]},
+        "a8w8": {"value": round(a["flops"] / (a["ms_per_step"] * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+                 "ms_per_step": round(a["ms_per_step"], 4),
+                 "roofline": {"bound": "mfma", "achieved": round(a_tflops, 2), "peak": FP8_PEAK_TFLOPS,
+                              "unit": "TFLOP/s", "frac": round(a_tflops / FP8_PEAK_TFLOPS, 4),
+                              "traffic": TRAFFIC["c2"]["gemm"], "algorithmic_bytes": a["gemm_bytes"],
+                              "kernel": "fp8_gemm_256_kernel", "kernel_ms": round(a["gemm_ms"], 4),
+                              "kernel_ms_min": round(a["gemm_ms_min"], 4)},
+                 "quant": {"bound": "hbm", "achieved": round(a["quant_bytes"] / (a["quant_ms"] * 1e-3) / 1e9, 1),
+                           "peak": HBM_PEAK_GBPS, "unit": "GB/s", "ms": round(a["quant_ms"], 4),
+                           "algorithmic_bytes": a["quant_bytes"]}},
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_gemm(r["x"], r["w"])
+        line["cpu_baseline"] = cpu_baseline_gemm(r["x"], r["w"], weight_only=True)
     return line
 
 

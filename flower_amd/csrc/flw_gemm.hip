@@ -338,6 +338,190 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
   }
 }
 
+// ---------------------------------------------------------------- W8A16: e4m3 weights x bf16 activations
+//
+// y[M, N] (bf16) = (x[M, K] . w8[N, K]^T) * sw[n] with x in bf16, unquantised. The weight codes are
+// widened to bf16 in registers (v_cvt_scalef32_pk_bf16_fp8, exact: every e4m3 value is a bf16
+// value) and the product runs on v_mfma_f32_32x32x16_bf16 (bf16 dense peak 2.5 PFLOP/s). Same
+// persistent 256 x 256 tiles, wave grid, XCD / group-M tile order and direct-to-LDS staging as
+// the FP8 kernel; a stage is 64 deep in K: a 256 x 128-byte X tile (bf16) and a 256 x 64-byte W
+// tile (e4m3), 48 KB, two stages.
+//
+// K order inside a stage. An MFMA only needs A and B to agree on which K each lane holds, so
+// k-step ks (16 deep) gives lane half h the K values 32 h + 8 ks .. +7: a lane then reads its W
+// row's 32 contiguous bytes once (two ds_read_b128) for all four k-steps, and its X row's 16
+// bytes at K offset 32 h + 8 ks (one ds_read_b128 per k-step).
+//
+// LDS layouts: X as the FP8 kernel's swizzled 128-byte rows (swz_off); W as 64-byte rows with
+// 16-byte chunk c of row r at position c ^ ((r >> 2) & 3), so that the eight rows one
+// ds_read_b128 phase touches fall in eight distinct bank groups.
+constexpr int kWK = 64;                           // K per stage
+constexpr int kWXBytes = 256 * 128;               // X tile per stage (32 KB)
+constexpr int kWWBytes = 256 * 64;                // W tile per stage (16 KB)
+constexpr int kWStageBytes = kWXBytes + kWWBytes;
+
+typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
+
+struct W8A16Params {
+  const uint16_t* x;   // [M, K] bf16, row stride xs
+  int64_t xs;
+  const uint8_t* w8;   // [N, K] e4m3
+  const float* sw;     // N or 1
+  int sw_step;
+  uint16_t* y;         // [M, N] bf16
+  int64_t ys;
+  int M, N, K;
+  int tiles_n, tiles_m;
+};
+
+__device__ __forceinline__ int wswz_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
+
+__device__ __forceinline__ v8bf_t bf16_frag(uint4 q) {
+  return __builtin_bit_cast(v8bf_t, q);
+}
+
+// Eight e4m3 codes (two words) widened to eight bf16 values.
+__device__ __forceinline__ v8bf_t widen8(uint32_t lo, uint32_t hi) {
+  const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)lo, 1.0f, false);
+  const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)lo, 1.0f, true);
+  const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)hi, 1.0f, false);
+  const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)hi, 1.0f, true);
+  return v8bf_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, uint8_t* st1, int m0,
+                                           int n0, int wave, int lane) {
+  const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
+  // Direct-to-LDS loads: wave w fills X rows 32 w .. 32 w + 31 (four instructions of 8 rows x
+  // 128 bytes) and W rows 32 w .. 32 w + 31 (two instructions of 16 rows x 64 bytes).
+  uint32_t xoff[4], woff[2];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int r = 32 * wave + 8 * t + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int grow = min(m0 + r, p.M - 1);
+    xoff[t] = (uint32_t)grow * (uint32_t)(p.xs * 2) + 16u * (uint32_t)c;
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int r = 32 * wave + 16 * t + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    const int grow = min(n0 + r, p.N - 1);
+    woff[t] = (uint32_t)grow * (uint32_t)p.K + 16u * (uint32_t)c;
+  }
+  auto issue = [&](uint8_t* stage, int s) __attribute__((always_inline)) {
+    const uint32_t kx = (uint32_t)s * kWK * 2, kw = (uint32_t)s * kWK;
+    const uint32_t lx = (uint32_t)(uintptr_t)(lds_u8_t*)(stage + 32 * wave * 128);
+    const uint32_t lw = (uint32_t)(uintptr_t)(lds_u8_t*)(stage + kWXBytes + 32 * wave * 64);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :: "s"(lx + t * 1024), "v"(xoff[t] + kx), "s"(p.x) : "memory", "m0");
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :: "s"(lw + t * 1024), "v"(woff[t] + kw), "s"(p.w8) : "memory", "m0");
+  };
+
+  v16f acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+  const int nst = p.K / kWK;
+  const int h = lane >> 5;
+  issue(st0, 0);
+  auto step = [&](int s, const uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+    if (s + 1 < nst) {
+      issue(nxt, s + 1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(6));   // this wave's loads of stage s landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    lds_barrier();                                // ... and every wave's
+    // X fragments for both m blocks and all four k-steps: chunk 4 h + ks of row 32 (2 wm + j) + lane % 32.
+    v8bf_t b[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 32 * (2 * wm + j) + (lane & 31);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        b[j][ks] = bf16_frag(*reinterpret_cast<const uint4*>(cur + swz_off(r, 4 * h + ks)));
+    }
+    const uint8_t* wt = cur + kWXBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 32 * (4 * wn + i) + (lane & 31);
+      const uint4 q0 = *reinterpret_cast<const uint4*>(wt + wswz_off(r, 2 * h));
+      const uint4 q1 = *reinterpret_cast<const uint4*>(wt + wswz_off(r, 2 * h + 1));
+      const v8bf_t a[4] = {widen8(q0.x, q0.y), widen8(q0.z, q0.w), widen8(q1.x, q1.y), widen8(q1.z, q1.w)};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], b[j][ks], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): reads of `cur` done
+    lds_barrier();
+  };
+  for (int s = 0; s < nst; s += 2) {
+    step(s, st0, st1);
+    if (s + 1 < nst) step(s + 1, st1, st0);
+  }
+
+  // Epilogue: lane owns m = m0 + 64 wm + 32 j + lane % 32, n = n0 + 128 wn + 32 i + 8 g + 4 h + 0..3
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float swn[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = min(n0 + 128 * wn + 32 * i + 8 * g + 4 * h, p.N - 4);
+      if (p.sw_step) {
+        const float4 v = *reinterpret_cast<const float4*>(p.sw + n);
+        swn[4 * g] = v.x; swn[4 * g + 1] = v.y; swn[4 * g + 2] = v.z; swn[4 * g + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) swn[4 * g + e] = p.sw[0];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = m0 + 64 * wm + 32 * j + (lane & 31);
+      if (m >= p.M) continue;
+      uint16_t* yrow = p.y + (int64_t)m * p.ys;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + 128 * wn + 32 * i + 8 * g + 4 * h;
+        if (n >= p.N) continue;      // N % 4 == 0 is required on the host
+        const v16f& c = acc[i][j];
+        uint2 w;
+        w.x = pack_bf16x2(c[4 * g] * swn[4 * g], c[4 * g + 1] * swn[4 * g + 1]);
+        w.y = pack_bf16x2(c[4 * g + 2] * swn[4 * g + 2], c[4 * g + 3] * swn[4 * g + 3]);
+        *reinterpret_cast<uint2*>(yrow + n) = w;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kFThreads, 1) void w8a16_gemm_kernel(W8A16Params p) {
+  __shared__ __align__(16) uint8_t st0[kWStageBytes];
+  __shared__ __align__(16) uint8_t st1[kWStageBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x;
+  const int L = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int ntiles = p.tiles_n * p.tiles_m;
+  for (int t = L; t < ntiles; t += G) {
+    const int group = t / (kGroupM * p.tiles_n);
+    const int first_m = group * kGroupM;
+    const int gm = min(p.tiles_m - first_m, kGroupM);
+    const int tm = first_m + (t % (kGroupM * p.tiles_n)) % gm;
+    const int tn = (t % (kGroupM * p.tiles_n)) / gm;
+    w8a16_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane);
+  }
+}
+
 // Compute units of the current device (queried once per device).
 static int compute_units() {
   static int cache[64] = {0};
@@ -385,6 +569,31 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
   return check_launch("flw_fp8_scaled_mm");
 }
 
+static int w8a16_mm(const uint16_t* x, int64_t M, int64_t K, int64_t xs, const uint8_t* w8, int64_t N,
+                    const float* sw, int64_t sw_count, void* y, int64_t ys, hipStream_t s) {
+  FLW_REQUIRE(x && w8 && sw && y, FLW_E_INVALID, "null pointer argument");
+  FLW_REQUIRE(M > 0 && N > 0 && K > 0, FLW_E_INVALID, "empty GEMM");
+  FLW_REQUIRE(K % kWK == 0, FLW_E_UNSUPPORTED, "W8A16 needs K a multiple of %d, got %lld", kWK, (long long)K);
+  FLW_REQUIRE(N % 4 == 0 && ys % 4 == 0 && ys >= N, FLW_E_INVALID, "N and the output row stride must be multiples of 4");
+  FLW_REQUIRE(xs >= K && xs % 8 == 0, FLW_E_INVALID, "x row stride must be >= K and a multiple of 8 elements");
+  FLW_REQUIRE(sw_count == 1 || sw_count == N, FLW_E_INVALID, "w_scale count must be 1 or N");
+  FLW_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w8 & 15) == 0 && ((uintptr_t)y & 7) == 0 &&
+              (sw_count == 1 || ((uintptr_t)sw & 15) == 0),
+              FLW_E_INVALID, "x / w8 must be 16-byte aligned, y 8-byte aligned, per-channel scales 16-byte aligned");
+  FLW_REQUIRE(M * xs * 2 < (1ll << 32) && N * K < (1ll << 32), FLW_E_UNSUPPORTED, "operand too large for 32-bit offsets");
+  W8A16Params p{};
+  p.x = x; p.xs = xs; p.w8 = w8; p.sw = sw; p.sw_step = sw_count == 1 ? 0 : 1;
+  p.y = static_cast<uint16_t*>(y); p.ys = ys;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.tiles_n = (int)((N + kFBN - 1) / kFBN);
+  p.tiles_m = (int)((M + kFBM - 1) / kFBM);
+  const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
+  FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
+  const int64_t grid = tiles < compute_units() ? tiles : compute_units();
+  launch_timed(reinterpret_cast<const void*>(&w8a16_gemm_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
+  return check_launch("flw_fp8_linear (W8A16)");
+}
+
 static size_t galign(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace flw
@@ -408,7 +617,10 @@ extern "C" int flw_fp8_linear(const void* x, int64_t M, int64_t K, int64_t x_row
                               const uint8_t* w8, int64_t N, const float* w_scale,
                               int64_t w_scale_count, int mode, void* y, int64_t y_row_stride,
                               void* workspace, size_t workspace_bytes, void* stream) {
-  FLW_REQUIRE(mode == FLW_GEMM_A8W8, FLW_E_UNSUPPORTED, "GEMM mode %d is not implemented in this build", mode);
+  FLW_REQUIRE(mode == FLW_GEMM_A8W8 || mode == FLW_GEMM_W8A16, FLW_E_INVALID, "unknown GEMM mode %d", mode);
+  if (mode == FLW_GEMM_W8A16)
+    return w8a16_mm(static_cast<const uint16_t*>(x), M, K, x_row_stride, w8, N, w_scale, w_scale_count, y,
+                    y_row_stride, static_cast<hipStream_t>(stream));
   const size_t need = flw_fp8_linear_workspace_bytes(M, K, mode);
   FLW_REQUIRE(workspace != nullptr && workspace_bytes >= need, FLW_E_WORKSPACE, "workspace needs %zu bytes", need);
   uint8_t* x8 = static_cast<uint8_t*>(workspace);

@@ -7,7 +7,9 @@ Mirrors flower/precision.py (the torchao-based FP8 conversion) with this build's
 ``Fp8Linear``          -- replaces torchao ``Float8Linear``: forward is the HIP FP8 GEMM
     (e4m3 weight x e4m3 per-row activation, fp32 accumulate, bf16 out, the ``_fp8_head``
     recipe of base.py:911-923). recipe "rowwise": per-output-channel weight scales, per-row
-    activation scales; "tensorwise": one weight scale and one activation scale.
+    activation scales; "tensorwise": one weight scale and one activation scale; "weight_only":
+    per-output-channel e4m3 weights times the bf16 activations as they are (W8A16: the weight is
+    widened to bf16 in the kernel, bf16 MFMA; needs K % 64 == 0).
     Backward (not on the FP8 path) is the bf16 matmul pair grad_x = g W, grad_W = g^T x.
 ``convert_model_to_fp8`` / ``maybe_convert_fp8`` -- precision.py:134-195, 356-381.
 ``fp8_weight_cache``   -- precision.py:198-353: quantise every FP8 weight ONCE on entry, patch
@@ -24,7 +26,7 @@ import torch.nn as nn
 from . import _lib
 
 _FP8_DIM_ALIGNMENT = 16
-RECIPES = ("rowwise", "tensorwise")
+RECIPES = ("rowwise", "tensorwise", "weight_only")
 
 
 def _block_index(fqn: str) -> int | None:
@@ -66,7 +68,7 @@ def quantize_weight(weight: torch.Tensor, recipe: str = "rowwise"):
     w = w.contiguous()
     N, K = w.shape
     w8 = torch.empty((N, K), dtype=torch.uint8, device=w.device)
-    if recipe == "rowwise":
+    if recipe in ("rowwise", "weight_only"):
         scale = torch.empty(N, dtype=torch.float32, device=w.device)
         rc = lib.flw_quant_rows_e4m3(w.data_ptr(), _lib.dtype_code(w.dtype), N, K, K, w8.data_ptr(),
                                      scale.data_ptr(), _lib.stream_of(w))
@@ -100,7 +102,11 @@ def fp8_linear_forward(x: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor,
     if M == 0:
         return y.reshape(*lead, N)
     stream = _lib.stream_of(x2)
-    if recipe == "rowwise":
+    if recipe == "weight_only":
+        rc = lib.flw_fp8_linear(x2.data_ptr(), M, K, x2.stride(0), w8.data_ptr(), N, w_scale.data_ptr(),
+                                w_scale.numel(), _lib.GEMM_W8A16, y.data_ptr(), N, None, 0, stream)
+        _lib.check(rc, "fp8_linear(weight_only)")
+    elif recipe == "rowwise":
         ws = _lib.workspace(lib.flw_fp8_linear_workspace_bytes(M, K, _lib.GEMM_A8W8), x.device)
         rc = lib.flw_fp8_linear(x2.data_ptr(), M, K, x2.stride(0), w8.data_ptr(), N, w_scale.data_ptr(),
                                 w_scale.numel(), _lib.GEMM_A8W8, y.data_ptr(), N, ws.data_ptr(),

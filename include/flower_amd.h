@@ -133,14 +133,17 @@ int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, i
 
 /* ---------------------------------------------------------------- GEMM */
 
-/* Workspace of flw_fp8_linear (the per-row e4m3 activations and their scales in A8W8 mode). */
+/* Workspace of flw_fp8_linear (the per-row e4m3 activations and their scales in A8W8 mode; 0
+ * bytes in W8A16 mode). */
 size_t flw_fp8_linear_workspace_bytes(int64_t M, int64_t K, int mode);
 
 /* y[M, N] (bf16) = x[M, K] (bf16) @ dequant(w8[N, K])^T, replacing the FP8 GEMM of
  * torchao Float8Linear / `torch._scaled_mm` (flower/models/base.py:919-923,
  * flower/precision.py:304-324). w_scale: N floats (per output channel) or 1 float
- * (w_scale_count = 1, per tensor). A8W8 quantises x per row (flw_quant_rows_e4m3 semantics)
- * into the workspace first. Requires K % 64 == 0, N % 16 == 0. */
+ * (w_scale_count = 1, per tensor). FLW_GEMM_A8W8 quantises x per row (flw_quant_rows_e4m3
+ * semantics) into the workspace first, then FP8 x FP8 MFMA (K % 16 == 0). FLW_GEMM_W8A16 keeps x
+ * in bf16, widens the e4m3 weight to bf16 in the kernel (exact) and multiplies on bf16 MFMA: no
+ * workspace, K % 64 == 0, x rows 16-byte aligned. N % 4 == 0 in both modes. */
 int flw_fp8_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride, const uint8_t* w8,
                    int64_t N, const float* w_scale, int64_t w_scale_count, int mode, void* y,
                    int64_t y_row_stride, void* workspace, size_t workspace_bytes, void* stream);

@@ -51,8 +51,10 @@ def test_host_only_calls_work_without_a_gpu():
     s = _lib.i64s(0, 0, 0)
     rc = lib.flw_fp8_swa_fwd(16, s, 16, s, 16, 16, 16, 16, 0, 16, 1, s, 1, 1, 64, 96, 16, None)
     assert rc == 2 and b"head_dim" in lib.flw_last_error()
-    rc = lib.flw_fp8_linear(16, 8, 64, 64, 16, 16, 16, 16, 1, 16, 16, 16, 1 << 20, None)
-    assert rc == 2 and b"not implemented" in lib.flw_last_error()
+    rc = lib.flw_fp8_linear(16, 8, 64, 64, 16, 16, 16, 16, 7, 16, 16, 16, 1 << 20, None)
+    assert rc == 1 and b"unknown GEMM mode" in lib.flw_last_error()
+    rc = lib.flw_fp8_linear(16, 8, 80, 80, 16, 16, 16, 16, 1, 16, 16, None, 0, None)   # W8A16
+    assert rc == 2 and b"multiple of 64" in lib.flw_last_error()
 
 
 def test_operators_refuse_cpu_tensors():

@@ -76,6 +76,61 @@ def test_config2_fp8_linear_full_size():
     assert rel < 0.05 and 0.9 < np.linalg.norm(y[rows]) / np.linalg.norm(full) < 1.1, rel
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 256, 512), (100, 36, 64), (257, 132, 1024), (1, 16, 64),
+                                   (513, 260, 1088), (256, 512, 384)])
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_w8a16_matches_closed_form(M, N, K, per_channel):
+    """FLW_GEMM_W8A16: bf16 activations (with x20 outliers) times widened e4m3 weights, against
+    the float64 closed form on the same values; a strided x (row stride K + 64) as well."""
+    from flower_amd import _lib as L
+    from oracle.gemm import fp8_linear_w8a16
+    lb = L.load()
+    w8 = codes((N, K), 4)
+    g = torch.Generator().manual_seed(5)
+    xs = K + 64
+    xbuf = (torch.randn(M, xs, generator=g) * 2).to(torch.bfloat16)
+    xbuf.view(-1)[::997] *= 20
+    x = xbuf[:, :K]
+    sw = np.random.default_rng(6).uniform(0.001, 0.01, N if per_channel else 1).astype(np.float32)
+    tw8, tsw, tx = torch.from_numpy(w8).cuda(), torch.from_numpy(sw).cuda(), xbuf.cuda()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    L.check(lb.flw_fp8_linear(tx.data_ptr(), M, K, xs, tw8.data_ptr(), N, tsw.data_ptr(), sw.size,
+                              L.GEMM_W8A16, y.data_ptr(), N, None, 0, L.stream_of(y)), "w8a16")
+    ref = fp8_linear_w8a16(x.float().numpy(), w8, np.broadcast_to(sw, (N,)))
+    assert_gemm_close(to_np(y), ref)
+
+
+def test_w8a16_rejects_unsupported_k():
+    from flower_amd import _lib as L
+    lb = L.load()
+    t = torch.empty(4096, dtype=torch.uint8, device="cuda")
+    rc = lb.flw_fp8_linear(t.data_ptr(), 16, 80, 80, t.data_ptr(), 16, t.data_ptr(), 1, L.GEMM_W8A16,
+                           t.data_ptr(), 16, None, 0, None)
+    assert rc == 2 and b"multiple of 64" in lb.flw_last_error()
+
+
+def test_config2_weight_only_full_size():
+    """BASELINE config 2 in weight-only mode: the cached per-channel e4m3 weight times the bf16
+    activations with their outliers, sampled rows against the closed form and the unquantised
+    product within the reference's FP8-head bounds."""
+    from flower_amd.precision import fp8_linear_forward, quantize_weight
+    from oracle.gemm import fp8_linear_w8a16
+    g = torch.Generator().manual_seed(7)
+    W = (torch.randn(4096, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    X = torch.randn(8192, 1024, generator=g)
+    idx = torch.randperm(X.numel(), generator=g)[: X.numel() // 1000]
+    X.view(-1)[idx] *= 20
+    X = X.to(torch.bfloat16)
+    w8, ws = quantize_weight(W.cuda(), "weight_only")
+    y = to_np(fp8_linear_forward(X.cuda(), w8, ws, "weight_only"))
+    rows = np.random.default_rng(1).choice(8192, 256, replace=False)
+    ref = fp8_linear_w8a16(X.float().numpy()[rows], to_np(w8), to_np(ws))
+    assert_gemm_close(y[rows], ref)
+    full = X.float().numpy()[rows] @ W.float().numpy().T
+    rel = np.linalg.norm(y[rows] - full) / np.linalg.norm(full)
+    assert rel < 0.05 and 0.9 < np.linalg.norm(y[rows]) / np.linalg.norm(full) < 1.1, rel
+
+
 def test_fp8_linear_module_matches_bf16_linear_and_backprops():
     from flower_amd.precision import Fp8Linear
     torch.manual_seed(0)
@@ -100,7 +155,7 @@ def _fp8_model(d: int = 256, hid: int = 512) -> nn.Module:
     return nn.Sequential(*(Fp8Linear.from_linear(l) for l in m))
 
 
-@pytest.mark.parametrize("recipe", ["rowwise", "tensorwise"])
+@pytest.mark.parametrize("recipe", ["rowwise", "tensorwise", "weight_only"])
 def test_cached_is_bit_identical_to_uncached(recipe):
     from flower_amd.precision import fp8_weight_cache
     accum = 3
