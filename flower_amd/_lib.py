@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_int, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
 
 import torch
 
@@ -41,6 +41,10 @@ SIGNATURES = {
                                     c_void_p]),
     "flw_quant_rows_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                     c_void_p]),
+    "flw_rmsnorm_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p,
+                                            c_void_p, c_void_p, c_void_p]),
+    "flw_gelu_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                                         c_void_p]),
     "flw_fp8_swa_fwd": (c_int, [c_void_p, _P64, c_void_p, _P64, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_int, c_void_p, c_int, _P64, c_int64, c_int64, c_int64, c_int64,
                                 c_int64, c_void_p]),
@@ -53,6 +57,8 @@ SIGNATURES = {
                                c_int64, c_int, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     "flw_fp8_scaled_mm": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
+    "flw_fp8_scaled_mm_residual": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                           c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "flw_diag_cvt_e4m3": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "flw_diag_quotient": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p]),
 }

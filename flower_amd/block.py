@@ -11,8 +11,11 @@ Layout and parameter names follow flower/models/base.py:
                               ``net.3`` Linear(ffn, d); dropout is identity in eval)
   ``Fp8DecoderBlock``         base.py:698-722: x + attn(ln1(x)), then + ff(ln2(x))
 
-Norms, GELU and residual adds are plain torch ops on the GPU; the linears, the quantisers and the
-attention run in libflower_amd.so. Wrap calls in ``fp8_weight_cache(block)`` to quantise the
+``forward`` runs the fused path on bf16 GPU inputs (RMSNorm and GELU fused with the next
+linear's per-row e4m3 quantisation, residual adds in the GEMM epilogues, the attention writing its
+(B, T, H, D) output in place: 11 library kernels, no torch elementwise kernels);
+``forward_unfused`` is the module-by-module composition (torch norms / GELU / adds around the
+library's linears and attention). Wrap calls in ``fp8_weight_cache(block)`` to quantise the
 weights once.
 """
 
@@ -21,6 +24,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
+from . import _lib
 from .kernels.fp8_swa_attention import fp8_swa_attention_forward
 from .precision import Fp8Linear
 
@@ -88,8 +92,87 @@ class Fp8DecoderBlock(nn.Module):
 
     @torch.no_grad()
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._fusable(x):
+            return self._forward_fused(x)
+        return self.forward_unfused(x)
+
+    @torch.no_grad()
+    def forward_unfused(self, x: torch.Tensor) -> torch.Tensor:
+        """The reference composition, one module after the other."""
         x = x + self.attn(self.ln1(x))
         return x + self.ff(self.ln2(x))
+
+    def _linears(self):
+        return self.attn.qkv, self.attn.out, self.ff.net[0], self.ff.net[3]
+
+    def _fusable(self, x: torch.Tensor) -> bool:
+        gelu = self.ff.net[1]
+        return (x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 3 and x.shape[-1] % 8 == 0
+                and x.shape[-1] <= 4096 and self.ff.net[0].out_features <= 4096
+                and all(l.bias is None and l.recipe == "rowwise" for l in self._linears())
+                and isinstance(gelu, nn.GELU) and gelu.approximate == "none"
+                and self.ln1.weight.dtype == self.ln2.weight.dtype == torch.bfloat16)
+
+    def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
+        """The same block with the work around the FP8 GEMMs fused into the library's kernels:
+        RMSNorm -> per-row e4m3 in one pass (flw_rmsnorm_quant_rows_e4m3), the attention writing
+        its (B, T, H, D) output in place, the residual adds in the GEMM epilogues
+        (flw_fp8_scaled_mm_residual), GELU -> per-row e4m3 in one pass (flw_gelu_quant_rows_e4m3).
+        Every rounding step of the unfused composition is kept (bf16 norm / GELU outputs, bf16
+        linear outputs before each residual add)."""
+        lib = _lib.load()
+        B, T, d = x.shape
+        M = B * T
+        dev = x.device
+        stream = _lib.stream_of(x)
+        x2 = x.reshape(M, d)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        qkv_l, out_l, ff1_l, ff2_l = self._linears()
+
+        def codes_of(kind, src, cols, norm=None):
+            c = torch.empty((M, cols), dtype=torch.uint8, device=dev)
+            sc = torch.empty(M, dtype=torch.float32, device=dev)
+            if kind == "rmsnorm":
+                rc = lib.flw_rmsnorm_quant_rows_e4m3(src.data_ptr(), M, cols, cols, norm.weight.data_ptr(),
+                                                     float(norm.eps), c.data_ptr(), sc.data_ptr(), None, stream)
+            elif kind == "gelu":
+                rc = lib.flw_gelu_quant_rows_e4m3(src.data_ptr(), M, cols, cols, c.data_ptr(), sc.data_ptr(),
+                                                  None, stream)
+            else:
+                rc = lib.flw_quant_rows_e4m3(src.data_ptr(), _lib.BF16, M, cols, cols, c.data_ptr(),
+                                             sc.data_ptr(), stream)
+            _lib.check(rc, kind)
+            return c, sc
+
+        def linear(codes, sc, lin, residual=None):
+            w8, ws = lin.weight_codes()
+            N, K = w8.shape
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            if residual is None:
+                rc = lib.flw_fp8_scaled_mm(codes.data_ptr(), M, K, w8.data_ptr(), N, sc.data_ptr(), M,
+                                           ws.data_ptr(), ws.numel(), y.data_ptr(), N, stream)
+            else:
+                rc = lib.flw_fp8_scaled_mm_residual(codes.data_ptr(), M, K, w8.data_ptr(), N, sc.data_ptr(), M,
+                                                    ws.data_ptr(), ws.numel(), y.data_ptr(), N,
+                                                    residual.data_ptr(), residual.stride(0), stream)
+            _lib.check(rc, "fp8 linear")
+            return y
+
+        att = self.attn
+        c1, s1 = codes_of("rmsnorm", x2, d, self.ln1)
+        qkv = linear(c1, s1, qkv_l).view(B, T, 3 * d)
+        q, k, v = (att._split(t) for t in qkv.chunk(3, dim=-1))
+        a = torch.empty((B, T, d), dtype=torch.bfloat16, device=dev)
+        window = T if att.local_window is None else att.local_window
+        fp8_swa_attention_forward(q, k, v, window, granularity=att.granularity,
+                                  out=a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2))
+        ca, sa = codes_of("plain", a.view(M, d), d)
+        x1 = linear(ca, sa, out_l, residual=x2)
+        c2, s2 = codes_of("rmsnorm", x1, d, self.ln2)
+        f = linear(c2, s2, ff1_l)
+        cg, sg = codes_of("gelu", f, f.shape[1])
+        return linear(cg, sg, ff2_l, residual=x1).view(B, T, d)
 
 
 def init_block_(block: Fp8DecoderBlock, std: float = 0.02, seed: int = 0) -> Fp8DecoderBlock:

@@ -39,7 +39,15 @@ struct GemmParams {
   int M, N, K;
   int tiles_n;         // output tiles along N
   int tiles_m;         // output tiles along M
+  const uint16_t* res; // optional bf16 residual [M, N] (row stride rs): y = bf16(res + bf16(..))
+  int64_t rs;
 };
+
+// The epilogue value of one output: bf16(v), or bf16(residual + bf16(v)) -- x + linear(h) with
+// both terms in bf16, as the reference's residual adds compute it.
+__device__ __forceinline__ float epi_value(float v, const uint16_t* res, int64_t idx) {
+  return res ? round_bf16(v) + __uint_as_float((uint32_t)res[idx] << 16) : v;
+}
 
 __device__ __forceinline__ v8i gfrag(const uint8_t* lds, int off) {
   const uint4 a = *reinterpret_cast<const uint4*>(lds + off);
@@ -133,7 +141,9 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmParams p) {
         if (n >= p.N) continue;      // N % 4 == 0 is required on the host
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e] * sxm * p.sw[(int64_t)(n + e) * p.sw_step];
+        for (int e = 0; e < 4; ++e)
+          v[e] = epi_value(acc[i][j][4 * g + e] * sxm * p.sw[(int64_t)(n + e) * p.sw_step], p.res,
+                           (int64_t)m * p.rs + n + e);
         uint2 w;
         w.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
         w.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
@@ -299,9 +309,19 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
         const int n = n0 + 128 * wn + 32 * i + 8 * g + 4 * hh;
         if (n >= p.N) continue;      // N % 4 == 0 is required on the host
         const v16f& c = acc[i][j];
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = c[4 * g + e] * sxm[j] * swn[4 * g + e];
+        if (p.res) {
+          const uint2 r = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.rs + n);
+          v[0] = round_bf16(v[0]) + __uint_as_float(r.x << 16);
+          v[1] = round_bf16(v[1]) + __uint_as_float(r.x & 0xFFFF0000u);
+          v[2] = round_bf16(v[2]) + __uint_as_float(r.y << 16);
+          v[3] = round_bf16(v[3]) + __uint_as_float(r.y & 0xFFFF0000u);
+        }
         uint2 w;
-        w.x = pack_bf16x2(c[4 * g] * sxm[j] * swn[4 * g], c[4 * g + 1] * sxm[j] * swn[4 * g + 1]);
-        w.y = pack_bf16x2(c[4 * g + 2] * sxm[j] * swn[4 * g + 2], c[4 * g + 3] * sxm[j] * swn[4 * g + 3]);
+        w.x = pack_bf16x2(v[0], v[1]);
+        w.y = pack_bf16x2(v[2], v[3]);
         *reinterpret_cast<uint2*>(yrow + n) = w;
       }
     }
@@ -537,7 +557,7 @@ static int compute_units() {
 
 static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
                      const float* sx, int64_t sx_count, const float* sw, int64_t sw_count,
-                     void* y, int64_t ys, hipStream_t s) {
+                     void* y, int64_t ys, hipStream_t s, const void* res = nullptr, int64_t rs = 0) {
   FLW_REQUIRE(x8 && w8 && sx && sw && y, FLW_E_INVALID, "null pointer argument");
   FLW_REQUIRE(M > 0 && N > 0 && K > 0, FLW_E_INVALID, "empty GEMM");
   FLW_REQUIRE(K % 16 == 0, FLW_E_UNSUPPORTED, "K must be a multiple of 16, got %lld", (long long)K);
@@ -552,6 +572,9 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
   p.sx_step = sx_count == 1 ? 0 : 1; p.sw_step = sw_count == 1 ? 0 : 1;
   p.y = static_cast<uint16_t*>(y); p.ys = ys;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.res = static_cast<const uint16_t*>(res); p.rs = rs;
+  FLW_REQUIRE(res == nullptr || (rs >= N && rs % 4 == 0 && ((uintptr_t)res & 7) == 0), FLW_E_INVALID,
+              "residual rows must be 8-byte aligned with a stride >= N, a multiple of 4");
   if (K % kFBK == 0 && N * K < (1ll << 32) && M * K < (1ll << 32)) {
     p.tiles_n = (int)((N + kFBN - 1) / kFBN);
     p.tiles_m = (int)((M + kFBM - 1) / kFBM);
@@ -606,6 +629,16 @@ extern "C" int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const 
                                  int64_t y_row_stride, void* stream) {
   return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y,
                    y_row_stride, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int flw_fp8_scaled_mm_residual(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
+                                          int64_t N, const float* x_scale, int64_t x_scale_count,
+                                          const float* w_scale, int64_t w_scale_count, void* y,
+                                          int64_t y_row_stride, const void* residual,
+                                          int64_t residual_row_stride, void* stream) {
+  FLW_REQUIRE(residual != nullptr, FLW_E_INVALID, "null residual");
+  return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y, y_row_stride,
+                   static_cast<hipStream_t>(stream), residual, residual_row_stride);
 }
 
 extern "C" size_t flw_fp8_linear_workspace_bytes(int64_t M, int64_t K, int mode) {

@@ -335,6 +335,109 @@ __global__ __launch_bounds__(kThreads) void rows_quant_kernel(const T* __restric
   }
 }
 
+// ---------------------------------------------------------------- activation + per-row quantiser
+//
+// The producer of an FP8 linear's input fused with its per-row quantiser (flw_quant_rows_e4m3
+// semantics), one wave per row, the row held in registers between the reductions:
+//   ACT_RMSNORM: h = bf16( bf16( x * (1 / sqrt(mean(x^2) + eps)) ) * w )   (base.py:324-338)
+//   ACT_GELU:    h = bf16( (0.5 x) * (1 + erf(x / sqrt 2)) )                 (F.gelu, exact erf)
+// then scale = max(amax|h| / 448, 1e-12), code = e4m3(h / scale). bf16 in and out; the bf16 h
+// is written too when h_out is given.
+constexpr int kActRmsnorm = 0, kActGelu = 1;
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int ACT, int NV>
+__global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
+    const uint16_t* __restrict__ x, int64_t rows, int cols, int64_t rs, const uint16_t* __restrict__ w,
+    float eps, uint8_t* __restrict__ out, float* __restrict__ scale_out, uint16_t* __restrict__ h_out) {
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;            // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int nvec = cols >> 3;
+  const uint16_t* src = x + row * rs;
+  float h[NV][8];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      Vec16<uint16_t>::load(src + 8 * v, h[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[i][e] = 0.0f;
+    }
+  }
+  if (ACT == kActRmsnorm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(h[i][e], h[i][e], ss);
+    const float ms = wave_sum_f32(ss) / (float)cols;
+    const float r = 1.0f / __builtin_sqrtf(ms + eps);        // IEEE sqrt and division
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int v = lane + 64 * i;
+      if (v >= nvec) continue;
+      float g[8];
+      Vec16<uint16_t>::load(w + 8 * v, g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[i][e] = round_bf16(round_bf16(h[i][e] * r) * g[e]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = h[i][e];
+        h[i][e] = round_bf16((0.5f * a) * (1.0f + erff(a * 0.70710678118654752f)));
+      }
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { const uint32_t a = abs_bits(h[i][e]); m = m > a ? m : a; }
+  m = wave_max_u32(m);
+  const float amax = __uint_as_float(m);
+  float sc = amax / kE4m3Max;
+  sc = sc < kEps ? kEps : sc;
+  if (lane == 0) scale_out[row] = sc;
+  const bool fast = __builtin_isfinite(amax);
+  const float rcp = 1.0f / sc;
+  uint8_t* dst = out + row * cols;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v >= nvec) continue;
+    uint32_t wd[2];
+    if (fast) {
+      codes_of<8>(h[i], sc, rcp, true, wd);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c |= (f32_to_e4m3(h[i][4 * q + j] / sc) & 0xFFu) << (8 * j);
+        wd[q] = c;
+      }
+    }
+    *reinterpret_cast<uint2*>(dst + 8 * v) = make_uint2(wd[0], wd[1]);
+    if (h_out) {
+      uint4 o;
+      o.x = f32_to_bf16_bits(h[i][0]) | (f32_to_bf16_bits(h[i][1]) << 16);
+      o.y = f32_to_bf16_bits(h[i][2]) | (f32_to_bf16_bits(h[i][3]) << 16);
+      o.z = f32_to_bf16_bits(h[i][4]) | (f32_to_bf16_bits(h[i][5]) << 16);
+      o.w = f32_to_bf16_bits(h[i][6]) | (f32_to_bf16_bits(h[i][7]) << 16);
+      *reinterpret_cast<uint4*>(h_out + row * cols + 8 * v) = o;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- host side
 
 static int64_t nchunks_of(int64_t T) { return (T + kRowsPerChunk - 1) / kRowsPerChunk; }
@@ -508,6 +611,47 @@ extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64
     hipLaunchKernelGGL(rows_quant_kernel<uint16_t>, grid, dim3(kThreads), 0, s,
                        static_cast<const uint16_t*>(x), rows, cols, row_stride, out, scale_out);
   return check_launch("flw_quant_rows_e4m3");
+}
+
+template <int ACT>
+static int rows_act_quant(const void* x, int64_t rows, int64_t cols, int64_t rs, const void* w, float eps,
+                          uint8_t* out, float* scale_out, void* h_out, hipStream_t s, const char* name) {
+  FLW_REQUIRE(x != nullptr && out != nullptr && scale_out != nullptr && (ACT != kActRmsnorm || w != nullptr),
+              FLW_E_INVALID, "null pointer");
+  FLW_REQUIRE(rows > 0 && cols > 0, FLW_E_INVALID, "empty matrix");
+  FLW_REQUIRE(cols % 8 == 0 && rs % 8 == 0 && rs >= cols && ((uintptr_t)x & 15) == 0 &&
+              ((uintptr_t)out & 7) == 0 && ((uintptr_t)h_out & 15) == 0 && ((uintptr_t)w & 15) == 0,
+              FLW_E_INVALID, "rows must be 16-byte aligned multiples of 8 bf16 elements");
+  FLW_REQUIRE(cols <= 4096, FLW_E_UNSUPPORTED, "rows longer than 4096 elements are not supported, got %lld",
+              (long long)cols);
+  FLW_REQUIRE((rows + 3) / 4 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many rows");
+  dim3 grid((unsigned)((rows + 3) / 4));
+  const int nv = (int)((cols / 8 + 63) / 64);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(w);
+  uint16_t* hp = static_cast<uint16_t*>(h_out);
+#define FLW_ACT_CASE(N)                                                                               \
+  if (nv <= N) {                                                                                      \
+    hipLaunchKernelGGL((rows_act_quant_kernel<ACT, N>), grid, dim3(kThreads), 0, s, xp, rows, (int)cols, \
+                       rs, wp, eps, out, scale_out, hp);                                              \
+    return check_launch(name);                                                                        \
+  }
+  FLW_ACT_CASE(2) FLW_ACT_CASE(4) FLW_ACT_CASE(8)
+#undef FLW_ACT_CASE
+  return set_error(FLW_E_UNSUPPORTED, "%s: row too long", name);
+}
+
+extern "C" int flw_rmsnorm_quant_rows_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride,
+                                           const void* weight, float eps, uint8_t* out, float* scale_out,
+                                           void* h_out, void* stream) {
+  return rows_act_quant<kActRmsnorm>(x, rows, cols, row_stride, weight, eps, out, scale_out, h_out,
+                                     static_cast<hipStream_t>(stream), "flw_rmsnorm_quant_rows_e4m3");
+}
+
+extern "C" int flw_gelu_quant_rows_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride,
+                                        uint8_t* out, float* scale_out, void* h_out, void* stream) {
+  return rows_act_quant<kActGelu>(x, rows, cols, row_stride, nullptr, 0.0f, out, scale_out, h_out,
+                                  static_cast<hipStream_t>(stream), "flw_gelu_quant_rows_e4m3");
 }
 
 extern "C" int flw_diag_quotient(const float* x, int64_t n, const float* scales, int64_t n_scales,

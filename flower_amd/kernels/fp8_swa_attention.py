@@ -92,10 +92,14 @@ def fp8_swa_attention_forward(
     num_warps: int = 4,
     num_stages: int = 3,
     granularity: str = "tensor",
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """FP8 sliding-window causal attention forward.
 
-    q/k/v: (B, H, T, D) bf16 or fp32 on the GPU. Returns (B, H, T, D) in q's dtype.
+    q/k/v: (B, H, T, D) bf16 or fp32 on the GPU. Returns (B, H, T, D) in q's dtype. ``out`` (an
+    extension; the reference has no such argument): a (B, H, T, D) tensor of q's dtype, any
+    strides with D contiguous -- e.g. the (B, T, H, D) head view of a (B, T, H*D) buffer -- that
+    the kernel writes in place and that is returned.
     ``window``: each query attends to the ``window`` keys at or behind it (window <= 0 gives
     an all-zero output, as the reference's masking does).
 
@@ -130,7 +134,11 @@ def fp8_swa_attention_forward(
     q, sq = _prepare(q)
     k, sk = _prepare(k)
     v, sv = _prepare(v)
-    out = torch.empty((B, H, T, D), device=q.device, dtype=q.dtype)
+    if out is None:
+        out = torch.empty((B, H, T, D), device=q.device, dtype=q.dtype)
+    elif (out.shape != (B, H, T, D) or out.dtype != q.dtype or out.device != q.device
+          or out.stride(-1) != 1):
+        raise ValueError("out must be a (B, H, T, D) tensor of q's dtype and device with D contiguous")
     so = out.stride()[:3]
     ws = _lib.workspace(lib.flw_fp8_swa_workspace_bytes(B, H, T, D), q.device)
     strides = _lib.i64s(*sq, *sk, *sv, *so)

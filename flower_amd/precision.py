@@ -177,6 +177,11 @@ class Fp8Linear(nn.Linear):
     def quantize_weight(self):
         return quantize_weight(self.weight, self.recipe)
 
+    def weight_codes(self):
+        """(w8, w_scale): the fp8_weight_cache's copy while one is active, else quantised now."""
+        cached = getattr(self, "_fp8_cached", None)
+        return cached if cached is not None else self.quantize_weight()
+
     def forward_with(self, x: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor) -> torch.Tensor:
         if torch.is_autocast_enabled():
             x = x.to(torch.get_autocast_gpu_dtype())
@@ -282,6 +287,7 @@ class fp8_weight_cache:
 
             self._orig_forwards[mod] = mod.forward
             mod.forward = cached_forward
+            mod._fp8_cached = (w8, w_scale)
             self._layers.append(mod)
             if self.verify:
                 self._fingerprints[mod] = self._fingerprint(mod.weight)
@@ -291,6 +297,7 @@ class fp8_weight_cache:
         changed = []
         for mod in self._layers:
             mod.forward = self._orig_forwards[mod]
+            mod._fp8_cached = None
             if self.verify and exc_type is None:
                 if self._fingerprint(mod.weight) != self._fingerprints[mod]:
                     changed.append(mod)

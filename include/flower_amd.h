@@ -131,6 +131,21 @@ int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, i
                                   float* scales_out, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* The producer of an FP8 linear's input fused with its per-row quantiser (flw_quant_rows_e4m3
+ * semantics: scale = max(amax / 448, 1e-12) per row, codes = e4m3(h / scale), no clamp), one read
+ * of the bf16 rows [rows, cols] (row stride in elements, cols <= 4096, multiples of 8):
+ *   flw_rmsnorm_quant_rows_e4m3: h = bf16(bf16(x * (1 / sqrt(mean(x^2) + eps))) * weight[cols]),
+ *     replacing RMSNorm (flower/models/base.py:324-338) followed by the next linear's activation
+ *     quantisation (base.py:912,917 / torchao Float8Linear's input cast);
+ *   flw_gelu_quant_rows_e4m3: h = bf16((0.5 x) (1 + erf(x / sqrt 2))), replacing the MLP's GELU
+ *     (base.py:514-525) followed by the same quantisation.
+ * h_out (bf16 [rows, cols], contiguous) receives h when not NULL. */
+int flw_rmsnorm_quant_rows_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride,
+                                const void* weight, float eps, uint8_t* out, float* scale_out,
+                                void* h_out, void* stream);
+int flw_gelu_quant_rows_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride,
+                             uint8_t* out, float* scale_out, void* h_out, void* stream);
+
 /* ---------------------------------------------------------------- GEMM */
 
 /* Workspace of flw_fp8_linear (the per-row e4m3 activations and their scales in A8W8 mode; 0
@@ -154,6 +169,15 @@ int flw_fp8_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride, co
 int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
                       const float* x_scale, int64_t x_scale_count, const float* w_scale,
                       int64_t w_scale_count, void* y, int64_t y_row_stride, void* stream);
+
+/* flw_fp8_scaled_mm with the block's residual add in the epilogue:
+ * y = bf16(residual + bf16((x8 . w8^T) * x_scale[m] * w_scale[n])), i.e. `x + linear(h)` of
+ * the decoder block (flower/models/base.py:698-722) with both terms rounded to bf16 as torch
+ * adds them. residual: bf16 [M, N], row stride in elements; it may alias y. */
+int flw_fp8_scaled_mm_residual(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
+                               const float* x_scale, int64_t x_scale_count, const float* w_scale,
+                               int64_t w_scale_count, void* y, int64_t y_row_stride,
+                               const void* residual, int64_t residual_row_stride, void* stream);
 
 /* ---------------------------------------------------------------- diagnostics */
 

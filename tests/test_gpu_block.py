@@ -94,3 +94,20 @@ def test_block_weight_cache_is_bit_identical():
         cached2 = blk(x)
     torch.cuda.synchronize()
     assert torch.equal(plain, cached) and torch.equal(cached, cached2)
+
+
+def test_fused_forward_matches_the_unfused_composition():
+    """The fused path (RMSNorm / GELU fused with the per-row quantisers, residual adds in the GEMM
+    epilogues, attention written in place) against the module-by-module composition: the two
+    differ only where torch's RMSNorm / GELU round differently in the last place."""
+    blk = make_block(seed=7)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(2, 512, CFG["d_model"], generator=g).to("cuda", torch.bfloat16)
+    assert blk._fusable(x)
+    fused = blk(x).float()
+    plain = blk.forward_unfused(x).float()
+    torch.cuda.synchronize()
+    d_f, d_p = fused - x.float(), plain - x.float()
+    rel = float((d_f - d_p).norm() / d_p.norm())
+    print(f"fused vs unfused delta rel: {rel:.2e}")
+    assert rel < 1e-2

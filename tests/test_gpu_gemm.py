@@ -230,3 +230,65 @@ def test_cache_uses_one_quantisation_per_enter():
     finally:
         Fp8Linear.quantize_weight = orig
 
+
+
+# ---------------------------------------------------------------- FP8 LM head (base.py:865-924)
+
+@pytest.mark.parametrize("shift", [0.0, -2.5])
+def test_fp8_lm_head_matches_bf16_head(shift):
+    """fp8_head vs the bf16 head on a tied-embedding-shaped weight (vocab 16384, d 1024): the
+    reference's bounds (test_training_speedups.py:359-412: relative Frobenius < 0.05, norm ratio in
+    (0.9, 1.1), next-token CE within 0.1; the -2.5 shift is its all-negative-rows regression),
+    and sampled rows against the oracle's closed form on the same codes."""
+    from flower_amd.lm_head import compute_logits, fp8_head
+    from oracle.quant import rowwise_fp8
+    torch.manual_seed(0)
+    vocab, d, B, T = 16384, 1024, 2, 64
+    head = nn.Linear(d, vocab, bias=False).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        head.weight.normal_(0.0, 0.02)
+    x = (torch.randn(B, T, d, device="cuda") + shift).to(torch.bfloat16)
+    with torch.no_grad():
+        fp8 = fp8_head(x, head.weight).float()
+        ref = head(x).float()
+        routed = compute_logits(head, x, fp8_lm_head=True, training=False).float()
+        train = compute_logits(head, x, fp8_lm_head=True, training=True).float()
+    assert fp8.shape == (B, T, vocab) and torch.equal(routed, fp8) and torch.equal(train, ref)
+    rel = ((fp8 - ref).norm() / ref.norm()).item()
+    assert rel < 0.05 and 0.9 < (fp8.norm() / ref.norm()).item() < 1.1, rel
+    labels = torch.randint(0, vocab, (B, T - 1), device="cuda")
+    ce = lambda lg: torch.nn.functional.cross_entropy(lg[:, :-1].reshape(-1, vocab), labels.reshape(-1))
+    assert abs(ce(fp8).item() - ce(ref).item()) < 0.1
+    w8, sw = rowwise_fp8(head.weight.detach().float().cpu().numpy())
+    xs = x.reshape(-1, d).float().cpu().numpy()[:16]
+    want, _, _ = fp8_linear_a8w8(xs, w8, sw.reshape(-1))
+    assert_gemm_close(to_np(fp8.reshape(-1, vocab)[:16]), want)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 1024, 1024), (300, 260, 128), (100, 36, 80)])
+def test_scaled_mm_residual_epilogue(M, N, K):
+    """flw_fp8_scaled_mm_residual: y = bf16(residual + bf16(scaled product)), against the closed
+    form with both roundings; the 256-tile kernel (K % 128 == 0) and the general one."""
+    from flower_amd import _lib as L
+    from oracle.e4m3 import round_bf16
+    lb = L.load()
+    x8, w8 = codes((M, K), 11), codes((N, K), 12)
+    rng = np.random.default_rng(13)
+    sx = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    res = torch.randn(M, N + 4, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16)
+    tx8, tw8, tsx, tsw = (torch.from_numpy(a).cuda() for a in (x8, w8, sx, sw))
+    tres = res.cuda()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    L.check(lb.flw_fp8_scaled_mm_residual(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), M,
+                                          tsw.data_ptr(), N, y.data_ptr(), N, tres.data_ptr(), N + 4,
+                                          L.stream_of(y)), "residual")
+    prod = round_bf16(scaled_mm(x8, w8, sx, sw))
+    ref = round_bf16((prod + res[:, :N].float().numpy()).astype(np.float32))
+    got = to_np(y).astype(np.float64)
+    # the product may differ from the closed form by one bf16 step (accumulation order), which the
+    # add carries into the sum, where it can flip the final rounding by one step
+    tol = 2.0 ** -7 * np.abs(prod) + 2.0 ** -7 * np.abs(ref) + 1e-3 * np.sqrt(np.mean(prod.astype(np.float64) ** 2))
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance"
+    assert (got == ref).mean() > 0.95

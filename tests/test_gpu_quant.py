@@ -426,3 +426,68 @@ def test_abi_rejects_bad_arguments():
                            sc.data_ptr(), ws.data_ptr(), 0, None)
     assert rc == 3 and b"workspace" in lb.flw_last_error()
     assert ctypes.c_int(rc).value == 3
+
+
+# ------------------------------------------------------------------ fused producers of FP8 inputs
+
+def _ulp(a, b):
+    from oracle.e4m3 import f32_to_bf16_bits
+    ia = f32_to_bf16_bits(np.asarray(a, np.float32)).astype(np.int32)
+    ib = f32_to_bf16_bits(np.asarray(b, np.float32)).astype(np.int32)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("rows,cols", [(300, 1024), (17, 4096), (64, 520), (5, 8)])
+def test_rmsnorm_quant_rows(rows, cols):
+    """flw_rmsnorm_quant_rows_e4m3: h against the oracle's RMSNorm (last-place differences from
+    the mean's summation order only), and the codes / scales bit-exact against the per-row
+    quantiser applied to the kernel's own h."""
+    from oracle.block import rmsnorm
+    L = lib()
+    lb = L.load()
+    g = torch.Generator().manual_seed(rows)
+    rs = cols + 16
+    xbuf = (torch.randn(rows, rs, generator=g) * 3).to(torch.bfloat16)
+    xbuf[rows // 2, :cols] = 0                      # an all-zero row: scale hits the 1e-12 floor
+    w = (1 + 0.2 * torch.randn(cols, generator=g)).to(torch.bfloat16)
+    tx, tw = xbuf.cuda(), w.cuda()
+    codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(rows, dtype=torch.float32, device="cuda")
+    h = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
+    L.check(lb.flw_rmsnorm_quant_rows_e4m3(tx.data_ptr(), rows, cols, rs, tw.data_ptr(), 1e-6, codes.data_ptr(),
+                                           sc.data_ptr(), h.data_ptr(), L.stream_of(tx)), "rmsnorm_quant")
+    torch.cuda.synchronize()
+    want_h = rmsnorm(xbuf[:, :cols].float().numpy(), w.float().numpy(), 1e-6)
+    d = _ulp(h.float().cpu().numpy(), want_h)
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3, ((d > 0).mean(), d.max())
+    want_c, want_s = rowwise_fp8(h.float().cpu().numpy())
+    np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
+    np.testing.assert_array_equal(to_np(sc), want_s.reshape(-1))
+
+
+@pytest.mark.parametrize("rows,cols", [(200, 4096), (33, 1024)])
+def test_gelu_quant_rows(rows, cols):
+    """flw_gelu_quant_rows_e4m3: h against the oracle's exact-erf GELU (the device erff differs in
+    the last place; outputs under 1e-4 compared absolutely), codes / scales bit-exact against the
+    per-row quantiser applied to the kernel's own h."""
+    from oracle.block import gelu
+    L = lib()
+    lb = L.load()
+    g = torch.Generator().manual_seed(cols)
+    x = (torch.randn(rows, cols, generator=g) * 3).to(torch.bfloat16)
+    tx = x.cuda()
+    codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(rows, dtype=torch.float32, device="cuda")
+    h = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
+    L.check(lb.flw_gelu_quant_rows_e4m3(tx.data_ptr(), rows, cols, cols, codes.data_ptr(), sc.data_ptr(),
+                                        h.data_ptr(), L.stream_of(tx)), "gelu_quant")
+    torch.cuda.synchronize()
+    got = h.float().cpu().numpy()
+    want = gelu(x.float().numpy())
+    big = np.abs(want) > 1e-4
+    d = _ulp(got[big], want[big])
+    assert d.max() <= 1 and (d > 0).mean() < 0.02, ((d > 0).mean(), d.max())
+    assert np.abs(got[~big] - want[~big]).max() < 2e-6
+    want_c, want_s = rowwise_fp8(got)
+    np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
+    np.testing.assert_array_equal(to_np(sc), want_s.reshape(-1))
