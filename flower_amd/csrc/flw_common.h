@@ -108,11 +108,17 @@ template <> struct Vec16<float> {
     float4 v = *reinterpret_cast<const float4*>(p);
     out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
   }
+  __device__ __forceinline__ static void unpack(uint4 v, float* out) {
+    out[0] = __uint_as_float(v.x); out[1] = __uint_as_float(v.y);
+    out[2] = __uint_as_float(v.z); out[3] = __uint_as_float(v.w);
+  }
 };
 template <> struct Vec16<uint16_t> {   // bf16
   static constexpr int N = 8;
   __device__ __forceinline__ static void load(const void* p, float* out) {
-    uint4 v = *reinterpret_cast<const uint4*>(p);
+    unpack(*reinterpret_cast<const uint4*>(p), out);
+  }
+  __device__ __forceinline__ static void unpack(uint4 v, float* out) {
     uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -340,10 +340,26 @@ __global__ __launch_bounds__(kThreads) void rows_quant_kernel(const T* __restric
 // The producer of an FP8 linear's input fused with its per-row quantiser (flw_quant_rows_e4m3
 // semantics), one wave per row, the row held in registers between the reductions:
 //   ACT_RMSNORM: h = bf16( bf16( x * (1 / sqrt(mean(x^2) + eps)) ) * w )   (base.py:324-338)
-//   ACT_GELU:    h = bf16( (0.5 x) * (1 + erf(x / sqrt 2)) )                 (F.gelu, exact erf)
+//   ACT_GELU:    h = bf16( (0.5 x) * (1 + erf(x / sqrt 2)) )                 (F.gelu, erf form)
 // then scale = max(amax|h| / 448, 1e-12), code = e4m3(h / scale). bf16 in and out; the bf16 h
 // is written too when h_out is given.
 constexpr int kActRmsnorm = 0, kActGelu = 1;
+
+// erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7): erf(|x|) = 1 - poly(t) exp(-x^2),
+// t = 1 / (1 + p |x|); two transcendental and six fused multiply-adds instead of the device
+// library's full-precision erff. In GELU, (0.5 x)(1 + erf(x / sqrt 2)), that error is far below
+// the bf16 rounding of the result.
+__device__ __forceinline__ float erf_as(float x) {
+  const float a = __builtin_fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+  float q = fmaf(1.061405429f, t, -1.453152027f);
+  q = fmaf(q, t, 1.421413741f);
+  q = fmaf(q, t, -0.284496736f);
+  q = fmaf(q, t, 0.254829592f);
+  q *= t;
+  const float e = __builtin_amdgcn_exp2f(-a * a * 1.4426950408889634f);
+  return __builtin_copysignf(fmaf(-q, e, 1.0f), x);
+}
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
@@ -360,48 +376,64 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
   const int lane = threadIdx.x & 63;
   const int nvec = cols >> 3;
   const uint16_t* src = x + row * rs;
-  float h[NV][8];
+  // The row stays in registers as packed bf16 (h is a bf16 value at every step that is kept).
+  uint4 hb[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int v = lane + 64 * i;
-    if (v < nvec) {
-      Vec16<uint16_t>::load(src + 8 * v, h[i]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) h[i][e] = 0.0f;
-    }
+    hb[i] = v < nvec ? *reinterpret_cast<const uint4*>(src + 8 * v) : make_uint4(0, 0, 0, 0);
   }
+  auto unpack = [](const uint4& q, float* f) __attribute__((always_inline)) { Vec16<uint16_t>::unpack(q, f); };
+  auto pack = [](const float* f) __attribute__((always_inline)) {
+    return make_uint4(f32_to_bf16_bits(f[0]) | (f32_to_bf16_bits(f[1]) << 16),
+                      f32_to_bf16_bits(f[2]) | (f32_to_bf16_bits(f[3]) << 16),
+                      f32_to_bf16_bits(f[4]) | (f32_to_bf16_bits(f[5]) << 16),
+                      f32_to_bf16_bits(f[6]) | (f32_to_bf16_bits(f[7]) << 16));
+  };
   if (ACT == kActRmsnorm) {
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < NV; ++i) {
+      float f[8];
+      unpack(hb[i], f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(h[i][e], h[i][e], ss);
+      for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+    }
     const float ms = wave_sum_f32(ss) / (float)cols;
     const float r = 1.0f / __builtin_sqrtf(ms + eps);        // IEEE sqrt and division
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int v = lane + 64 * i;
       if (v >= nvec) continue;
-      float g[8];
+      float f[8], g[8];
+      unpack(hb[i], f);
       Vec16<uint16_t>::load(w + 8 * v, g);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[i][e] = round_bf16(round_bf16(h[i][e] * r) * g[e]);
+      for (int e = 0; e < 8; ++e) f[e] = round_bf16(round_bf16(f[e] * r) * g[e]);
+      hb[i] = pack(f);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < NV; ++i) {
+      float f[8];
+      unpack(hb[i], f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a = h[i][e];
-        h[i][e] = round_bf16((0.5f * a) * (1.0f + erff(a * 0.70710678118654752f)));
-      }
+      for (int e = 0; e < 8; ++e) f[e] = (0.5f * f[e]) * (1.0f + erf_as(f[e] * 0.70710678118654752f));
+      hb[i] = pack(f);
+      __builtin_amdgcn_sched_barrier(0);        // one vector's erf at a time: bounded registers
+    }
   }
   uint32_t m = 0;
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t q[4] = {hb[i].x, hb[i].y, hb[i].z, hb[i].w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) { const uint32_t a = abs_bits(h[i][e]); m = m > a ? m : a; }
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = (q[e] << 16) & 0x7FFFFFFFu, hi = q[e] & 0x7FFF0000u;
+      m = m > lo ? m : lo;
+      m = m > hi ? m : hi;
+    }
+  }
   m = wave_max_u32(m);
   const float amax = __uint_as_float(m);
   float sc = amax / kE4m3Max;
@@ -414,27 +446,22 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
   for (int i = 0; i < NV; ++i) {
     const int v = lane + 64 * i;
     if (v >= nvec) continue;
+    float f[8];
+    unpack(hb[i], f);
     uint32_t wd[2];
     if (fast) {
-      codes_of<8>(h[i], sc, rcp, true, wd);
+      codes_of<8>(f, sc, rcp, true, wd);
     } else {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         uint32_t c = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) c |= (f32_to_e4m3(h[i][4 * q + j] / sc) & 0xFFu) << (8 * j);
+        for (int j = 0; j < 4; ++j) c |= (f32_to_e4m3(f[4 * q + j] / sc) & 0xFFu) << (8 * j);
         wd[q] = c;
       }
     }
     *reinterpret_cast<uint2*>(dst + 8 * v) = make_uint2(wd[0], wd[1]);
-    if (h_out) {
-      uint4 o;
-      o.x = f32_to_bf16_bits(h[i][0]) | (f32_to_bf16_bits(h[i][1]) << 16);
-      o.y = f32_to_bf16_bits(h[i][2]) | (f32_to_bf16_bits(h[i][3]) << 16);
-      o.z = f32_to_bf16_bits(h[i][4]) | (f32_to_bf16_bits(h[i][5]) << 16);
-      o.w = f32_to_bf16_bits(h[i][6]) | (f32_to_bf16_bits(h[i][7]) << 16);
-      *reinterpret_cast<uint4*>(h_out + row * cols + 8 * v) = o;
-    }
+    if (h_out) *reinterpret_cast<uint4*>(h_out + row * cols + 8 * v) = hb[i];
   }
 }
 
