@@ -52,6 +52,12 @@ SIGNATURES = {
     "flw_fp8_swa_attention_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_int, _P64, c_int64,
                                               c_int64, c_int64, c_int64, c_int64, c_int, c_void_p,
                                               c_void_p, c_void_p, c_size_t, c_void_p]),
+    "flw_swa_bf16_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                 c_void_p, c_void_p, c_void_p]),
+    "flw_swa_bf16_bwd_workspace_bytes": (c_size_t, [c_int64] * 4),
+    "flw_swa_bf16_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                 c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                 c_void_p]),
     "flw_fp8_linear_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int]),
     "flw_fp8_linear": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                c_int64, c_int, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),

@@ -1,0 +1,642 @@
+// bf16 causal sliding-window attention, forward (with the log-sum-exp) and backward, for gfx950.
+//
+// The differentiable counterpart of the FP8 forward (flower/kernels/swa_attention.py): bf16 Q/K/V
+// in, bf16 out, softmax and accumulation in fp32, v_mfma_f32_32x32x16_bf16 for every product.
+//
+// Forward: one workgroup = 4 waves = 128 queries of one (b, h); a wave owns 32 queries and walks
+// the 64-key tiles of its band. S^T = K Q^T (keys are the MFMA rows, so a lane holds 16 scores of
+// ONE query and the softmax row reductions are lane-local plus one v_permlane32_swap), the online
+// softmax in base 2, P packed to bf16 straight from those registers into the B operand of
+// O^T += V^T P^T. For that the K order of each 16-deep k-step is permuted: lane half h takes the
+// keys {0-3, 8-11} + 4h of the step, exactly the scores it already holds, and the V^T tile in LDS
+// is stored in that order (V is transposed while it is staged). L = m + log(l) is written for the
+// backward.
+//
+// Backward (after Delta = rowsum(dO * O)):
+//   dK / dV: one workgroup = 128 keys (4 waves x 32 keys, their K and V fragments in registers),
+//     walking the 64-query tiles that see them. S = Q K^T and dP = dO V^T with queries as MFMA
+//     rows, so a lane holds 16 queries of ONE key; P = exp(S - L), dS = P (dP - Delta) / sqrt(D)
+//     feed dV += P^T dO and dK += dS^T Q directly as A operands (the same k-step permutation over
+//     queries), with dO^T and Q^T staged transposed in LDS.
+//   dQ: one workgroup = 128 queries (Q and dO fragments in registers), walking key tiles:
+//     S^T = K Q^T, dP^T = V dO^T (keys as rows, one query per lane), dS^T, then
+//     dQ^T += K^T dS^T with K^T staged transposed in LDS.
+// Rows past T are loaded as zeros and never stored.
+#include <math.h>
+
+#include <type_traits>
+
+#include "flw_common.h"
+
+namespace flw {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ v16f mfma16(v8bf a, v8bf b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v8bf as_v8bf(uint4 q) { return __builtin_bit_cast(v8bf, q); }
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v{a, b}), bf16x2v));
+}
+
+constexpr float kLog2eB = 1.4426950408889634f;
+
+struct SwaB16Params {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;      // forward output (backward: read)
+  const uint16_t* dout;   // backward only
+  uint16_t* out;          // forward: O; dq kernel: dQ
+  uint16_t* out2;         // dkdv kernel: dK
+  uint16_t* out3;         // dkdv kernel: dV
+  float* lse;             // [B, H, T]
+  float* delta;           // [B, H, T]
+  int H, T, W, nblk, nwg; // nblk: 128-row blocks per (b, h)
+  float sm_scale;
+};
+
+// ---------------------------------------------------------------- LDS tile layouts
+//
+// A natural tile: 64 rows x D bf16 (2D bytes per row), 16-byte chunk c of row r at position
+// c ^ swz(r) so that 8 consecutive rows reading the same chunk hit 8 distinct bank groups.
+template <int D>
+__device__ __forceinline__ int nat_off(int r, int c) {
+  if (D == 32) return r * 64 + 16 * (c ^ ((r >> 2) & 3));
+  if (D == 64) return r * 128 + 16 * (c ^ ((r >> 1) & 7));
+  return r * 256 + 16 * (c ^ (r & 7));
+}
+
+// A transposed tile: D rows (the model dimension) x 64 positions (of rows of the source tile)
+// in the k-step order: source row s = 16 g + w goes to position 16 g + perm(w), perm swapping
+// the middle quads ({0-3, 8-11} first, {4-7, 12-15} second), so that lane half h of k-step g
+// reads the 16 bytes at position 16 g + 8 h. 128 bytes per row, chunk c at c ^ ((d >> 1) & 7).
+__device__ __forceinline__ int tr_pos(int s) {
+  const int w = s & 15, q = w >> 2;
+  const int qq = q == 1 ? 2 : (q == 2 ? 1 : q);
+  return (s & ~15) | (qq << 2) | (w & 3);
+}
+__device__ __forceinline__ int tr_off(int d, int pos) {
+  return d * 128 + 16 * ((pos >> 3) ^ ((d >> 1) & 7)) + 2 * (pos & 7);
+}
+
+// Global -> registers for one 64-row tile of a (T, D) bf16 slice: 64 * D / 8 chunks of 16 bytes
+// over 256 threads. Rows past T read as zero.
+template <int D>
+struct TileLoad {
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int NCH = 64 * CPR;
+  static constexpr int CPT = (NCH + 255) / 256;
+  uint4 r[CPT];
+  __device__ __forceinline__ void load(const uint16_t* base, int row0, int T, int tid) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int i = tid + 256 * j;
+      const int row = row0 + i / CPR, c = i % CPR;
+      r[j] = (i < NCH && row < T) ? *reinterpret_cast<const uint4*>(base + (int64_t)row * D + 8 * c)
+                                  : make_uint4(0, 0, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void store_nat(uint8_t* lds, int tid) const {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int i = tid + 256 * j;
+      if (i < NCH) *reinterpret_cast<uint4*>(lds + nat_off<D>(i / CPR, i % CPR)) = r[j];
+    }
+  }
+  __device__ __forceinline__ void store_tr(uint8_t* lds, int tid) const {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int i = tid + 256 * j;
+      if (i >= NCH) continue;
+      const int pos = tr_pos(i / CPR), d0 = 8 * (i % CPR);
+      const uint32_t w[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<uint16_t*>(lds + tr_off(d0 + e, pos)) = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+};
+
+// Fragment of a natural tile for the rows 32 rb .. 32 rb + 31, k-step ks (K = model dim):
+// lane (row rb*32 + lane%32, half h) takes dims 16 ks + 8 h .. +7.
+template <int D>
+__device__ __forceinline__ v8bf nat_frag(const uint8_t* lds, int rb, int ks, int lane) {
+  return as_v8bf(*reinterpret_cast<const uint4*>(lds + nat_off<D>(32 * rb + (lane & 31), 2 * ks + (lane >> 5))));
+}
+// Fragment of a transposed tile for the dims 32 db .. 32 db + 31, k-step g (K = the 64 rows).
+__device__ __forceinline__ v8bf tr_frag(const uint8_t* lds, int db, int g, int lane) {
+  const int d = 32 * db + (lane & 31);
+  return as_v8bf(*reinterpret_cast<const uint4*>(lds + tr_off(d, 16 * g + 8 * (lane >> 5))));
+}
+// Fragment of a row of global memory: 8 dims 16 ks + 8 h of row `row` (zero past T).
+template <int D>
+__device__ __forceinline__ v8bf row_frag(const uint16_t* base, int row, int T, int ks, int lane) {
+  if (row >= T) return as_v8bf(make_uint4(0, 0, 0, 0));
+  return as_v8bf(*reinterpret_cast<const uint4*>(base + (int64_t)row * D + 16 * ks + 8 * (lane >> 5)));
+}
+
+// The 16 values of a 32x32 C block, packed to bf16 as the B (or A) operand of the next product
+// with K over the block's rows: k-step 2 b + s gets values 8 s .. 8 s + 7.
+__device__ __forceinline__ v8bf pack_frag(const v16f& c, int s) {
+  uint4 q;
+  q.x = pk_bf16(c[8 * s + 0], c[8 * s + 1]);
+  q.y = pk_bf16(c[8 * s + 2], c[8 * s + 3]);
+  q.z = pk_bf16(c[8 * s + 4], c[8 * s + 5]);
+  q.w = pk_bf16(c[8 * s + 6], c[8 * s + 7]);
+  return as_v8bf(q);
+}
+
+__device__ __forceinline__ float pmax_pair(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float psum_pair(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Element v of a 32x32 C block held by lane (col, h) is row 8 (v / 4) + 4 h + v % 4.
+__device__ __forceinline__ int crow(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
+
+// XCD-contiguous work numbering (as in the FP8 kernel).
+__device__ __forceinline__ int xcd_id(int nwg) {
+  int L = (int)blockIdx.x;
+  if ((nwg & 7) == 0) L = (L & 7) * (nwg >> 3) + (L >> 3);
+  return L;
+}
+
+// ---------------------------------------------------------------- forward
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
+  constexpr int KS = D / 16;                      // k-steps over the head dim
+  constexpr int NDB = D / 32;                     // 32-row blocks of O^T
+  constexpr int NAT = 64 * D * 2;                 // bytes of a natural / transposed tile
+  __shared__ __align__(16) uint8_t lk[2][NAT];
+  __shared__ __align__(16) uint8_t lv[2][NAT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
+  const int L = xcd_id(p.nwg);
+  const int bh = L / p.nblk, mt = L % p.nblk;
+  const int T = p.T, W = p.W;
+  const int m0 = mt * 128, q0 = m0 + 32 * wave;
+  const int64_t slice = (int64_t)bh * T * D;
+  const uint16_t* Q = p.q + slice;
+  const uint16_t* K = p.k + slice;
+  const uint16_t* V = p.v + slice;
+  const float c = p.sm_scale * kLog2eB;
+
+  v8bf qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = row_frag<D>(Q, q0 + qc, T, ks, lane);
+
+  const int lo_raw = m0 - W + 1;
+  const int lo = lo_raw <= 0 ? 0 : (lo_raw & ~63);
+  const int hi = min(T, m0 + 128);
+  const int nt = hi > lo ? (hi - lo + 63) / 64 : 0;
+  const int wk0 = max(0, q0 - W + 1), wk1 = min(q0 + 31, T - 1);
+  const int ta = q0 < T ? (wk0 - lo) / 64 : 1;
+  const int tb = q0 < T ? (wk1 - lo) / 64 : 0;
+
+  v16f o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = v16f{};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  TileLoad<D> tk, tv;
+  if (nt > 0) {
+    tk.load(K, lo, T, tid);
+    tv.load(V, lo, T, tid);
+    tk.store_nat(lk[0], tid);
+    tv.store_tr(lv[0], tid);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nt; ++j) {
+    const int buf = j & 1;
+    const bool pre = j + 1 < nt;
+    if (pre) {
+      tk.load(K, lo + (j + 1) * 64, T, tid);
+      tv.load(V, lo + (j + 1) * 64, T, tid);
+    }
+    if (j >= ta && j <= tb) {
+      const int n0 = lo + 64 * j;
+      v16f s[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        s[b] = v16f{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s[b] = mfma16(nat_frag<D>(lk[buf], b, ks, lane), qf[ks], s[b]);
+      }
+      // mask: key n0 + 32 b + crow(v, h) against query q0 + qc
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int d0 = q0 + qc - (n0 + 32 * b);         // i - j for row 0 of the block
+        const bool full = (q0 - (n0 + 32 * b) >= 31) && (q0 + 31 - (n0 + 32 * b) < W) && (n0 + 32 * b + 31 < T);
+        if (!full) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int dd = d0 - crow(v, h);
+            s[b][v] = (dd >= 0 && dd < W && n0 + 32 * b + crow(v, h) < T) ? s[b][v] : -INFINITY;
+          }
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[b][v]);
+      const float m_new = fmaxf(m_run, pmax_pair(mx));
+      const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_safe) * c);
+      const float nb = -m_safe * c;
+      m_run = m_new;
+      float ls = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          s[b][v] = __builtin_amdgcn_exp2f(fmaf(s[b][v], c, nb));
+          ls += s[b][v];
+        }
+      l_run = fmaf(l_run, alpha, ls);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        o[db] *= alpha;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) o[db] = mfma16(tr_frag(lv[buf], db, g, lane), pack_frag(s[g >> 1], g & 1), o[db]);
+      }
+    }
+    // The other buffer was last read in step j - 1, which every wave finished before the barrier
+    // that ended it; one barrier per tile publishes the new tile.
+    if (pre) {
+      tk.store_nat(lk[buf ^ 1], tid);
+      tv.store_tr(lv[buf ^ 1], tid);
+    }
+    __syncthreads();
+  }
+
+  const float l_tot = psum_pair(l_run);
+  const int qi = q0 + qc;
+  if (qi < T) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t* op = p.out + slice + (int64_t)qi * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * db + 8 * j + 4 * h;
+        uint2 w;
+        w.x = pk_bf16(o[db][4 * j] * inv, o[db][4 * j + 1] * inv);
+        w.y = pk_bf16(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+        *reinterpret_cast<uint2*>(op + d) = w;
+      }
+    if (h == 0) p.lse[(int64_t)bh * T + qi] = fmaf(m_run, p.sm_scale, __logf(l_tot));
+  }
+}
+
+// ---------------------------------------------------------------- backward: Delta
+
+// Delta[row] = sum_d dO[row, d] * O[row, d] in fp32; D / 8 consecutive lanes per row.
+template <int D>
+__global__ __launch_bounds__(256) void swa_bf16_delta_kernel(const uint16_t* __restrict__ o,
+                                                             const uint16_t* __restrict__ dout,
+                                                             float* __restrict__ delta, int64_t rows) {
+  constexpr int LPR = D / 8;                      // lanes per row (8 elements each)
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / LPR;
+  const int part = (int)(gid % LPR);
+  float s = 0.0f;
+  if (row < rows) {
+    float a[8], b[8];
+    Vec16<uint16_t>::load(o + row * D + 8 * part, a);
+    Vec16<uint16_t>::load(dout + row * D + 8 * part, b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = fmaf(a[e], b[e], s);
+  }
+#pragma unroll
+  for (int w = LPR / 2; w >= 1; w >>= 1) s += __shfl_xor(s, w, 64);
+  if (row < rows && part == 0) delta[row] = s;
+}
+
+// ---------------------------------------------------------------- backward: dK, dV
+
+template <int D>
+__global__ __launch_bounds__(256, 1) void swa_bf16_dkdv_kernel(SwaB16Params p) {
+  constexpr int KS = D / 16, NDB = D / 32, NAT = 64 * D * 2;
+  __shared__ __align__(16) uint8_t lq[2][NAT];     // Q tile, natural (A operand of S)
+  __shared__ __align__(16) uint8_t lqt[2][NAT];    // Q tile, transposed (B operand of dK)
+  __shared__ __align__(16) uint8_t ldo[2][NAT];    // dO tile, natural (A operand of dP)
+  __shared__ __align__(16) uint8_t ldot[2][NAT];   // dO tile, transposed (B operand of dV)
+  __shared__ __align__(16) float lstat[2][2][64];  // L and Delta of the tile's queries
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, kc = lane & 31;
+  const int L = xcd_id(p.nwg);
+  const int bh = L / p.nblk, nt0 = L % p.nblk;
+  const int T = p.T, W = p.W;
+  const int k0w = nt0 * 128, k0 = k0w + 32 * wave;     // this wave's 32 keys
+  const int64_t slice = (int64_t)bh * T * D;
+  const uint16_t* Q = p.q + slice;
+  const uint16_t* DO = p.dout + slice;
+  const float* LSE = p.lse + (int64_t)bh * T;
+  const float* DLT = p.delta + (int64_t)bh * T;
+  const float c = p.sm_scale * kLog2eB;
+
+  // K and V of this wave's keys as B operands (lane = key column, 8 dims per k-step).
+  v8bf kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    kf[ks] = row_frag<D>(p.k + slice, k0 + kc, T, ks, lane);
+    vf[ks] = row_frag<D>(p.v + slice, k0 + kc, T, ks, lane);
+  }
+  v16f dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) { dk[db] = v16f{}; dv[db] = v16f{}; }
+
+  // Query tiles that see the workgroup's keys [k0w, k0w + 127]: queries [k0w, k0w + 127 + W - 1].
+  const int lo = k0w & ~63;
+  const int hi = min(T, k0w + 127 + W);
+  const int nt = hi > lo ? (hi - lo + 63) / 64 : 0;
+  // This wave's keys are seen by queries [k0, k0 + 31 + W - 1].
+  const int wq1 = min(T - 1, k0 + 31 + W - 1);
+  const int ta = k0 < T ? (k0 - lo) / 64 : 1;
+  const int tb = k0 < T ? (wq1 - lo) / 64 : 0;
+
+  TileLoad<D> tq, tdo;
+  auto stage_stats = [&](int buf, int r0) __attribute__((always_inline)) {
+    if (tid < 128) {
+      const int i = tid & 63, r = r0 + i;
+      lstat[buf][tid >> 6][i] = r < T ? (tid < 64 ? LSE[r] : DLT[r]) : 0.0f;
+    }
+  };
+  if (nt > 0) {
+    tq.load(Q, lo, T, tid);
+    tdo.load(DO, lo, T, tid);
+    tq.store_nat(lq[0], tid);
+    tq.store_tr(lqt[0], tid);
+    tdo.store_nat(ldo[0], tid);
+    tdo.store_tr(ldot[0], tid);
+    stage_stats(0, lo);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nt; ++j) {
+    const int buf = j & 1;
+    const bool pre = j + 1 < nt;
+    if (pre) {
+      tq.load(Q, lo + (j + 1) * 64, T, tid);
+      tdo.load(DO, lo + (j + 1) * 64, T, tid);
+    }
+    if (j >= ta && j <= tb) {
+      const int r0 = lo + 64 * j;                    // first query of the tile
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        // S and dP for queries r0 + 32 qb + crow(v, h) (rows) and key k0 + kc (column).
+        v16f s = v16f{}, dp = v16f{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = mfma16(nat_frag<D>(lq[buf], qb, ks, lane), kf[ks], s);
+          dp = mfma16(nat_frag<D>(ldo[buf], qb, ks, lane), vf[ks], dp);
+        }
+        const int key = k0 + kc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int ql = 32 * qb + crow(v, h), qi = r0 + ql;
+          const int dd = qi - key;
+          const bool ok = dd >= 0 && dd < W && qi < T && key < T;
+          const float lse2 = lstat[buf][0][ql] * kLog2eB;
+          const float pr = ok ? __builtin_amdgcn_exp2f(fmaf(s[v], c, -lse2)) : 0.0f;
+          s[v] = pr;
+          dp[v] = pr * (dp[v] - lstat[buf][1][ql]) * p.sm_scale;
+        }
+        // dV += P^T dO, dK += dS^T Q: A = this lane's key row, K = the 32 queries of block qb.
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+          const v8bf pa = pack_frag(s, hs), da = pack_frag(dp, hs);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            dv[db] = mfma16(pa, tr_frag(ldot[buf], db, 2 * qb + hs, lane), dv[db]);
+            dk[db] = mfma16(da, tr_frag(lqt[buf], db, 2 * qb + hs, lane), dk[db]);
+          }
+        }
+      }
+    }
+    if (pre) {
+      tq.store_nat(lq[buf ^ 1], tid);
+      tq.store_tr(lqt[buf ^ 1], tid);
+      tdo.store_nat(ldo[buf ^ 1], tid);
+      tdo.store_tr(ldot[buf ^ 1], tid);
+      stage_stats(buf ^ 1, lo + (j + 1) * 64);
+    }
+    __syncthreads();
+  }
+
+  // The A operands' rows were keys, the B operands' columns dims: lane (dim 32 db + lane % 32)
+  // holds dK / dV of the keys k0 + crow(v, h).
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int key = k0 + crow(v, h), d = 32 * db + kc;
+      if (key < T) {
+        p.out2[slice + (int64_t)key * D + d] = (uint16_t)f32_to_bf16_bits(dk[db][v]);
+        p.out3[slice + (int64_t)key * D + d] = (uint16_t)f32_to_bf16_bits(dv[db][v]);
+      }
+    }
+}
+
+// ---------------------------------------------------------------- backward: dQ
+
+template <int D>
+__global__ __launch_bounds__(256, 1) void swa_bf16_dq_kernel(SwaB16Params p) {
+  constexpr int KS = D / 16, NDB = D / 32, NAT = 64 * D * 2;
+  __shared__ __align__(16) uint8_t lk[2][NAT];     // K tile, natural (A operand of S^T)
+  __shared__ __align__(16) uint8_t lkt[2][NAT];    // K tile, transposed (A operand of dQ^T)
+  __shared__ __align__(16) uint8_t lv[2][NAT];     // V tile, natural (A operand of dP^T)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
+  const int L = xcd_id(p.nwg);
+  const int bh = L / p.nblk, mt = L % p.nblk;
+  const int T = p.T, W = p.W;
+  const int m0 = mt * 128, q0 = m0 + 32 * wave;
+  const int64_t slice = (int64_t)bh * T * D;
+  const uint16_t* K = p.k + slice;
+  const uint16_t* V = p.v + slice;
+  const float c = p.sm_scale * kLog2eB;
+  const int qi = q0 + qc;
+  const float lse2 = qi < T ? p.lse[(int64_t)bh * T + qi] * kLog2eB : 0.0f;
+  const float dl = qi < T ? p.delta[(int64_t)bh * T + qi] : 0.0f;
+
+  v8bf qf[KS], df[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[ks] = row_frag<D>(p.q + slice, qi, T, ks, lane);
+    df[ks] = row_frag<D>(p.dout + slice, qi, T, ks, lane);
+  }
+  v16f dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dq[db] = v16f{};
+
+  const int lo_raw = m0 - W + 1;
+  const int lo = lo_raw <= 0 ? 0 : (lo_raw & ~63);
+  const int hi = min(T, m0 + 128);
+  const int nt = hi > lo ? (hi - lo + 63) / 64 : 0;
+  const int wk0 = max(0, q0 - W + 1), wk1 = min(q0 + 31, T - 1);
+  const int ta = q0 < T ? (wk0 - lo) / 64 : 1;
+  const int tb = q0 < T ? (wk1 - lo) / 64 : 0;
+
+  TileLoad<D> tk, tv;
+  if (nt > 0) {
+    tk.load(K, lo, T, tid);
+    tv.load(V, lo, T, tid);
+    tk.store_nat(lk[0], tid);
+    tk.store_tr(lkt[0], tid);
+    tv.store_nat(lv[0], tid);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nt; ++j) {
+    const int buf = j & 1;
+    const bool pre = j + 1 < nt;
+    if (pre) {
+      tk.load(K, lo + (j + 1) * 64, T, tid);
+      tv.load(V, lo + (j + 1) * 64, T, tid);
+    }
+    if (j >= ta && j <= tb) {
+      const int n0 = lo + 64 * j;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        v16f s = v16f{}, dp = v16f{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = mfma16(nat_frag<D>(lk[buf], b, ks, lane), qf[ks], s);
+          dp = mfma16(nat_frag<D>(lv[buf], b, ks, lane), df[ks], dp);
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = n0 + 32 * b + crow(v, h);
+          const int dd = qi - key;
+          const bool ok = dd >= 0 && dd < W && qi < T && key < T;
+          const float pr = ok ? __builtin_amdgcn_exp2f(fmaf(s[v], c, -lse2)) : 0.0f;
+          dp[v] = pr * (dp[v] - dl) * p.sm_scale;
+        }
+        // dQ^T += K^T dS^T: A = K^T (dims as rows, keys of block b as K), B = dS^T (this lane's query).
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+          const v8bf db_ = pack_frag(dp, hs);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) dq[db] = mfma16(tr_frag(lkt[buf], db, 2 * b + hs, lane), db_, dq[db]);
+        }
+      }
+    }
+    if (pre) {
+      tk.store_nat(lk[buf ^ 1], tid);
+      tk.store_tr(lkt[buf ^ 1], tid);
+      tv.store_nat(lv[buf ^ 1], tid);
+    }
+    __syncthreads();
+  }
+
+  if (qi < T) {
+    uint16_t* op = p.out + slice + (int64_t)qi * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * db + 8 * j + 4 * h;
+        uint2 w;
+        w.x = pk_bf16(dq[db][4 * j], dq[db][4 * j + 1]);
+        w.y = pk_bf16(dq[db][4 * j + 2], dq[db][4 * j + 3]);
+        *reinterpret_cast<uint2*>(op + d) = w;
+      }
+  }
+}
+
+// ---------------------------------------------------------------- host
+
+static int check_b16(const void* a, const void* b, const void* c, int64_t B, int64_t H, int64_t T, int64_t D,
+                     int64_t window) {
+  FLW_REQUIRE(a && b && c, FLW_E_INVALID, "null pointer argument");
+  FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
+  FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
+  FLW_REQUIRE(window > 0, FLW_E_INVALID, "window must be positive");
+  FLW_REQUIRE(T <= (1 << 30) && B * H * ((T + 127) / 128) <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "shape too large");
+  FLW_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0 && ((uintptr_t)c & 15) == 0, FLW_E_INVALID,
+              "tensors must be 16-byte aligned");
+  return FLW_OK;
+}
+
+}  // namespace flw
+
+using namespace flw;
+
+extern "C" int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H,
+                                int64_t T, int64_t D, int64_t window, void* out, float* lse,
+                                void* stream) {
+  int rc = check_b16(q, k, v, B, H, T, D, window);
+  if (rc) return rc;
+  FLW_REQUIRE(out && lse && ((uintptr_t)out & 15) == 0, FLW_E_INVALID, "out / lse");
+  SwaB16Params p{};
+  p.q = static_cast<const uint16_t*>(q); p.k = static_cast<const uint16_t*>(k); p.v = static_cast<const uint16_t*>(v);
+  p.out = static_cast<uint16_t*>(out); p.lse = lse;
+  p.H = (int)H; p.T = (int)T; p.W = (int)(window < T ? window : T);
+  p.nblk = (int)((T + 127) / 128); p.nwg = (int)(B * H * p.nblk);
+  p.sm_scale = 1.0f / sqrtf((float)D);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)p.nwg);
+  const void* kf = D == 32 ? reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<32>)
+                 : D == 64 ? reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<64>)
+                           : reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<128>);
+  launch_timed(kf, grid, dim3(256), s, p);
+  return check_launch("flw_swa_bf16_fwd");
+}
+
+extern "C" size_t flw_swa_bf16_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
+  (void)D;
+  return (size_t)(B * H * T) * sizeof(float);
+}
+
+extern "C" int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, const void* out,
+                                const void* dout, const float* lse, int64_t B, int64_t H, int64_t T,
+                                int64_t D, int64_t window, void* dq, void* dk, void* dv,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_b16(q, k, v, B, H, T, D, window);
+  if (rc) return rc;
+  FLW_REQUIRE(out && dout && lse && dq && dk && dv, FLW_E_INVALID, "null pointer argument");
+  FLW_REQUIRE(((uintptr_t)out & 15) == 0 && ((uintptr_t)dout & 15) == 0 && ((uintptr_t)dq & 15) == 0 &&
+              ((uintptr_t)dk & 1) == 0 && ((uintptr_t)dv & 1) == 0, FLW_E_INVALID, "misaligned tensor");
+  const size_t need = flw_swa_bf16_bwd_workspace_bytes(B, H, T, D);
+  FLW_REQUIRE(workspace && workspace_bytes >= need, FLW_E_WORKSPACE, "workspace needs %zu bytes", need);
+  SwaB16Params p{};
+  p.q = static_cast<const uint16_t*>(q); p.k = static_cast<const uint16_t*>(k); p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<const uint16_t*>(out); p.dout = static_cast<const uint16_t*>(dout);
+  p.lse = const_cast<float*>(lse); p.delta = static_cast<float*>(workspace);
+  p.H = (int)H; p.T = (int)T; p.W = (int)(window < T ? window : T);
+  p.nblk = (int)((T + 127) / 128); p.nwg = (int)(B * H * p.nblk);
+  p.sm_scale = 1.0f / sqrtf((float)D);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t rows = B * H * T;
+  const int64_t threads = rows * (D / 8);
+  const dim3 dgrid((unsigned)((threads + 255) / 256));
+  if (D == 32) hipLaunchKernelGGL(swa_bf16_delta_kernel<32>, dgrid, dim3(256), 0, s, p.o, p.dout, p.delta, rows);
+  else if (D == 64) hipLaunchKernelGGL(swa_bf16_delta_kernel<64>, dgrid, dim3(256), 0, s, p.o, p.dout, p.delta, rows);
+  else hipLaunchKernelGGL(swa_bf16_delta_kernel<128>, dgrid, dim3(256), 0, s, p.o, p.dout, p.delta, rows);
+  const dim3 grid((unsigned)p.nwg);
+  SwaB16Params pk = p;
+  pk.out2 = static_cast<uint16_t*>(dk); pk.out3 = static_cast<uint16_t*>(dv);
+  SwaB16Params pq = p;
+  pq.out = static_cast<uint16_t*>(dq);
+  if (D == 32) {
+    hipLaunchKernelGGL(swa_bf16_dkdv_kernel<32>, grid, dim3(256), 0, s, pk);
+    hipLaunchKernelGGL(swa_bf16_dq_kernel<32>, grid, dim3(256), 0, s, pq);
+  } else if (D == 64) {
+    hipLaunchKernelGGL(swa_bf16_dkdv_kernel<64>, grid, dim3(256), 0, s, pk);
+    hipLaunchKernelGGL(swa_bf16_dq_kernel<64>, grid, dim3(256), 0, s, pq);
+  } else {
+    hipLaunchKernelGGL(swa_bf16_dkdv_kernel<128>, grid, dim3(256), 0, s, pk);
+    hipLaunchKernelGGL(swa_bf16_dq_kernel<128>, grid, dim3(256), 0, s, pq);
+  }
+  return check_launch("flw_swa_bf16_bwd");
+}

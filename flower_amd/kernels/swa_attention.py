@@ -1,0 +1,79 @@
+"""bf16 causal sliding-window attention, forward + backward, on the HIP library (gfx950).
+
+Mirrors flower/kernels/swa_attention.py: ``swa_attention(q, k, v, window, *, fwd_cfg, dkdv_cfg,
+dq_cfg)`` (:243-261) is differentiable; the forward saves L = m + log(l) per query (:77-160) and
+the backward computes Delta = rowsum(dO * O), then dK / dV (one program per key block walking the
+query blocks that see it) and dQ (one per query block walking its keys), :162-320. The Triton
+launch-geometry tuples are accepted and ignored (the HIP kernels use their own tiling).
+
+Errors as in the reference: ValueError for a non-(B, H, T, D) input, a head_dim outside
+{32, 64, 128} or a window <= 0 (:255-260). This build computes in bf16 only: other dtypes raise
+TypeError. No CPU fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+_FWD_CFG = (128, 64, 4, 2)
+_DKDV_CFG = (128, 64, 4, 2)
+_DQ_CFG = (128, 64, 4, 2)
+
+
+class _SlidingWindowAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, window):
+        lib = _lib.load()
+        B, H, T, D = q.shape
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        out = torch.empty_like(q)
+        lse = torch.empty((B, H, T), device=q.device, dtype=torch.float32)
+        rc = lib.flw_swa_bf16_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), B, H, T, D, int(window),
+                                  out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+        _lib.check(rc, "swa_attention forward")
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.window = int(window)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        lib = _lib.load()
+        q, k, v, out, lse = ctx.saved_tensors
+        B, H, T, D = q.shape
+        do = do.contiguous()
+        if do.dtype != q.dtype:
+            do = do.to(q.dtype)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        ws = _lib.workspace(lib.flw_swa_bf16_bwd_workspace_bytes(B, H, T, D), q.device)
+        rc = lib.flw_swa_bf16_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), do.data_ptr(),
+                                  lse.data_ptr(), B, H, T, D, ctx.window, dq.data_ptr(), dk.data_ptr(),
+                                  dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+        _lib.check(rc, "swa_attention backward")
+        return dq, dk, dv, None
+
+
+def swa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, *,
+                  fwd_cfg=_FWD_CFG, dkdv_cfg=_DKDV_CFG, dq_cfg=_DQ_CFG) -> torch.Tensor:
+    """Causal sliding-window attention. q/k/v: (B, H, T, D) bf16 on the GPU. Differentiable."""
+    del fwd_cfg, dkdv_cfg, dq_cfg
+    try:
+        _lib.load()
+    except RuntimeError as e:
+        raise RuntimeError(f"swa_attention requires the HIP library: {e}") from e
+    if q.dim() != 4:
+        raise ValueError(f"expected (B, H, T, D), got {tuple(q.shape)}")
+    if q.shape[-1] not in (32, 64, 128):
+        raise ValueError(f"head_dim must be 32/64/128, got {q.shape[-1]}")
+    if window <= 0:
+        raise ValueError("window must be positive; use flex for full-context attention")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        raise TypeError("swa_attention computes in bf16; got " + str(q.dtype))
+    _lib.require_gpu(q, k, v)
+    return _SlidingWindowAttention.apply(q, k, v, window)
+
+
+__all__ = ["swa_attention"]

@@ -146,6 +146,25 @@ int flw_rmsnorm_quant_rows_e4m3(const void* x, int64_t rows, int64_t cols, int64
 int flw_gelu_quant_rows_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride,
                              uint8_t* out, float* scale_out, void* h_out, void* stream);
 
+/* ---------------------------------------------------------------- bf16 sliding-window attention */
+
+/* The differentiable bf16 causal sliding-window attention of flower/kernels/swa_attention.py
+ * (`swa_attention`, :243-261; its Triton kernels :77-320). q, k, v, out, dout, dq, dk, dv:
+ * contiguous (B, H, T, D) bf16, 16-byte aligned; D in {32, 64, 128}; window > 0 (query i attends
+ * keys j with 0 <= i - j < window). Softmax and accumulation in fp32.
+ * flw_swa_bf16_fwd: out, and lse = m + log(l) per query ([B, H, T] fp32, natural log) for the
+ *   backward (the reference's _swa_fwd, :77-160).
+ * flw_swa_bf16_bwd: dq, dk, dv from dout and the forward's out / lse (the reference's
+ *   _swa_bwd_preprocess, _swa_bwd_dkdv and _swa_bwd_dq, :162-320); the workspace holds
+ *   Delta = rowsum(dout * out). */
+int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t T,
+                     int64_t D, int64_t window, void* out, float* lse, void* stream);
+size_t flw_swa_bf16_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
+int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                     const float* lse, int64_t B, int64_t H, int64_t T, int64_t D, int64_t window,
+                     void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
 /* ---------------------------------------------------------------- GEMM */
 
 /* Workspace of flw_fp8_linear (the per-row e4m3 activations and their scales in A8W8 mode; 0
