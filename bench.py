@@ -1,6 +1,6 @@
 """Benchmark of the FP8 sliding-window-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|swa_bf16|swa_bf16_450m]
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
@@ -27,6 +27,9 @@ x[8192, 1024] with 0.1 % outliers at 20x, cached e4m3 weight [4096, 1024] with p
 scales): the headline is the weight-only GEMM (e4m3 weight x bf16 activations on bf16 MFMA, one
 kernel per step); the A8W8 recipe (per-row activation quantisation + FP8 GEMM) is reported
 beside it, in GEMM TFLOP/s.
+--workload swa_bf16 / swa_bf16_450m measure the bf16 sliding-window attention training op (forward
+with log-sum-exp, then the backward) at the reference's measurement shape B1 H20 T4096 D64 W2048 /
+its 450M model shape B2 H20 T8192 D64 W2048; roofline = the backward entry point.
 Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
 """
 
@@ -56,6 +59,10 @@ WORKLOADS = {
     "c1": dict(B=1, H=8, T=1024, D=64, W=256, granularity="tensor", inputs="randn_fp32"),
     "c2": dict(M=8192, N=4096, K=1024, outlier_frac=0.001, outlier_scale=20.0, w_std=0.02),
     "c5": dict(B=1, T=32768, d_model=1024, num_heads=16, ffn_dim=4096, W=4096, w_std=0.02),
+    # bf16 sliding-window attention as a training op (forward with log-sum-exp + backward): the
+    # reference's own measurement shape (swa_attention.py:10-14, :40-43) and its 450M model shape
+    "swa_bf16": dict(B=1, H=20, T=4096, D=64, W=2048, ref="B1 H20 T4096 D64 W2048"),
+    "swa_bf16_450m": dict(B=2, H=20, T=8192, D=64, W=2048, ref="B2 H20 T8192 D64 W2048"),
 }
 DATA = {
     "lognormal_heads": "synthetic (seeded; bf16 N(0,1) x a lognormal(0,1) factor per head)",
@@ -63,6 +70,7 @@ DATA = {
     "randn_fp32": "synthetic (seeded; fp32 N(0,1))",
     "c2": "synthetic (seeded; bf16 x N(0,1) with 0.1% outliers x20; weight N(0,0.02), random init)",
     "c5": "synthetic (seeded; bf16 x N(0,1); every Linear weight N(0,0.02), random init)",
+    "swa_bf16": "synthetic (seeded; bf16 q, k, v, dO ~ N(0,1))",
 }
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on each workload
@@ -390,6 +398,8 @@ def main():
         line = run_gemm(cfg, args)
     elif args.workload == "c5":
         line = run_block(cfg, args)
+    elif args.workload.startswith("swa_bf16"):
+        line = run_swa_bf16(cfg, args)
     else:
         line = run_attention(cfg, args)
     print(json.dumps(line), flush=True)
@@ -518,6 +528,107 @@ def run_block(cfg, args):
                      "traffic": None, "kernel": "whole block (HIP events around each forward)",
                      "kernel_ms": round(ms, 4), "flop_per_launch": flops},
     }
+
+
+def bench_swa_bf16(cfg, steps, warmup):
+    """One training step of the attention op through the C ABI: flw_swa_bf16_fwd (O and the
+    log-sum-exp) then flw_swa_bf16_bwd (Delta, dK/dV, dQ), each timed by its own dispatches."""
+    from flower_amd import _lib
+    lib = _lib.load()
+    B, H, T, D, W = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["W"]
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, T, D, generator=g).to("cuda", torch.bfloat16) for _ in range(4))
+    out = torch.empty_like(q)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    ws = _lib.workspace(lib.flw_swa_bf16_bwd_workspace_bytes(B, H, T, D), q.device)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def fwd():
+        _lib.check(lib.flw_swa_bf16_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), B, H, T, D, W,
+                                        out.data_ptr(), lse.data_ptr(), stream), "fwd")
+
+    def bwd():
+        _lib.check(lib.flw_swa_bf16_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), do.data_ptr(),
+                                        lse.data_ptr(), B, H, T, D, W, dq.data_ptr(), dk.data_ptr(),
+                                        dv.data_ptr(), ws.data_ptr(), ws.numel(), stream), "bwd")
+
+    _spin_up(lambda: (fwd(), bwd()))
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    fev, bev = _events(steps), _events(steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        _arm(lib, fev[i])
+        fwd()
+        _arm(lib, bev[i])
+        bwd()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    f_ms = np.array([a.elapsed_time(b) for a, b in fev])
+    b_ms = np.array([a.elapsed_time(b) for a, b in bev])
+    pairs = B * H * in_window_pairs(T, W)
+    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, fwd_ms=float(f_ms.mean()), fwd_ms_min=float(f_ms.min()),
+                bwd_ms=float(b_ms.mean()), bwd_ms_min=float(b_ms.min()), fwd_flops=4 * D * pairs,
+                bwd_flops=10 * D * pairs)
+
+
+def cpu_baseline_swa_bf16(cfg, budget_s=20.0):
+    """The float64 oracle of the same op (oracle/swa_grad.py: banded forward + log-sum-exp, then
+    the backward) on the host, (b, h) slice by slice until the time budget, scaled linearly."""
+    from threadpoolctl import threadpool_limits
+    from oracle.swa_grad import swa_backward, swa_forward_lse
+    cores = min(16, os.cpu_count() or 1)
+    B, H, T, D, W = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["W"]
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(1, 1, T, D, generator=g).to(torch.bfloat16).double().numpy() for _ in range(4))
+    done, t_total = 0, 0.0
+    with threadpool_limits(cores):
+        while t_total < budget_s and done < B * H:
+            t0 = time.perf_counter()
+            o, lse = swa_forward_lse(q, k, v, W, chunk=512)
+            swa_backward(q, k, v, o, lse, do, W, chunk=512)
+            t_total += time.perf_counter() - t0
+            done += 1
+    flops = 14 * D * done * in_window_pairs(T, W)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{done} of {B * H} (b, h) slices of the same workload in {t_total:.1f} s: oracle "
+                      f"float64 banded forward + log-sum-exp + backward (numpy / multithreaded BLAS), "
+                      f"FLOPs counted as 4*D + 10*D per in-window pair"}
+
+
+def run_swa_bf16(cfg, args):
+    """bf16 sliding-window attention, forward (with log-sum-exp) + backward, one training step.
+    FLOPs per in-window (query, key) pair: forward 4*D (Q K^T, P V), backward 10*D (S recomputed,
+    dP, dV, dK, dQ), as FlashAttention counts them; the dQ kernel's second S / dP (14*D in all) is
+    not counted."""
+    r = bench_swa_bf16(cfg, args.steps, args.warmup)
+    flops = r["fwd_flops"] + r["bwd_flops"]
+    value = flops / (r["ms_per_step"] * 1e-3) / 1e12
+    b_tf = r["bwd_flops"] / (r["bwd_ms"] * 1e-3) / 1e12
+    f_tf = r["fwd_flops"] / (r["fwd_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": "bf16 SWA attention forward+backward TFLOPS (training op), % bf16 MFMA peak",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "spin_up_s": SPIN_UP_S, "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 MFMA, fp32 softmax / accumulate", "data": DATA["swa_bf16"],
+        "config": {"workload": f"swa_attention forward + backward, {cfg['ref']}", "B": cfg["B"], "H": cfg["H"],
+                   "T": cfg["T"], "D": cfg["D"], "window": cfg["W"], "causal": True},
+        "roofline": {"bound": "mfma", "achieved": round(b_tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(b_tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "flw_swa_bf16_bwd (delta + dkdv + dq kernels)", "kernel_ms": round(r["bwd_ms"], 4),
+                     "kernel_ms_min": round(r["bwd_ms_min"], 4), "flop_per_launch": r["bwd_flops"]},
+        "forward": {"bound": "mfma", "achieved": round(f_tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(f_tf / BF16_PEAK_TFLOPS, 4), "kernel": "swa_bf16_fwd_kernel<64>",
+                    "ms": round(r["fwd_ms"], 4), "ms_min": round(r["fwd_ms_min"], 4), "flop_per_launch": r["fwd_flops"]},
+        "fwd_plus_bwd_kernel_ms": round(r["fwd_ms"] + r["bwd_ms"], 4),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_swa_bf16(cfg)
+    return line
 
 
 if __name__ == "__main__":

@@ -582,13 +582,13 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
     FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
     // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per tile.
     const int64_t grid = tiles < compute_units() ? tiles : compute_units();
-    launch_timed(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
+    (void)launch_timed(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
     return check_launch("flw_fp8_scaled_mm");
   }
   p.tiles_n = (int)((N + kGBN - 1) / kGBN);
   const int64_t tiles = (int64_t)p.tiles_n * ((M + kGBM - 1) / kGBM);
   FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
-  launch_timed(reinterpret_cast<const void*>(&fp8_gemm_kernel), dim3((unsigned)tiles), dim3(256), s, p);
+  (void)launch_timed(reinterpret_cast<const void*>(&fp8_gemm_kernel), dim3((unsigned)tiles), dim3(256), s, p);
   return check_launch("flw_fp8_scaled_mm");
 }
 
@@ -613,7 +613,7 @@ static int w8a16_mm(const uint16_t* x, int64_t M, int64_t K, int64_t xs, const u
   const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
   FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
   const int64_t grid = tiles < compute_units() ? tiles : compute_units();
-  launch_timed(reinterpret_cast<const void*>(&w8a16_gemm_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
+  (void)launch_timed(reinterpret_cast<const void*>(&w8a16_gemm_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
   return check_launch("flw_fp8_linear (W8A16)");
 }
 

@@ -499,8 +499,8 @@ static int launch_quant(const QuantParams& p, int ntensors, int dtype, hipStream
                                     : reinterpret_cast<const void*>(&amax_kernel<uint16_t>);
   const void* kq = dtype == FLW_F32 ? reinterpret_cast<const void*>(&quant_kernel<float, MODE>)
                                     : reinterpret_cast<const void*>(&quant_kernel<uint16_t, MODE>);
-  launch_ext(ka, grid, dim3(kThreads), 0, s, p, tm.start, nullptr);
-  launch_ext(kq, grid, dim3(kThreads), lds, s, p, nullptr, tm.stop);
+  (void)launch_ext(ka, grid, dim3(kThreads), 0, s, p, tm.start, nullptr);
+  (void)launch_ext(kq, grid, dim3(kThreads), lds, s, p, nullptr, tm.stop);
   return check_launch(name);
 }
 

@@ -377,7 +377,7 @@ template <int D>
 static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s, Timer tm) {
   const void* k = out_dtype == FLW_F32 ? reinterpret_cast<const void*>(&swa_fwd_kernel<D, float>)
                                        : reinterpret_cast<const void*>(&swa_fwd_kernel<D, uint16_t>);
-  launch_ext(k, grid, dim3(256), 0, s, p, tm.start, tm.stop);
+  (void)launch_ext(k, grid, dim3(256), 0, s, p, tm.start, tm.stop);
 }
 
 static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, const int64_t* kst,

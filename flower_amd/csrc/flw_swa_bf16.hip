@@ -58,30 +58,24 @@ struct SwaB16Params {
   float* delta;           // [B, H, T]
   int H, T, W, nblk, nwg; // nblk: 128-row blocks per (b, h)
   float sm_scale;
+  int64_t rows;           // B * H * T (delta kernel)
 };
 
 // ---------------------------------------------------------------- LDS tile layouts
 //
 // A natural tile: 64 rows x D bf16 (2D bytes per row), 16-byte chunk c of row r at position
-// c ^ swz(r) so that 8 consecutive rows reading the same chunk hit 8 distinct bank groups.
+// c ^ swz(r). The swizzle serves both ways the tile is read:
+//  - ds_read_b128 of one chunk by 16 consecutive rows (nat_frag) hits 16 distinct 16-byte bank
+//    slots of the 256-byte bank space (a row of D = 64 is 128 bytes, so row parity picks the
+//    half and swz must be a permutation over each parity class);
+//  - ds_read_b64_tr_b16 (trr_frag) by a half-wave reads 4 consecutive rows x 64 bytes, which
+//    must land in 4 distinct 64-byte quarters.
+// D = 32 (64-byte rows) gets the quarters from the row address alone.
 template <int D>
 __device__ __forceinline__ int nat_off(int r, int c) {
   if (D == 32) return r * 64 + 16 * (c ^ ((r >> 2) & 3));
-  if (D == 64) return r * 128 + 16 * (c ^ ((r >> 1) & 7));
-  return r * 256 + 16 * (c ^ (r & 7));
-}
-
-// A transposed tile: D rows (the model dimension) x 64 positions (of rows of the source tile)
-// in the k-step order: source row s = 16 g + w goes to position 16 g + perm(w), perm swapping
-// the middle quads ({0-3, 8-11} first, {4-7, 12-15} second), so that lane half h of k-step g
-// reads the 16 bytes at position 16 g + 8 h. 128 bytes per row, chunk c at c ^ ((d >> 1) & 7).
-__device__ __forceinline__ int tr_pos(int s) {
-  const int w = s & 15, q = w >> 2;
-  const int qq = q == 1 ? 2 : (q == 2 ? 1 : q);
-  return (s & ~15) | (qq << 2) | (w & 3);
-}
-__device__ __forceinline__ int tr_off(int d, int pos) {
-  return d * 128 + 16 * ((pos >> 3) ^ ((d >> 1) & 7)) + 2 * (pos & 7);
+  if (D == 64) return r * 128 + 16 * (c ^ ((((r >> 1) & 1) << 2) | ((r >> 2) & 3)));
+  return r * 256 + 16 * (c ^ (((r & 3) << 2) | ((r >> 2) & 3)));
 }
 
 // Global -> registers for one 64-row tile of a (T, D) bf16 slice: 64 * D / 8 chunks of 16 bytes
@@ -108,18 +102,6 @@ struct TileLoad {
       if (i < NCH) *reinterpret_cast<uint4*>(lds + nat_off<D>(i / CPR, i % CPR)) = r[j];
     }
   }
-  __device__ __forceinline__ void store_tr(uint8_t* lds, int tid) const {
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int i = tid + 256 * j;
-      if (i >= NCH) continue;
-      const int pos = tr_pos(i / CPR), d0 = 8 * (i % CPR);
-      const uint32_t w[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<uint16_t*>(lds + tr_off(d0 + e, pos)) = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-    }
-  }
 };
 
 // Fragment of a natural tile for the rows 32 rb .. 32 rb + 31, k-step ks (K = model dim):
@@ -128,10 +110,25 @@ template <int D>
 __device__ __forceinline__ v8bf nat_frag(const uint8_t* lds, int rb, int ks, int lane) {
   return as_v8bf(*reinterpret_cast<const uint4*>(lds + nat_off<D>(32 * rb + (lane & 31), 2 * ks + (lane >> 5))));
 }
-// Fragment of a transposed tile for the dims 32 db .. 32 db + 31, k-step g (K = the 64 rows).
-__device__ __forceinline__ v8bf tr_frag(const uint8_t* lds, int db, int g, int lane) {
-  const int d = 32 * db + (lane & 31);
-  return as_v8bf(*reinterpret_cast<const uint4*>(lds + tr_off(d, 16 * g + 8 * (lane >> 5))));
+// Fragment of a natural tile read transposed, for the dims 32 db .. 32 db + 31 (the MFMA row /
+// column, lane % 32) with K = the tile's 64 rows, k-step g, in the permuted k-step order (lane
+// half h holds rows 16 g + {0-3, 8-11} + 4 h). ds_read_b64_tr_b16 works on groups of 16 lanes:
+// lane 4 j + a supplies the address of 4 consecutive bf16 (row j, dims 4 a .. 4 a + 3 of its
+// group's 16 dims) and lane 4 a + e receives element e of the rows j = 0..3 supplied by lanes
+// a, a + 4, a + 8, a + 12. Two reads (rows 16 g + 4 h + j and 16 g + 8 + 4 h + j) give the 8 values.
+template <int D>
+__device__ __forceinline__ v8bf trr_frag(const uint8_t* lds, int db, int g, int lane) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef short v8s __attribute__((ext_vector_type(8)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  const int s = lane & 15, j = s >> 2, a = s & 3, h = lane >> 5;
+  const int d = 32 * db + 16 * ((lane >> 4) & 1) + 4 * a;
+  const int r = 16 * g + 4 * h + j;
+  const int cb = 2 * (d & 7);
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(lds + nat_off<D>(r, d >> 3) + cb));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(lds + nat_off<D>(r + 8, d >> 3) + cb));
+  const v8s w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(v8bf, w);
 }
 // Fragment of a row of global memory: 8 dims 16 ks + 8 h of row `row` (zero past T).
 template <int D>
@@ -212,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
     tk.load(K, lo, T, tid);
     tv.load(V, lo, T, tid);
     tk.store_nat(lk[0], tid);
-    tv.store_tr(lv[0], tid);
+    tv.store_nat(lv[0], tid);
   }
   __syncthreads();
 
@@ -268,14 +265,14 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
       for (int db = 0; db < NDB; ++db) {
         o[db] *= alpha;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) o[db] = mfma16(tr_frag(lv[buf], db, g, lane), pack_frag(s[g >> 1], g & 1), o[db]);
+        for (int g = 0; g < 4; ++g) o[db] = mfma16(trr_frag<D>(lv[buf], db, g, lane), pack_frag(s[g >> 1], g & 1), o[db]);
       }
     }
     // The other buffer was last read in step j - 1, which every wave finished before the barrier
     // that ended it; one barrier per tile publishes the new tile.
     if (pre) {
       tk.store_nat(lk[buf ^ 1], tid);
-      tv.store_tr(lv[buf ^ 1], tid);
+      tv.store_nat(lv[buf ^ 1], tid);
     }
     __syncthreads();
   }
@@ -303,10 +300,11 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
 
 // Delta[row] = sum_d dO[row, d] * O[row, d] in fp32; D / 8 consecutive lanes per row.
 template <int D>
-__global__ __launch_bounds__(256) void swa_bf16_delta_kernel(const uint16_t* __restrict__ o,
-                                                             const uint16_t* __restrict__ dout,
-                                                             float* __restrict__ delta, int64_t rows) {
+__global__ __launch_bounds__(256) void swa_bf16_delta_kernel(SwaB16Params p) {
   constexpr int LPR = D / 8;                      // lanes per row (8 elements each)
+  const uint16_t* __restrict__ o = p.o;
+  const uint16_t* __restrict__ dout = p.dout;
+  const int64_t rows = p.rows;
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = gid / LPR;
   const int part = (int)(gid % LPR);
@@ -320,18 +318,16 @@ __global__ __launch_bounds__(256) void swa_bf16_delta_kernel(const uint16_t* __r
   }
 #pragma unroll
   for (int w = LPR / 2; w >= 1; w >>= 1) s += __shfl_xor(s, w, 64);
-  if (row < rows && part == 0) delta[row] = s;
+  if (row < rows && part == 0) p.delta[row] = s;
 }
 
 // ---------------------------------------------------------------- backward: dK, dV
 
 template <int D>
-__global__ __launch_bounds__(256, 1) void swa_bf16_dkdv_kernel(SwaB16Params p) {
+__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(SwaB16Params p) {
   constexpr int KS = D / 16, NDB = D / 32, NAT = 64 * D * 2;
-  __shared__ __align__(16) uint8_t lq[2][NAT];     // Q tile, natural (A operand of S)
-  __shared__ __align__(16) uint8_t lqt[2][NAT];    // Q tile, transposed (B operand of dK)
-  __shared__ __align__(16) uint8_t ldo[2][NAT];    // dO tile, natural (A operand of dP)
-  __shared__ __align__(16) uint8_t ldot[2][NAT];   // dO tile, transposed (B operand of dV)
+  __shared__ __align__(16) uint8_t lq[2][NAT];     // Q tile: A operand of S, read transposed for dK
+  __shared__ __align__(16) uint8_t ldo[2][NAT];    // dO tile: A operand of dP, read transposed for dV
   __shared__ __align__(16) float lstat[2][2][64];  // L and Delta of the tile's queries
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, kc = lane & 31;
   const int L = xcd_id(p.nwg);
@@ -376,9 +372,7 @@ __global__ __launch_bounds__(256, 1) void swa_bf16_dkdv_kernel(SwaB16Params p) {
     tq.load(Q, lo, T, tid);
     tdo.load(DO, lo, T, tid);
     tq.store_nat(lq[0], tid);
-    tq.store_tr(lqt[0], tid);
     tdo.store_nat(ldo[0], tid);
-    tdo.store_tr(ldot[0], tid);
     stage_stats(0, lo);
   }
   __syncthreads();
@@ -418,17 +412,15 @@ __global__ __launch_bounds__(256, 1) void swa_bf16_dkdv_kernel(SwaB16Params p) {
           const v8bf pa = pack_frag(s, hs), da = pack_frag(dp, hs);
 #pragma unroll
           for (int db = 0; db < NDB; ++db) {
-            dv[db] = mfma16(pa, tr_frag(ldot[buf], db, 2 * qb + hs, lane), dv[db]);
-            dk[db] = mfma16(da, tr_frag(lqt[buf], db, 2 * qb + hs, lane), dk[db]);
+            dv[db] = mfma16(pa, trr_frag<D>(ldo[buf], db, 2 * qb + hs, lane), dv[db]);
+            dk[db] = mfma16(da, trr_frag<D>(lq[buf], db, 2 * qb + hs, lane), dk[db]);
           }
         }
       }
     }
     if (pre) {
       tq.store_nat(lq[buf ^ 1], tid);
-      tq.store_tr(lqt[buf ^ 1], tid);
       tdo.store_nat(ldo[buf ^ 1], tid);
-      tdo.store_tr(ldot[buf ^ 1], tid);
       stage_stats(buf ^ 1, lo + (j + 1) * 64);
     }
     __syncthreads();
@@ -451,10 +443,9 @@ __global__ __launch_bounds__(256, 1) void swa_bf16_dkdv_kernel(SwaB16Params p) {
 // ---------------------------------------------------------------- backward: dQ
 
 template <int D>
-__global__ __launch_bounds__(256, 1) void swa_bf16_dq_kernel(SwaB16Params p) {
+__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dq_kernel(SwaB16Params p) {
   constexpr int KS = D / 16, NDB = D / 32, NAT = 64 * D * 2;
-  __shared__ __align__(16) uint8_t lk[2][NAT];     // K tile, natural (A operand of S^T)
-  __shared__ __align__(16) uint8_t lkt[2][NAT];    // K tile, transposed (A operand of dQ^T)
+  __shared__ __align__(16) uint8_t lk[2][NAT];     // K tile: A operand of S^T, read transposed for dQ^T
   __shared__ __align__(16) uint8_t lv[2][NAT];     // V tile, natural (A operand of dP^T)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
   const int L = xcd_id(p.nwg);
@@ -492,7 +483,6 @@ __global__ __launch_bounds__(256, 1) void swa_bf16_dq_kernel(SwaB16Params p) {
     tk.load(K, lo, T, tid);
     tv.load(V, lo, T, tid);
     tk.store_nat(lk[0], tid);
-    tk.store_tr(lkt[0], tid);
     tv.store_nat(lv[0], tid);
   }
   __syncthreads();
@@ -527,13 +517,12 @@ __global__ __launch_bounds__(256, 1) void swa_bf16_dq_kernel(SwaB16Params p) {
         for (int hs = 0; hs < 2; ++hs) {
           const v8bf db_ = pack_frag(dp, hs);
 #pragma unroll
-          for (int db = 0; db < NDB; ++db) dq[db] = mfma16(tr_frag(lkt[buf], db, 2 * b + hs, lane), db_, dq[db]);
+          for (int db = 0; db < NDB; ++db) dq[db] = mfma16(trr_frag<D>(lk[buf], db, 2 * b + hs, lane), db_, dq[db]);
         }
       }
     }
     if (pre) {
       tk.store_nat(lk[buf ^ 1], tid);
-      tk.store_tr(lkt[buf ^ 1], tid);
       tv.store_nat(lv[buf ^ 1], tid);
     }
     __syncthreads();
@@ -589,7 +578,7 @@ extern "C" int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int
   const void* kf = D == 32 ? reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<32>)
                  : D == 64 ? reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<64>)
                            : reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<128>);
-  launch_timed(kf, grid, dim3(256), s, p);
+  (void)launch_timed(kf, grid, dim3(256), s, p);
   return check_launch("flw_swa_bf16_fwd");
 }
 
@@ -617,26 +606,26 @@ extern "C" int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, con
   p.nblk = (int)((T + 127) / 128); p.nwg = (int)(B * H * p.nblk);
   p.sm_scale = 1.0f / sqrtf((float)D);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t rows = B * H * T;
-  const int64_t threads = rows * (D / 8);
+  p.rows = B * H * T;
+  const int64_t threads = p.rows * (D / 8);
   const dim3 dgrid((unsigned)((threads + 255) / 256));
-  if (D == 32) hipLaunchKernelGGL(swa_bf16_delta_kernel<32>, dgrid, dim3(256), 0, s, p.o, p.dout, p.delta, rows);
-  else if (D == 64) hipLaunchKernelGGL(swa_bf16_delta_kernel<64>, dgrid, dim3(256), 0, s, p.o, p.dout, p.delta, rows);
-  else hipLaunchKernelGGL(swa_bf16_delta_kernel<128>, dgrid, dim3(256), 0, s, p.o, p.dout, p.delta, rows);
   const dim3 grid((unsigned)p.nwg);
   SwaB16Params pk = p;
   pk.out2 = static_cast<uint16_t*>(dk); pk.out3 = static_cast<uint16_t*>(dv);
   SwaB16Params pq = p;
   pq.out = static_cast<uint16_t*>(dq);
-  if (D == 32) {
-    hipLaunchKernelGGL(swa_bf16_dkdv_kernel<32>, grid, dim3(256), 0, s, pk);
-    hipLaunchKernelGGL(swa_bf16_dq_kernel<32>, grid, dim3(256), 0, s, pq);
-  } else if (D == 64) {
-    hipLaunchKernelGGL(swa_bf16_dkdv_kernel<64>, grid, dim3(256), 0, s, pk);
-    hipLaunchKernelGGL(swa_bf16_dq_kernel<64>, grid, dim3(256), 0, s, pq);
-  } else {
-    hipLaunchKernelGGL(swa_bf16_dkdv_kernel<128>, grid, dim3(256), 0, s, pk);
-    hipLaunchKernelGGL(swa_bf16_dq_kernel<128>, grid, dim3(256), 0, s, pq);
-  }
+  const void* kd = D == 32 ? reinterpret_cast<const void*>(&swa_bf16_delta_kernel<32>)
+                 : D == 64 ? reinterpret_cast<const void*>(&swa_bf16_delta_kernel<64>)
+                           : reinterpret_cast<const void*>(&swa_bf16_delta_kernel<128>);
+  const void* kk = D == 32 ? reinterpret_cast<const void*>(&swa_bf16_dkdv_kernel<32>)
+                 : D == 64 ? reinterpret_cast<const void*>(&swa_bf16_dkdv_kernel<64>)
+                           : reinterpret_cast<const void*>(&swa_bf16_dkdv_kernel<128>);
+  const void* kq = D == 32 ? reinterpret_cast<const void*>(&swa_bf16_dq_kernel<32>)
+                 : D == 64 ? reinterpret_cast<const void*>(&swa_bf16_dq_kernel<64>)
+                           : reinterpret_cast<const void*>(&swa_bf16_dq_kernel<128>);
+  const Timer tm = take_timer();   // start on the delta kernel, stop on the dQ kernel
+  (void)launch_ext(kd, dgrid, dim3(256), 0, s, p, tm.start, nullptr);
+  (void)launch_ext(kk, grid, dim3(256), 0, s, pk, nullptr, nullptr);
+  (void)launch_ext(kq, grid, dim3(256), 0, s, pq, nullptr, tm.stop);
   return check_launch("flw_swa_bf16_bwd");
 }
