@@ -79,27 +79,34 @@ __device__ __forceinline__ int nat_off(int r, int c) {
 }
 
 // Global -> registers for one 64-row tile of a (T, D) bf16 slice: 64 * D / 8 chunks of 16 bytes
-// over 256 threads. Rows past T read as zero.
+// over 256 threads (a whole number of chunks per thread for D = 32 / 64 / 128), through a buffer
+// descriptor covering the slice's T rows, so rows past T read as zero with no compare. The row
+// offset goes into the VGPR offset, which the descriptor's range check covers.
+constexpr int kBufferFlags = 0x00020000;   // buffer descriptor word 3 for raw dword access (gfx9)
+
 template <int D>
 struct TileLoad {
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int NCH = 64 * CPR;
-  static constexpr int CPT = (NCH + 255) / 256;
+  static constexpr int CPT = 64 * CPR / 256;        // chunks per thread
+  static_assert(CPT * 256 == 64 * CPR, "whole chunks per thread");
+  __amdgpu_buffer_rsrc_t rs;
   uint4 r[CPT];
-  __device__ __forceinline__ void load(const uint16_t* base, int row0, int T, int tid) {
+  __device__ __forceinline__ void init(const uint16_t* base, int T) {
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, T * D * 2, kBufferFlags);
+  }
+  __device__ __forceinline__ void load(int row0, int tid) {
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int i = tid + 256 * j;
-      const int row = row0 + i / CPR, c = i % CPR;
-      r[j] = (i < NCH && row < T) ? *reinterpret_cast<const uint4*>(base + (int64_t)row * D + 8 * c)
-                                  : make_uint4(0, 0, 0, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (row0 + i / CPR) * (2 * D) + 16 * (i % CPR), 0, 0);
+      r[j] = make_uint4(v[0], v[1], v[2], v[3]);
     }
   }
   __device__ __forceinline__ void store_nat(uint8_t* lds, int tid) const {
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int i = tid + 256 * j;
-      if (i < NCH) *reinterpret_cast<uint4*>(lds + nat_off<D>(i / CPR, i % CPR)) = r[j];
+      *reinterpret_cast<uint4*>(lds + nat_off<D>(i / CPR, i % CPR)) = r[j];
     }
   }
 };
@@ -160,6 +167,15 @@ __device__ __forceinline__ float psum_pair(float x) {
 // Element v of a 32x32 C block held by lane (col, h) is row 8 (v / 4) + 4 h + v % 4.
 __device__ __forceinline__ int crow(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
+// Before a tile loop: every load issued so far (this lane's own row fragments, the first
+// tile) has landed, and the first tile is published. Without the explicit wait the compiler's
+// wait-count placement, merging the path that skips the first tile, would wait inside the loop
+// for the row fragments and with them for the next tile's prefetch, every iteration.
+__device__ __forceinline__ void wait_all_loads() {
+  __builtin_amdgcn_s_waitcnt(0);   // vmcnt(0) expcnt(0) lgkmcnt(0)
+  __syncthreads();
+}
+
 // XCD-contiguous work numbering (as in the FP8 kernel).
 __device__ __forceinline__ int xcd_id(int nwg) {
   int L = (int)blockIdx.x;
@@ -176,7 +192,7 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
   constexpr int NAT = 64 * D * 2;                 // bytes of a natural / transposed tile
   __shared__ __align__(16) uint8_t lk[2][NAT];
   __shared__ __align__(16) uint8_t lv[2][NAT];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, qc = lane & 31;
   const int L = xcd_id(p.nwg);
   const int bh = L / p.nblk, mt = L % p.nblk;
   const int T = p.T, W = p.W;
@@ -205,20 +221,22 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
   float m_run = -INFINITY, l_run = 0.0f;
 
   TileLoad<D> tk, tv;
+  tk.init(K, T);
+  tv.init(V, T);
   if (nt > 0) {
-    tk.load(K, lo, T, tid);
-    tv.load(V, lo, T, tid);
+    tk.load(lo, tid);
+    tv.load(lo, tid);
     tk.store_nat(lk[0], tid);
     tv.store_nat(lv[0], tid);
   }
-  __syncthreads();
+  wait_all_loads();
 
   for (int j = 0; j < nt; ++j) {
     const int buf = j & 1;
     const bool pre = j + 1 < nt;
     if (pre) {
-      tk.load(K, lo + (j + 1) * 64, T, tid);
-      tv.load(V, lo + (j + 1) * 64, T, tid);
+      tk.load(lo + (j + 1) * 64, tid);
+      tv.load(lo + (j + 1) * 64, tid);
     }
     if (j >= ta && j <= tb) {
       const int n0 = lo + 64 * j;
@@ -328,15 +346,13 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
   constexpr int KS = D / 16, NDB = D / 32, NAT = 64 * D * 2;
   __shared__ __align__(16) uint8_t lq[2][NAT];     // Q tile: A operand of S, read transposed for dK
   __shared__ __align__(16) uint8_t ldo[2][NAT];    // dO tile: A operand of dP, read transposed for dV
-  __shared__ __align__(16) float lstat[2][2][64];  // L and Delta of the tile's queries
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, kc = lane & 31;
+  __shared__ __align__(16) float lstat[2][2][64];  // -L log2(e) and Delta of the tile's queries
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, kc = lane & 31;
   const int L = xcd_id(p.nwg);
   const int bh = L / p.nblk, nt0 = L % p.nblk;
   const int T = p.T, W = p.W;
   const int k0w = nt0 * 128, k0 = k0w + 32 * wave;     // this wave's 32 keys
   const int64_t slice = (int64_t)bh * T * D;
-  const uint16_t* Q = p.q + slice;
-  const uint16_t* DO = p.dout + slice;
   const float* LSE = p.lse + (int64_t)bh * T;
   const float* DLT = p.delta + (int64_t)bh * T;
   const float c = p.sm_scale * kLog2eB;
@@ -361,28 +377,46 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
   const int ta = k0 < T ? (k0 - lo) / 64 : 1;
   const int tb = k0 < T ? (wq1 - lo) / 64 : 0;
 
+  // Queries past T: Q and dO load as zeros and their L / Delta stage as zeros, so P = 1,
+  // dS = 1 * (0 - 0) = 0 and P^T dO = 0: they add nothing, without a compare. Keys past T are
+  // computed on zeros and never stored. Only the band 0 <= i - j < W is masked, and only in
+  // the 32 x 32 blocks it cuts.
   TileLoad<D> tq, tdo;
-  auto stage_stats = [&](int buf, int r0) __attribute__((always_inline)) {
-    if (tid < 128) {
-      const int i = tid & 63, r = r0 + i;
-      lstat[buf][tid >> 6][i] = r < T ? (tid < 64 ? LSE[r] : DLT[r]) : 0.0f;
-    }
+  tq.init(p.q + slice, T);
+  tdo.init(p.dout + slice, T);
+  // Wave 0 carries L of the tile's 64 queries (stored as -L log2(e)), wave 1 their Delta; both
+  // through buffer descriptors over the slice's T values, so queries past T read as 0.
+  const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(LSE), 0, T * 4, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(DLT), 0, T * 4, kBufferFlags);
+  auto load_stat = [&](int r0) __attribute__((always_inline)) {
+    float x = 0.0f;
+    if (wave == 0) x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(lrs, 4 * (r0 + lane), 0, 0));
+    else if (wave == 1) x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(drs, 4 * (r0 + lane), 0, 0));
+    return x;
   };
+  auto store_stat = [&](int buf, float x) __attribute__((always_inline)) {
+    if (wave == 0) lstat[buf][0][lane] = -x * kLog2eB;
+    else if (wave == 1) lstat[buf][1][lane] = x;
+  };
+  float st = 0.0f;
   if (nt > 0) {
-    tq.load(Q, lo, T, tid);
-    tdo.load(DO, lo, T, tid);
+    tq.load(lo, tid);
+    tdo.load(lo, tid);
+    st = load_stat(lo);
     tq.store_nat(lq[0], tid);
     tdo.store_nat(ldo[0], tid);
-    stage_stats(0, lo);
+    store_stat(0, st);
   }
-  __syncthreads();
+  wait_all_loads();
 
+  const int key = k0 + kc;
   for (int j = 0; j < nt; ++j) {
     const int buf = j & 1;
     const bool pre = j + 1 < nt;
     if (pre) {
-      tq.load(Q, lo + (j + 1) * 64, T, tid);
-      tdo.load(DO, lo + (j + 1) * 64, T, tid);
+      tq.load(lo + (j + 1) * 64, tid);
+      tdo.load(lo + (j + 1) * 64, tid);
+      st = load_stat(lo + (j + 1) * 64);
     }
     if (j >= ta && j <= tb) {
       const int r0 = lo + 64 * j;                    // first query of the tile
@@ -395,16 +429,26 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
           s = mfma16(nat_frag<D>(lq[buf], qb, ks, lane), kf[ks], s);
           dp = mfma16(nat_frag<D>(ldo[buf], qb, ks, lane), vf[ks], dp);
         }
-        const int key = k0 + kc;
+        const int q0b = r0 + 32 * qb;
+        if (!(q0b >= k0 + 31 && q0b + 31 - k0 < W)) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int ql = 32 * qb + crow(v, h), qi = r0 + ql;
-          const int dd = qi - key;
-          const bool ok = dd >= 0 && dd < W && qi < T && key < T;
-          const float lse2 = lstat[buf][0][ql] * kLog2eB;
-          const float pr = ok ? __builtin_amdgcn_exp2f(fmaf(s[v], c, -lse2)) : 0.0f;
-          s[v] = pr;
-          dp[v] = pr * (dp[v] - lstat[buf][1][ql]) * p.sm_scale;
+          for (int v = 0; v < 16; ++v)
+            if ((unsigned)(q0b + crow(v, h) - key) >= (unsigned)W) s[v] = -INFINITY;
+        }
+        // Rows crow(4 i + e, h) = 8 i + 4 h + e: four consecutive stats per i.
+        const float4* nl4 = reinterpret_cast<const float4*>(&lstat[buf][0][32 * qb + 4 * h]);
+        const float4* dl4 = reinterpret_cast<const float4*>(&lstat[buf][1][32 * qb + 4 * h]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 nl = nl4[2 * i], dl = dl4[2 * i];
+          const float nla[4] = {nl.x, nl.y, nl.z, nl.w}, dla[4] = {dl.x, dl.y, dl.z, dl.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int v = 4 * i + e;
+            const float pr = __builtin_amdgcn_exp2f(fmaf(s[v], c, nla[e]));
+            s[v] = pr;
+            dp[v] = pr * (dp[v] - dla[e]);           // dS / sm_scale
+          }
         }
         // dV += P^T dO, dK += dS^T Q: A = this lane's key row, K = the 32 queries of block qb.
 #pragma unroll
@@ -421,21 +465,21 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
     if (pre) {
       tq.store_nat(lq[buf ^ 1], tid);
       tdo.store_nat(ldo[buf ^ 1], tid);
-      stage_stats(buf ^ 1, lo + (j + 1) * 64);
+      store_stat(buf ^ 1, st);
     }
     __syncthreads();
   }
 
   // The A operands' rows were keys, the B operands' columns dims: lane (dim 32 db + lane % 32)
-  // holds dK / dV of the keys k0 + crow(v, h).
+  // holds dK / dV of the keys k0 + crow(v, h). dK carries the softmax scale left out of dS.
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int key = k0 + crow(v, h), d = 32 * db + kc;
-      if (key < T) {
-        p.out2[slice + (int64_t)key * D + d] = (uint16_t)f32_to_bf16_bits(dk[db][v]);
-        p.out3[slice + (int64_t)key * D + d] = (uint16_t)f32_to_bf16_bits(dv[db][v]);
+      const int kr = k0 + crow(v, h), d = 32 * db + kc;
+      if (kr < T) {
+        p.out2[slice + (int64_t)kr * D + d] = (uint16_t)f32_to_bf16_bits(dk[db][v] * p.sm_scale);
+        p.out3[slice + (int64_t)kr * D + d] = (uint16_t)f32_to_bf16_bits(dv[db][v]);
       }
     }
 }
@@ -447,7 +491,7 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dq_kernel(SwaB
   constexpr int KS = D / 16, NDB = D / 32, NAT = 64 * D * 2;
   __shared__ __align__(16) uint8_t lk[2][NAT];     // K tile: A operand of S^T, read transposed for dQ^T
   __shared__ __align__(16) uint8_t lv[2][NAT];     // V tile, natural (A operand of dP^T)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, qc = lane & 31;
   const int L = xcd_id(p.nwg);
   const int bh = L / p.nblk, mt = L % p.nblk;
   const int T = p.T, W = p.W;
@@ -457,7 +501,7 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dq_kernel(SwaB
   const uint16_t* V = p.v + slice;
   const float c = p.sm_scale * kLog2eB;
   const int qi = q0 + qc;
-  const float lse2 = qi < T ? p.lse[(int64_t)bh * T + qi] * kLog2eB : 0.0f;
+  const float nlse2 = qi < T ? -p.lse[(int64_t)bh * T + qi] * kLog2eB : 0.0f;
   const float dl = qi < T ? p.delta[(int64_t)bh * T + qi] : 0.0f;
 
   v8bf qf[KS], df[KS];
@@ -479,20 +523,22 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dq_kernel(SwaB
   const int tb = q0 < T ? (wk1 - lo) / 64 : 0;
 
   TileLoad<D> tk, tv;
+  tk.init(K, T);
+  tv.init(V, T);
   if (nt > 0) {
-    tk.load(K, lo, T, tid);
-    tv.load(V, lo, T, tid);
+    tk.load(lo, tid);
+    tv.load(lo, tid);
     tk.store_nat(lk[0], tid);
     tv.store_nat(lv[0], tid);
   }
-  __syncthreads();
+  wait_all_loads();
 
   for (int j = 0; j < nt; ++j) {
     const int buf = j & 1;
     const bool pre = j + 1 < nt;
     if (pre) {
-      tk.load(K, lo + (j + 1) * 64, T, tid);
-      tv.load(V, lo + (j + 1) * 64, T, tid);
+      tk.load(lo + (j + 1) * 64, tid);
+      tv.load(lo + (j + 1) * 64, tid);
     }
     if (j >= ta && j <= tb) {
       const int n0 = lo + 64 * j;
@@ -504,13 +550,18 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dq_kernel(SwaB
           s = mfma16(nat_frag<D>(lk[buf], b, ks, lane), qf[ks], s);
           dp = mfma16(nat_frag<D>(lv[buf], b, ks, lane), df[ks], dp);
         }
+        // Keys past T are zeros (S = 0, dP = 0) and meet K^T = 0 in dQ: no compare needed for
+        // them; queries past T are never stored. Only the band 0 <= i - j < W is masked.
+        const int kb0 = n0 + 32 * b;
+        if (!(q0 >= kb0 + 31 && q0 + 31 - kb0 < W)) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            if ((unsigned)(qi - kb0 - crow(v, h)) >= (unsigned)W) s[v] = -INFINITY;
+        }
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int key = n0 + 32 * b + crow(v, h);
-          const int dd = qi - key;
-          const bool ok = dd >= 0 && dd < W && qi < T && key < T;
-          const float pr = ok ? __builtin_amdgcn_exp2f(fmaf(s[v], c, -lse2)) : 0.0f;
-          dp[v] = pr * (dp[v] - dl) * p.sm_scale;
+          const float pr = __builtin_amdgcn_exp2f(fmaf(s[v], c, nlse2));
+          dp[v] = pr * (dp[v] - dl);                  // dS / sm_scale
         }
         // dQ^T += K^T dS^T: A = K^T (dims as rows, keys of block b as K), B = dS^T (this lane's query).
 #pragma unroll
@@ -536,8 +587,8 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dq_kernel(SwaB
       for (int j = 0; j < 4; ++j) {
         const int d = 32 * db + 8 * j + 4 * h;
         uint2 w;
-        w.x = pk_bf16(dq[db][4 * j], dq[db][4 * j + 1]);
-        w.y = pk_bf16(dq[db][4 * j + 2], dq[db][4 * j + 3]);
+        w.x = pk_bf16(dq[db][4 * j] * p.sm_scale, dq[db][4 * j + 1] * p.sm_scale);
+        w.y = pk_bf16(dq[db][4 * j + 2] * p.sm_scale, dq[db][4 * j + 3] * p.sm_scale);
         *reinterpret_cast<uint2*>(op + d) = w;
       }
   }
