@@ -77,7 +77,7 @@ DATA = {
 # (summaries under profiles/). FETCH_SIZE is scaled by 2.0: a plain 256 MiB device copy reads back
 # 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0).
 TRAFFIC = {
-    "c3": {"swa_fwd": 167_979_008, "quant": 503_929_856},
+    "c3": {"swa_fwd": 167_982_080, "quant": 504_024_064},
     "c2": {"gemm": 120_440_320, "w8a16": 136_010_752},
 }
 
