@@ -79,6 +79,7 @@ DATA = {
 TRAFFIC = {
     "c3": {"swa_fwd": 167_982_080, "quant": 504_024_064},
     "c2": {"gemm": 120_440_320, "w8a16": 136_010_752},
+    "swa_bf16_450m": {"bwd": 554_757_120, "fwd": 169_459_712},
 }
 
 
@@ -618,11 +619,13 @@ def run_swa_bf16(cfg, args):
         "config": {"workload": f"swa_attention forward + backward, {cfg['ref']}", "B": cfg["B"], "H": cfg["H"],
                    "T": cfg["T"], "D": cfg["D"], "window": cfg["W"], "causal": True},
         "roofline": {"bound": "mfma", "achieved": round(b_tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(b_tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(b_tf / BF16_PEAK_TFLOPS, 4),
+                     "traffic": TRAFFIC.get(args.workload, {}).get("bwd"),
                      "kernel": "flw_swa_bf16_bwd (delta + dkdv + dq kernels)", "kernel_ms": round(r["bwd_ms"], 4),
                      "kernel_ms_min": round(r["bwd_ms_min"], 4), "flop_per_launch": r["bwd_flops"]},
         "forward": {"bound": "mfma", "achieved": round(f_tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(f_tf / BF16_PEAK_TFLOPS, 4), "kernel": "swa_bf16_fwd_kernel<64>",
+                    "traffic": TRAFFIC.get(args.workload, {}).get("fwd"),
                     "ms": round(r["fwd_ms"], 4), "ms_min": round(r["fwd_ms_min"], 4), "flop_per_launch": r["fwd_flops"]},
         "fwd_plus_bwd_kernel_ms": round(r["fwd_ms"] + r["bwd_ms"], 4),
     }
