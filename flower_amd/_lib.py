@@ -16,7 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflower_amd.so")
 
 F32, BF16 = 0, 1
-SCALE_TENSOR, SCALE_HEAD, SCALE_BH = 0, 1, 2
+SCALE_TENSOR, SCALE_HEAD, SCALE_BH, SCALE_COLUMN = 0, 1, 2, 3
 LAYOUT_BHTD, LAYOUT_VTILE = 0, 1
 GEMM_A8W8, GEMM_W8A16 = 0, 1
 
@@ -41,6 +41,9 @@ SIGNATURES = {
                                     c_void_p]),
     "flw_quant_rows_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                     c_void_p]),
+    "flw_quant_cols_workspace_bytes": (c_size_t, [c_int64, c_int64]),
+    "flw_quant_cols_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int, c_void_p, c_int64,
+                                    c_void_p, c_void_p, c_size_t, c_void_p]),
     "flw_rmsnorm_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p,
                                             c_void_p, c_void_p, c_void_p]),
     "flw_gelu_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,

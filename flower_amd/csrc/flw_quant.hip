@@ -335,6 +335,159 @@ __global__ __launch_bounds__(kThreads) void rows_quant_kernel(const T* __restric
   }
 }
 
+// ---------------------------------------------------------------- column quantiser, transposed out
+//
+// The operands of the FP8 backward GEMMs: for a [rows, cols] matrix (activations x, output
+// gradient g, or a weight) the e4m3 codes of each COLUMN, written transposed as out_t[cols, ld]
+// (ld >= rows, rows past `rows` coded 0), so that the reduction over rows becomes the contiguous
+// K dimension of the "TN" FP8 GEMM. Scales:
+//   per column (FLW_SCALE_COLUMN): the _fp8_head recipe on the column, s = max(amax / 448, 1e-12),
+//     code = e4m3(x / s) (flw_quant_rows_e4m3 applied to the transpose);
+//   per tensor (FLW_SCALE_TENSOR): the _per_tensor_fp8 recipe, s = max(amax, 1e-12) / 448,
+//     code = e4m3(clamp(x / s, -448, 448)) (flw_quant_e4m3's codes, transposed).
+// Pass 1 (cols_amax_kernel) writes one |x| max per 64 columns x 256 rows tile and column (per tile
+// in tensor mode); pass 2 (cols_quant_t_kernel) folds the partials of its columns, quantises its
+// 256 x 64 tile and transposes it through LDS so that every output row segment is written with
+// 16-byte stores. A thread covers 8 rows x 8 columns (8 rows of one column pack into 8 bytes).
+constexpr int kCT = 64, kRT = 256;               // tile: kRT rows x kCT columns
+constexpr int kCTStride = kRT + 8;               // LDS bytes per transposed column (bank spread)
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* src, float* f) {
+  if constexpr (sizeof(T) == 2) {
+    Vec16<uint16_t>::load(src, f);
+  } else {
+    Vec16<float>::load(src, f);
+    Vec16<float>::load(src + 4, f + 4);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void load_tile8(const T* x, int64_t rows, int64_t cols, int64_t rs, int64_t r0,
+                                           int64_t c0, float (&f)[8][8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = r0 + i;
+    if (r < rows && c0 < cols) {
+      load8(x + r * rs + c0, f[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[i][j] = 0.0f;
+    }
+  }
+}
+
+template <typename T, bool TENSOR>
+__global__ __launch_bounds__(kThreads) void cols_amax_kernel(const T* __restrict__ x, int64_t rows,
+                                                             int64_t cols, int64_t rs,
+                                                             uint32_t* __restrict__ partials) {
+  __shared__ uint32_t red[kThreads / 8][kCT + 1];
+  const int t = threadIdx.x, cg = t & 7, rg = t >> 3;
+  const int64_t c0 = (int64_t)blockIdx.x * kCT + 8 * cg;
+  const int64_t r0 = (int64_t)blockIdx.y * kRT + 8 * rg;
+  float f[8][8];
+  load_tile8(x, rows, cols, rs, r0, c0, f);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { const uint32_t a = abs_bits(f[i][j]); m = m > a ? m : a; }
+    red[rg][8 * cg + j] = m;
+  }
+  __syncthreads();
+  if (t < kCT) {
+    uint32_t m = 0;
+    for (int g = 0; g < kThreads / 8; ++g) m = m > red[g][t] ? m : red[g][t];
+    if (TENSOR) {
+      m = wave_max_u32(m);
+      if (t == 0) partials[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = m;
+    } else if ((int64_t)blockIdx.x * kCT + t < cols) {
+      partials[(int64_t)blockIdx.y * cols + (int64_t)blockIdx.x * kCT + t] = m;
+    }
+  }
+}
+
+template <typename T, bool TENSOR>
+__global__ __launch_bounds__(kThreads) void cols_quant_t_kernel(const T* __restrict__ x, int64_t rows,
+                                                                int64_t cols, int64_t rs,
+                                                                const uint32_t* __restrict__ partials,
+                                                                int64_t nchunks, int64_t ncb,
+                                                                uint8_t* __restrict__ out, int64_t ld,
+                                                                float* __restrict__ scale_out) {
+  __shared__ __align__(16) uint8_t lt[kCT * kCTStride];
+  __shared__ float sc[kCT], rc[kCT];
+  __shared__ uint32_t red[kThreads / 64];
+  const int t = threadIdx.x, cg = t & 7, rg = t >> 3;
+  const int64_t cb0 = (int64_t)blockIdx.x * kCT;
+  // Scales of this tile's columns.
+  if (TENSOR) {
+    uint32_t m = 0;
+    for (int64_t i = t; i < nchunks * ncb; i += kThreads) m = m > partials[i] ? m : partials[i];
+    m = block_max_u32(m, red);
+    const float amax = __uint_as_float(m);
+    const float s = (amax < kEps ? kEps : amax) / kE4m3Max;
+    if (t < kCT) { sc[t] = s; rc[t] = 1.0f / s; }
+    if (blockIdx.x == 0 && blockIdx.y == 0 && t == 0) scale_out[0] = s;
+  } else if (t < kCT) {
+    const int64_t c = cb0 + t;
+    uint32_t m = 0;
+    if (c < cols)
+      for (int64_t k = 0; k < nchunks; ++k) m = m > partials[k * cols + c] ? m : partials[k * cols + c];
+    const float amax = __uint_as_float(m);
+    float s = amax / kE4m3Max;
+    s = s < kEps ? kEps : s;
+    sc[t] = s;
+    rc[t] = 1.0f / s;
+    if (blockIdx.y == 0 && c < cols) scale_out[c] = s;
+  }
+  __syncthreads();
+
+  const int64_t c0 = cb0 + 8 * cg;
+  const int64_t r0 = (int64_t)blockIdx.y * kRT + 8 * rg;
+  float f[8][8];
+  load_tile8(x, rows, cols, rs, r0, c0, f);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int cj = 8 * cg + j;
+    const float s = sc[cj], r = rc[cj];
+    float col[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) col[i] = f[i][j];
+    uint32_t w[2];
+    if (__builtin_isfinite(s * kE4m3Max) && __builtin_isfinite(r)) {
+      codes_of<8>(col, s, r, true, w);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float q = col[4 * h + e] / s;
+          c |= (f32_to_e4m3(TENSOR ? clamp448(q) : q) & 0xFFu) << (8 * e);
+        }
+        w[h] = c;
+      }
+    }
+    *reinterpret_cast<uint2*>(lt + cj * kCTStride + 8 * rg) = make_uint2(w[0], w[1]);
+  }
+  __syncthreads();
+  // Store: thread t writes column t / 4, rows 64 (t % 4) .. + 63 of the tile, as 4 x 16 bytes.
+  const int cl = t >> 2, part = t & 3;
+  const int64_t c = cb0 + cl;
+  if (c < cols) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int rr = 64 * part + 16 * q;
+      const int64_t r = (int64_t)blockIdx.y * kRT + rr;
+      if (r < ld) {
+        const uint2 a = *reinterpret_cast<const uint2*>(lt + cl * kCTStride + rr);
+        const uint2 b = *reinterpret_cast<const uint2*>(lt + cl * kCTStride + rr + 8);
+        *reinterpret_cast<uint4*>(out + c * ld + r) = make_uint4(a.x, a.y, b.x, b.y);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- activation + per-row quantiser
 //
 // The producer of an FP8 linear's input fused with its per-row quantiser (flw_quant_rows_e4m3
@@ -638,6 +791,54 @@ extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64
     hipLaunchKernelGGL(rows_quant_kernel<uint16_t>, grid, dim3(kThreads), 0, s,
                        static_cast<const uint16_t*>(x), rows, cols, row_stride, out, scale_out);
   return check_launch("flw_quant_rows_e4m3");
+}
+
+extern "C" size_t flw_quant_cols_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const int64_t nchunks = (rows + kRT - 1) / kRT, ncb = (cols + kCT - 1) / kCT;
+  return (size_t)(nchunks * (cols > ncb ? cols : ncb)) * sizeof(uint32_t);
+}
+
+extern "C" int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                                   int granularity, uint8_t* out_t, int64_t ld, float* scale_out,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  FLW_REQUIRE(x != nullptr && out_t != nullptr && scale_out != nullptr, FLW_E_INVALID, "null pointer");
+  FLW_REQUIRE(dtype == FLW_F32 || dtype == FLW_BF16, FLW_E_UNSUPPORTED, "dtype %d not supported", dtype);
+  FLW_REQUIRE(granularity == FLW_SCALE_TENSOR || granularity == FLW_SCALE_COLUMN, FLW_E_INVALID,
+              "granularity must be FLW_SCALE_TENSOR or FLW_SCALE_COLUMN");
+  FLW_REQUIRE(rows > 0 && cols > 0, FLW_E_INVALID, "empty matrix");
+  FLW_REQUIRE(cols % 8 == 0 && row_stride % 8 == 0 && row_stride >= cols, FLW_E_INVALID,
+              "cols and row_stride must be multiples of 8");
+  const int64_t esz = dtype == FLW_F32 ? 4 : 2;
+  FLW_REQUIRE(((uintptr_t)x & 15) == 0 && (row_stride * esz) % 16 == 0, FLW_E_INVALID, "rows must be 16-byte aligned");
+  FLW_REQUIRE(ld >= rows && ld % 16 == 0 && ((uintptr_t)out_t & 15) == 0, FLW_E_INVALID,
+              "ld must be >= rows and a multiple of 16, out_t 16-byte aligned");
+  const int64_t nchunks = (rows + kRT - 1) / kRT, ncb = (cols + kCT - 1) / kCT;
+  const int64_t oy = (ld + kRT - 1) / kRT;
+  FLW_REQUIRE(ncb <= 0x7FFFFFFF && oy <= 65535, FLW_E_UNSUPPORTED, "matrix too large");
+  const size_t need = flw_quant_cols_workspace_bytes(rows, cols);
+  FLW_REQUIRE(workspace != nullptr && workspace_bytes >= need, FLW_E_WORKSPACE, "workspace needs %zu bytes", need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* part = static_cast<uint32_t*>(workspace);
+  const dim3 g1((unsigned)ncb, (unsigned)nchunks), g2((unsigned)ncb, (unsigned)oy);
+  const bool tensor = granularity == FLW_SCALE_TENSOR;
+#define FLW_COLS(T)                                                                                        \
+  do {                                                                                                     \
+    const T* xt = static_cast<const T*>(x);                                                                \
+    if (tensor) {                                                                                          \
+      hipLaunchKernelGGL((cols_amax_kernel<T, true>), g1, dim3(kThreads), 0, s, xt, rows, cols, row_stride, part); \
+      hipLaunchKernelGGL((cols_quant_t_kernel<T, true>), g2, dim3(kThreads), 0, s, xt, rows, cols, row_stride,    \
+                         part, nchunks, ncb, out_t, ld, scale_out);                                         \
+    } else {                                                                                               \
+      hipLaunchKernelGGL((cols_amax_kernel<T, false>), g1, dim3(kThreads), 0, s, xt, rows, cols, row_stride, part); \
+      hipLaunchKernelGGL((cols_quant_t_kernel<T, false>), g2, dim3(kThreads), 0, s, xt, rows, cols, row_stride,   \
+                         part, nchunks, ncb, out_t, ld, scale_out);                                         \
+    }                                                                                                      \
+  } while (0)
+  if (dtype == FLW_F32) FLW_COLS(float);
+  else FLW_COLS(uint16_t);
+#undef FLW_COLS
+  return check_launch("flw_quant_cols_e4m3");
 }
 
 template <int ACT>

@@ -10,7 +10,13 @@ Mirrors flower/precision.py (the torchao-based FP8 conversion) with this build's
     activation scales; "tensorwise": one weight scale and one activation scale; "weight_only":
     per-output-channel e4m3 weights times the bf16 activations as they are (W8A16: the weight is
     widened to bf16 in the kernel, bf16 MFMA; needs K % 64 == 0).
-    Backward (not on the FP8 path) is the bf16 matmul pair grad_x = g W, grad_W = g^T x.
+    Backward ("rowwise" / "tensorwise", as torchao's Float8Linear does under
+    ``training.fp8_linear``): both gradient GEMMs in FP8 on the same kernel —
+    dgrad  grad_x = g W:    per-row e4m3 g (per tensor for "tensorwise") x the weight's per-column
+                            e4m3 codes stored transposed (cached with the forward codes);
+    wgrad  grad_W = g^T x:  per-column e4m3 of g and of x (the token axis becomes the contiguous
+                            reduction), written transposed by flw_quant_cols_e4m3.
+    "weight_only" (and ``backward_fp8 = False``) keeps the bf16 matmul pair.
 ``convert_model_to_fp8`` / ``maybe_convert_fp8`` -- precision.py:134-195, 356-381.
 ``fp8_weight_cache``   -- precision.py:198-353: quantise every FP8 weight ONCE on entry, patch
     the layers' forwards to reuse it across grad-accumulation microsteps, restore the forwards
@@ -85,6 +91,92 @@ def quantize_weight(weight: torch.Tensor, recipe: str = "rowwise"):
     return w8, scale
 
 
+def quantize_cols(x2: torch.Tensor, granularity: str, ld: int | None = None):
+    """(codes_t [C, ld] uint8, scale float32 [C] or [1]): e4m3 of each column of x2 [R, C] (bf16 or
+    fp32, rows contiguous), transposed; rows past R up to ld (a multiple of 16) are coded 0."""
+    lib = _lib.load()
+    _lib.require_gpu(x2)
+    if x2.dtype not in (torch.float32, torch.bfloat16):
+        x2 = x2.to(torch.bfloat16)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    R, C = x2.shape
+    ld = ((R + 15) // 16) * 16 if ld is None else ld
+    gran = _lib.SCALE_COLUMN if granularity == "column" else _lib.SCALE_TENSOR
+    out = torch.empty((C, ld), dtype=torch.uint8, device=x2.device)
+    scale = torch.empty(C if gran == _lib.SCALE_COLUMN else 1, dtype=torch.float32, device=x2.device)
+    ws = _lib.workspace(lib.flw_quant_cols_workspace_bytes(R, C), x2.device)
+    rc = lib.flw_quant_cols_e4m3(x2.data_ptr(), _lib.dtype_code(x2.dtype), R, C, x2.stride(0), gran,
+                                 out.data_ptr(), ld, scale.data_ptr(), ws.data_ptr(), ws.numel(),
+                                 _lib.stream_of(x2))
+    _lib.check(rc, "quantize_cols")
+    return out, scale
+
+
+def quantize_weight_cols(weight: torch.Tensor, recipe: str = "rowwise"):
+    """The weight's codes for dgrad: (w8c [K, N] = per-column e4m3 of W [N, K], transposed;
+    scales [K] ("rowwise") or [1] ("tensorwise"))."""
+    w = weight.detach()
+    return quantize_cols(w, "column" if recipe == "rowwise" else "tensor", ld=w.shape[0])
+
+
+def _quantize_rows(x2: torch.Tensor, recipe: str):
+    """(x8 [M, K], scale [M] or [1]) of a contiguous bf16 / fp32 matrix, per row ("rowwise") or
+    per tensor ("tensorwise")."""
+    lib = _lib.load()
+    M, K = x2.shape
+    x8 = torch.empty((M, K), dtype=torch.uint8, device=x2.device)
+    stream = _lib.stream_of(x2)
+    if recipe == "rowwise":
+        sx = torch.empty(M, dtype=torch.float32, device=x2.device)
+        rc = lib.flw_quant_rows_e4m3(x2.data_ptr(), _lib.dtype_code(x2.dtype), M, K, x2.stride(0),
+                                     x8.data_ptr(), sx.data_ptr(), stream)
+    else:
+        sx = torch.empty(1, dtype=torch.float32, device=x2.device)
+        ws = _lib.workspace(lib.flw_quant_workspace_bytes(1, 1, M, K), x2.device)
+        rc = lib.flw_quant_e4m3(x2.data_ptr(), _lib.dtype_code(x2.dtype), 1, 1, M, K, M * x2.stride(0),
+                                M * x2.stride(0), x2.stride(0), _lib.SCALE_TENSOR, _lib.LAYOUT_BHTD,
+                                x8.data_ptr(), sx.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "quantize rows")
+    return x8, sx
+
+
+def scaled_mm(a8: torch.Tensor, sa: torch.Tensor, b8: torch.Tensor, sb: torch.Tensor) -> torch.Tensor:
+    """bf16 [M, N] = (a8 [M, K] . b8 [N, K]^T) * sa[m] * sb[n] through flw_fp8_scaled_mm."""
+    lib = _lib.load()
+    M, K = a8.shape
+    N = b8.shape[0]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=a8.device)
+    rc = lib.flw_fp8_scaled_mm(a8.data_ptr(), M, K, b8.data_ptr(), N, sa.data_ptr(), sa.numel(),
+                               sb.data_ptr(), sb.numel(), y.data_ptr(), N, _lib.stream_of(a8))
+    _lib.check(rc, "fp8_scaled_mm")
+    return y
+
+
+def fp8_linear_backward(g2: torch.Tensor, x2: torch.Tensor, w_cols, recipe: str,
+                        need_x: bool = True, need_w: bool = True):
+    """FP8 gradient GEMMs of y = x W^T: (grad_x [M, K], grad_W [N, K]), bf16.
+
+    g2: [M, N] output gradient, x2: [M, K] the forward input, w_cols: (w8c [K, N], scale) from
+    ``quantize_weight_cols`` (or a callable returning it). Row / column granularity per recipe:
+    "rowwise" -> g per row for dgrad, g and x per column for wgrad; "tensorwise" -> one scale per
+    tensor everywhere. The token axis is zero-padded to a multiple of 128 for wgrad."""
+    gx = gw = None
+    g2 = g2.to(torch.bfloat16).contiguous()
+    if need_x:
+        g8, sg = _quantize_rows(g2, recipe)
+        w8c, swc = w_cols() if callable(w_cols) else w_cols
+        gx = scaled_mm(g8, sg, w8c, swc)
+    if need_w:
+        gran = "column" if recipe == "rowwise" else "tensor"
+        M = g2.shape[0]
+        ld = ((M + 127) // 128) * 128
+        g8c, sgc = quantize_cols(g2, gran, ld)
+        x8c, sxc = quantize_cols(x2, gran, ld)
+        gw = scaled_mm(g8c, sgc, x8c, sxc)
+    return gx, gw
+
+
 def fp8_linear_forward(x: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor,
                        recipe: str = "rowwise") -> torch.Tensor:
     """bf16 y[..., N] = x[..., K] @ dequant(w8)^T through the HIP FP8 GEMM."""
@@ -128,9 +220,10 @@ def fp8_linear_forward(x: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor,
 
 class _Fp8LinearFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weight, bias, w8, w_scale, recipe):
+    def forward(ctx, x, weight, bias, w8, w_scale, recipe, mod):
         ctx.save_for_backward(x, weight)
         ctx.has_bias = bias is not None
+        ctx.recipe, ctx.mod = recipe, mod
         y = fp8_linear_forward(x, w8, w_scale, recipe)
         if bias is not None:
             y = y + bias.to(y.dtype)
@@ -140,13 +233,21 @@ class _Fp8LinearFn(torch.autograd.Function):
     def backward(ctx, g):
         x, weight = ctx.saved_tensors
         g2 = g.reshape(-1, g.shape[-1])
-        w = weight.to(g2.dtype)
-        gx = (g2 @ w).reshape(x.shape).to(x.dtype) if ctx.needs_input_grad[0] else None
-        gw = None
-        if ctx.needs_input_grad[1]:
-            gw = (g2.t() @ x.reshape(-1, x.shape[-1]).to(g2.dtype)).to(weight.dtype)
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        fp8 = ctx.recipe in ("rowwise", "tensorwise") and getattr(ctx.mod, "backward_fp8", True)
+        gx = gw = None
+        if fp8 and (need_x or need_w):
+            x2 = x.reshape(-1, x.shape[-1])
+            gx, gw = fp8_linear_backward(g2, x2, ctx.mod.weight_col_codes, ctx.recipe, need_x, need_w)
+            gx = gx.reshape(x.shape).to(x.dtype) if gx is not None else None
+            gw = gw.to(weight.dtype) if gw is not None else None
+        else:
+            w = weight.to(g2.dtype)
+            gx = (g2 @ w).reshape(x.shape).to(x.dtype) if need_x else None
+            if need_w:
+                gw = (g2.t() @ x.reshape(-1, x.shape[-1]).to(g2.dtype)).to(weight.dtype)
         gb = g2.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
-        return gx, gw, gb, None, None, None
+        return gx, gw, gb, None, None, None, None
 
 
 class Fp8Linear(nn.Linear):
@@ -159,6 +260,7 @@ class Fp8Linear(nn.Linear):
             raise RuntimeError(f"training.fp8_recipe must be one of {sorted(RECIPES)}, got {recipe!r}")
         super().__init__(in_features, out_features, bias=bias, device=device, dtype=dtype)
         self.recipe = recipe
+        self.backward_fp8 = True
 
     @classmethod
     def from_linear(cls, lin: nn.Linear, recipe: str = "rowwise") -> "Fp8Linear":
@@ -171,6 +273,7 @@ class Fp8Linear(nn.Linear):
         new.register_parameter("weight", lin.weight)
         new.register_parameter("bias", lin.bias)
         new.recipe = recipe
+        new.backward_fp8 = True
         new.train(lin.training)
         return new
 
@@ -182,10 +285,21 @@ class Fp8Linear(nn.Linear):
         cached = getattr(self, "_fp8_cached", None)
         return cached if cached is not None else self.quantize_weight()
 
+    def weight_col_codes(self):
+        """(w8c [K, N], scale) for the dgrad GEMM: quantised once per fp8_weight_cache context
+        (on the first backward inside it), else on every call."""
+        cached = getattr(self, "_fp8_cached_cols", None)
+        if cached is not None:
+            return cached
+        codes = quantize_weight_cols(self.weight, self.recipe)
+        if getattr(self, "_fp8_cached", None) is not None:       # a cache context is active
+            self._fp8_cached_cols = codes
+        return codes
+
     def forward_with(self, x: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor) -> torch.Tensor:
         if torch.is_autocast_enabled():
             x = x.to(torch.get_autocast_gpu_dtype())
-        return _Fp8LinearFn.apply(x, self.weight, self.bias, w8, w_scale, self.recipe)
+        return _Fp8LinearFn.apply(x, self.weight, self.bias, w8, w_scale, self.recipe, self)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         w8, w_scale = self.quantize_weight()
@@ -298,6 +412,7 @@ class fp8_weight_cache:
         for mod in self._layers:
             mod.forward = self._orig_forwards[mod]
             mod._fp8_cached = None
+            mod._fp8_cached_cols = None
             if self.verify and exc_type is None:
                 if self._fingerprint(mod.weight) != self._fingerprints[mod]:
                     changed.append(mod)

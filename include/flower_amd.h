@@ -33,7 +33,7 @@ enum flw_dtype { FLW_F32 = 0, FLW_BF16 = 1 };
 
 /* Scale granularity for a (B, H, T, D) tensor: one scale, one per head h (amax over B, T, D),
  * or one per (b, h) slice (amax over T, D). Scale arrays hold 1, H or B*H floats. */
-enum flw_granularity { FLW_SCALE_TENSOR = 0, FLW_SCALE_HEAD = 1, FLW_SCALE_BH = 2 };
+enum flw_granularity { FLW_SCALE_TENSOR = 0, FLW_SCALE_HEAD = 1, FLW_SCALE_BH = 2, FLW_SCALE_COLUMN = 3 };
 
 /* Layout of e4m3 codes written by flw_quant_e4m3:
  *   FLW_LAYOUT_BHTD  -- contiguous (B, H, T, D), one byte per element;
@@ -102,6 +102,22 @@ int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t 
  * out: contiguous [rows, cols]; scale_out: [rows]. */
 int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
                         uint8_t* out, float* scale_out, void* stream);
+
+/* Per-column e4m3 quantisation of a [rows, cols] matrix with the codes written TRANSPOSED,
+ * out_t[cols, ld] (ld >= rows, ld % 16 == 0; rows past `rows` coded 0): the operands of the FP8
+ * backward GEMMs that torchao's Float8Linear runs under `training.fp8_linear` (torchao 0.18.0,
+ * uv.lock:1642-1644, not vendored; enabled at flower/train.py:368-370), where the reduction runs
+ * over the rows (wgrad: tokens) or a weight is consumed along its other axis (dgrad).
+ *   FLW_SCALE_COLUMN: scale[c] = max(amax_c / 448, 1e-12), code = e4m3_rne(x / scale[c])
+ *                     (flw_quant_rows_e4m3 of the transpose); scale_out: [cols].
+ *   FLW_SCALE_TENSOR: scale = max(amax, 1e-12) / 448, code = e4m3_rne(clamp(x / scale, +-448))
+ *                     (flw_quant_e4m3's per-tensor codes, transposed); scale_out: [1].
+ * cols and row_stride multiples of 8, rows 16-byte aligned. workspace: amax partials,
+ * flw_quant_cols_workspace_bytes(rows, cols) bytes. */
+size_t flw_quant_cols_workspace_bytes(int64_t rows, int64_t cols);
+int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                        int granularity, uint8_t* out_t, int64_t ld, float* scale_out, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- attention */
 

@@ -55,6 +55,14 @@ def test_host_only_calls_work_without_a_gpu():
     assert rc == 1 and b"unknown GEMM mode" in lib.flw_last_error()
     rc = lib.flw_fp8_linear(16, 8, 80, 80, 16, 16, 16, 16, 1, 16, 16, None, 0, None)   # W8A16
     assert rc == 2 and b"multiple of 64" in lib.flw_last_error()
+    assert lib.flw_quant_cols_workspace_bytes(1000, 100) == 4 * 100 * 4   # 4 row chunks x 100 columns
+    assert lib.flw_quant_cols_workspace_bytes(1000, 8) == 4 * 8 * 4
+    rc = lib.flw_quant_cols_e4m3(16, 1, 100, 64, 64, _lib.SCALE_HEAD, 16, 112, 16, 16, 1 << 20, None)
+    assert rc == 1 and b"granularity" in lib.flw_last_error()
+    rc = lib.flw_quant_cols_e4m3(16, 1, 100, 64, 64, _lib.SCALE_COLUMN, 16, 96, 16, 16, 1 << 20, None)
+    assert rc == 1 and b"ld must be" in lib.flw_last_error()
+    rc = lib.flw_quant_cols_e4m3(16, 1, 100, 64, 64, _lib.SCALE_COLUMN, 16, 112, 16, 16, 4, None)
+    assert rc != 0 and b"workspace" in lib.flw_last_error()
 
 
 def test_operators_refuse_cpu_tensors():
