@@ -1,6 +1,6 @@
 """Benchmark of the FP8 sliding-window-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|swa_bf16|swa_bf16_450m]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|c2_train|swa_bf16|swa_bf16_450m]
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
@@ -30,6 +30,8 @@ beside it, in GEMM TFLOP/s.
 --workload swa_bf16 / swa_bf16_450m measure the bf16 sliding-window attention training op (forward
 with log-sum-exp, then the backward) at the reference's measurement shape B1 H20 T4096 D64 W2048 /
 its 450M model shape B2 H20 T8192 D64 W2048; roofline = the backward entry point.
+--workload c2_train measures the C2 linear as an FP8 training step (forward, dgrad and wgrad GEMMs
+with their quantisers), beside torch's bf16 matmuls of the same three products.
 Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
 """
 
@@ -59,6 +61,8 @@ WORKLOADS = {
     "c1": dict(B=1, H=8, T=1024, D=64, W=256, granularity="tensor", inputs="randn_fp32"),
     "c2": dict(M=8192, N=4096, K=1024, outlier_frac=0.001, outlier_scale=20.0, w_std=0.02),
     "c5": dict(B=1, T=32768, d_model=1024, num_heads=16, ffn_dim=4096, W=4096, w_std=0.02),
+    # the C2 linear as a training step: forward + FP8 dgrad + FP8 wgrad (rowwise recipe)
+    "c2_train": dict(M=8192, N=4096, K=1024, outlier_frac=0.001, outlier_scale=20.0, w_std=0.02),
     # bf16 sliding-window attention as a training op (forward with log-sum-exp + backward): the
     # reference's own measurement shape (swa_attention.py:10-14, :40-43) and its 450M model shape
     "swa_bf16": dict(B=1, H=20, T=4096, D=64, W=2048, ref="B1 H20 T4096 D64 W2048"),
@@ -401,6 +405,8 @@ def main():
         line = run_block(cfg, args)
     elif args.workload.startswith("swa_bf16"):
         line = run_swa_bf16(cfg, args)
+    elif args.workload == "c2_train":
+        line = run_linear_train(cfg, args)
     else:
         line = run_attention(cfg, args)
     print(json.dumps(line), flush=True)
@@ -631,6 +637,150 @@ def run_swa_bf16(cfg, args):
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_swa_bf16(cfg)
+    return line
+
+
+def bench_linear_train(cfg, steps, warmup):
+    """One FP8 training step of the C2 linear through the C ABI, rowwise recipe, weights quantised
+    once outside the steps (the weight cache: row codes for the forward, column codes for dgrad):
+      forward  x8 = rows(x); y = x8 . w8^T                          (2 launches)
+      dgrad    g8 = rows(g); dx = g8 . w8c^T                        (2)
+      wgrad    g8c = cols(g), x8c = cols(x) (transposed); dW = g8c . x8c^T   (3)
+    Each entry point is timed by the event pair its own dispatches record."""
+    from flower_amd import _lib
+    lib = _lib.load()
+    M, N, K = cfg["M"], cfg["N"], cfg["K"]
+    x, w = (t.cuda() for t in make_gemm_inputs(cfg))
+    g = torch.randn(M, N, generator=torch.Generator().manual_seed(1)).to("cuda", torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    Mp = (M + 127) // 128 * 128
+    u8 = lambda *sh: torch.empty(sh, dtype=torch.uint8, device="cuda")
+    f32 = lambda n: torch.empty(n, dtype=torch.float32, device="cuda")
+    bf = lambda *sh: torch.empty(sh, dtype=torch.bfloat16, device="cuda")
+    w8, sw, w8c, swc = u8(N, K), f32(N), u8(K, N), f32(K)
+    x8, sx, y = u8(M, K), f32(M), bf(M, N)
+    g8, sg, dx = u8(M, N), f32(M), bf(M, K)
+    g8c, sgc, x8c, sxc, dw = u8(N, Mp), f32(N), u8(K, Mp), f32(K), bf(N, K)
+    ws = torch.empty(max(lib.flw_quant_cols_workspace_bytes(M, N), lib.flw_quant_cols_workspace_bytes(M, K),
+                         lib.flw_quant_cols_workspace_bytes(N, K)), dtype=torch.uint8, device="cuda")
+    C = _lib.check
+    C(lib.flw_quant_rows_e4m3(w.data_ptr(), _lib.BF16, N, K, K, w8.data_ptr(), sw.data_ptr(), stream), "w rows")
+    C(lib.flw_quant_cols_e4m3(w.data_ptr(), _lib.BF16, N, K, K, _lib.SCALE_COLUMN, w8c.data_ptr(), N,
+                              swc.data_ptr(), ws.data_ptr(), ws.numel(), stream), "w cols")
+
+    def mm(a8, sa, b8, sb, out, m, n, k):
+        C(lib.flw_fp8_scaled_mm(a8.data_ptr(), m, k, b8.data_ptr(), n, sa.data_ptr(), sa.numel(),
+                                sb.data_ptr(), sb.numel(), out.data_ptr(), n, stream), "mm")
+
+    calls = [
+        ("fwd_quant", lambda: C(lib.flw_quant_rows_e4m3(x.data_ptr(), _lib.BF16, M, K, K, x8.data_ptr(),
+                                                        sx.data_ptr(), stream), "x rows")),
+        ("fwd_gemm", lambda: mm(x8, sx, w8, sw, y, M, N, K)),
+        ("dgrad_quant", lambda: C(lib.flw_quant_rows_e4m3(g.data_ptr(), _lib.BF16, M, N, N, g8.data_ptr(),
+                                                          sg.data_ptr(), stream), "g rows")),
+        ("dgrad_gemm", lambda: mm(g8, sg, w8c, swc, dx, M, K, N)),
+        ("wgrad_quant_g", lambda: C(lib.flw_quant_cols_e4m3(g.data_ptr(), _lib.BF16, M, N, N, _lib.SCALE_COLUMN,
+                                                            g8c.data_ptr(), Mp, sgc.data_ptr(), ws.data_ptr(),
+                                                            ws.numel(), stream), "g cols")),
+        ("wgrad_quant_x", lambda: C(lib.flw_quant_cols_e4m3(x.data_ptr(), _lib.BF16, M, K, K, _lib.SCALE_COLUMN,
+                                                            x8c.data_ptr(), Mp, sxc.data_ptr(), ws.data_ptr(),
+                                                            ws.numel(), stream), "x cols")),
+        ("wgrad_gemm", lambda: mm(g8c, sgc, x8c, sxc, dw, N, K, Mp)),
+    ]
+
+    def step():
+        for _, f in calls:
+            f()
+
+    _spin_up(step)
+    for _ in range(warmup):
+        step()
+    ev = [_events(steps) for _ in calls]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        for j, (_, f) in enumerate(calls):
+            _arm(lib, ev[j][i])
+            f()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = {name: float(np.mean([a.elapsed_time(b) for a, b in ev[j]])) for j, (name, _) in enumerate(calls)}
+    # the same three products in bf16 through torch (hipBLASLt), for comparison
+    wt = w.t()
+    for _ in range(3):                      # library heuristics / first-call set-up outside the timing
+        torch.matmul(x, wt)
+        torch.matmul(g, w)
+        torch.matmul(g.t(), x)
+    torch.cuda.synchronize()
+    tev = _events(steps, per=4)
+    for a, b, c_, d in tev:
+        a.record()
+        torch.matmul(x, wt)
+        b.record()
+        torch.matmul(g, w)
+        c_.record()
+        torch.matmul(g.t(), x)
+        d.record()
+    torch.cuda.synchronize()
+    bf16 = {"fwd_ms": float(np.median([a.elapsed_time(b) for a, b, _, _ in tev])),
+            "dgrad_ms": float(np.median([b.elapsed_time(c_) for _, b, c_, _ in tev])),
+            "wgrad_ms": float(np.median([c_.elapsed_time(d) for _, _, c_, d in tev]))}
+    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, ms=ms, bf16=bf16, flops_gemm=2 * M * N * K,
+                x=x, w=w, g=g)
+
+
+def cpu_baseline_linear_train(x, w, g, budget_s=15.0):
+    """The oracle's FP8 forward + backward (oracle/gemm.py: per-row / per-column e4m3, float64
+    closed-form GEMMs) on a sub-batch of token rows, scaled to the same FLOPs unit."""
+    from threadpoolctl import threadpool_limits
+    from oracle.gemm import fp8_linear_a8w8, fp8_linear_backward
+    from oracle.quant import rowwise_fp8
+    cores = min(16, os.cpu_count() or 1)
+    xf, wf, gf = (t.float().cpu().numpy() for t in (x, w, g))
+    w8, sw = rowwise_fp8(wf)
+    rows, t_total = 0, 0.0
+    with threadpool_limits(cores):
+        for r0 in range(0, xf.shape[0], 1024):
+            t0 = time.perf_counter()
+            fp8_linear_a8w8(xf[r0:r0 + 1024], w8, sw.reshape(-1))
+            fp8_linear_backward(gf[r0:r0 + 1024], xf[r0:r0 + 1024], wf, "rowwise")
+            t_total += time.perf_counter() - t0
+            rows += min(1024, xf.shape[0] - r0)
+            if t_total > budget_s:
+                break
+    flops = 3 * 2 * rows * wf.shape[0] * wf.shape[1]
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{rows} of {xf.shape[0]} token rows in {t_total:.1f} s, 1024 at a time: oracle per-row / "
+                      f"per-column e4m3 + float64 closed-form forward, dgrad and wgrad GEMMs (numpy / BLAS); "
+                      f"the weight's column codes re-made per sub-batch"}
+
+
+def run_linear_train(cfg, args):
+    r = bench_linear_train(cfg, args.steps, args.warmup)
+    ms, f = r["ms"], r["flops_gemm"]
+    value = 3 * f / (r["ms_per_step"] * 1e-3) / 1e12
+    tf = lambda t: round(f / (t * 1e-3) / 1e12, 2)
+    gemms = {k: ms[k] for k in ("fwd_gemm", "dgrad_gemm", "wgrad_gemm")}
+    dom = max(gemms, key=gemms.get)
+    line = {
+        "metric": "FP8 linear training step TFLOPS (forward + dgrad + wgrad, rowwise e4m3), BASELINE C2 shape",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "spin_up_s": SPIN_UP_S, "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate), bf16 in / out", "data": DATA["c2"],
+        "config": {"workload": "Fp8Linear training step at the C2 shape", "M": cfg["M"], "N": cfg["N"],
+                   "K": cfg["K"], "recipe": "rowwise (per-row x / g for forward / dgrad, per-column g / x for wgrad)"},
+        "roofline": {"bound": "mfma", "achieved": tf(gemms[dom]), "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(f / (gemms[dom] * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": f"fp8_gemm_256_kernel ({dom})", "kernel_ms": round(gemms[dom], 4),
+                     "flop_per_launch": f},
+        "kernels_ms": {k: round(v, 4) for k, v in ms.items()},
+        "gemm_tflops": {k: tf(v) for k, v in gemms.items()},
+        "bf16_torch_ms": {k: round(v, 4) for k, v in r["bf16"].items()},
+        "bf16_torch_tflops": {k: tf(v) for k, v in r["bf16"].items()},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_linear_train(r["x"], r["w"], r["g"])
     return line
 
 

@@ -23,12 +23,23 @@ struct Timer {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 Timer take_timer();
+// Re-arm (part of) a taken pair for an entry point that calls other entry points in turn.
+void arm_timer(Timer t);
 
 // Launch of a kernel taking one parameter struct, optionally recording start / stop events.
 template <typename P>
 inline hipError_t launch_ext(const void* kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
                              P p, hipEvent_t start, hipEvent_t stop) {
   void* args[] = {static_cast<void*>(&p)};
+  return hipExtLaunchKernel(kernel, grid, block, args, lds, stream, start, stop, 0);
+}
+
+// Launch of a kernel taking plain arguments. The argument types must be exactly the kernel's
+// parameter types (no conversion happens through the void* array).
+template <typename... A>
+inline hipError_t launch_args(const void* kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                              hipEvent_t start, hipEvent_t stop, A... a) {
+  void* args[] = {static_cast<void*>(&a)...};
   return hipExtLaunchKernel(kernel, grid, block, args, lds, stream, start, stop, 0);
 }
 

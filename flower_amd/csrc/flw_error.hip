@@ -26,6 +26,11 @@ Timer take_timer() {
   return t;
 }
 
+void arm_timer(Timer t) {
+  g_timer_start = t.start;
+  g_timer_stop = t.stop;
+}
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FLW_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));

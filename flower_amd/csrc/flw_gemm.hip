@@ -658,8 +658,16 @@ extern "C" int flw_fp8_linear(const void* x, int64_t M, int64_t K, int64_t x_row
   FLW_REQUIRE(workspace != nullptr && workspace_bytes >= need, FLW_E_WORKSPACE, "workspace needs %zu bytes", need);
   uint8_t* x8 = static_cast<uint8_t*>(workspace);
   float* sx = reinterpret_cast<float*>(x8 + galign((size_t)(M * K)));
+  const Timer tm = take_timer();   // start on the row quantiser, stop on the GEMM
+  arm_timer(Timer{tm.start, nullptr});
   int rc = flw_quant_rows_e4m3(x, FLW_BF16, M, K, x_row_stride, x8, sx, stream);
-  if (rc) return rc;
-  return scaled_mm(x8, M, K, w8, N, sx, M, w_scale, w_scale_count, y, y_row_stride,
-                   static_cast<hipStream_t>(stream));
+  if (rc) {
+    arm_timer(Timer{});
+    return rc;
+  }
+  arm_timer(Timer{nullptr, tm.stop});
+  rc = scaled_mm(x8, M, K, w8, N, sx, M, w_scale, w_scale_count, y, y_row_stride,
+                 static_cast<hipStream_t>(stream));
+  if (rc) arm_timer(Timer{});
+  return rc;
 }

@@ -784,12 +784,13 @@ extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64
   FLW_REQUIRE((rows + 3) / 4 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid((unsigned)((rows + 3) / 4));
+  const Timer tm = take_timer();
   if (dtype == FLW_F32)
-    hipLaunchKernelGGL(rows_quant_kernel<float>, grid, dim3(kThreads), 0, s,
-                       static_cast<const float*>(x), rows, cols, row_stride, out, scale_out);
+    (void)launch_args(reinterpret_cast<const void*>(&rows_quant_kernel<float>), grid, dim3(kThreads), 0, s,
+                      tm.start, tm.stop, static_cast<const float*>(x), rows, cols, row_stride, out, scale_out);
   else
-    hipLaunchKernelGGL(rows_quant_kernel<uint16_t>, grid, dim3(kThreads), 0, s,
-                       static_cast<const uint16_t*>(x), rows, cols, row_stride, out, scale_out);
+    (void)launch_args(reinterpret_cast<const void*>(&rows_quant_kernel<uint16_t>), grid, dim3(kThreads), 0, s,
+                      tm.start, tm.stop, static_cast<const uint16_t*>(x), rows, cols, row_stride, out, scale_out);
   return check_launch("flw_quant_rows_e4m3");
 }
 
@@ -822,21 +823,21 @@ extern "C" int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64
   uint32_t* part = static_cast<uint32_t*>(workspace);
   const dim3 g1((unsigned)ncb, (unsigned)nchunks), g2((unsigned)ncb, (unsigned)oy);
   const bool tensor = granularity == FLW_SCALE_TENSOR;
-#define FLW_COLS(T)                                                                                        \
+  const Timer tm = take_timer();   // start on the amax pass, stop on the quantise pass
+#define FLW_COLS(T, TEN)                                                                                   \
   do {                                                                                                     \
     const T* xt = static_cast<const T*>(x);                                                                \
-    if (tensor) {                                                                                          \
-      hipLaunchKernelGGL((cols_amax_kernel<T, true>), g1, dim3(kThreads), 0, s, xt, rows, cols, row_stride, part); \
-      hipLaunchKernelGGL((cols_quant_t_kernel<T, true>), g2, dim3(kThreads), 0, s, xt, rows, cols, row_stride,    \
-                         part, nchunks, ncb, out_t, ld, scale_out);                                         \
-    } else {                                                                                               \
-      hipLaunchKernelGGL((cols_amax_kernel<T, false>), g1, dim3(kThreads), 0, s, xt, rows, cols, row_stride, part); \
-      hipLaunchKernelGGL((cols_quant_t_kernel<T, false>), g2, dim3(kThreads), 0, s, xt, rows, cols, row_stride,   \
-                         part, nchunks, ncb, out_t, ld, scale_out);                                         \
-    }                                                                                                      \
+    (void)launch_args(reinterpret_cast<const void*>(&cols_amax_kernel<T, TEN>), g1, dim3(kThreads), 0, s, \
+                      tm.start, nullptr, xt, rows, cols, row_stride, part);                                \
+    (void)launch_args(reinterpret_cast<const void*>(&cols_quant_t_kernel<T, TEN>), g2, dim3(kThreads), 0, \
+                      s, nullptr, tm.stop, xt, rows, cols, row_stride, static_cast<const uint32_t*>(part), \
+                      nchunks, ncb, out_t, ld, scale_out);                                                 \
   } while (0)
-  if (dtype == FLW_F32) FLW_COLS(float);
-  else FLW_COLS(uint16_t);
+  if (dtype == FLW_F32) {
+    if (tensor) FLW_COLS(float, true); else FLW_COLS(float, false);
+  } else {
+    if (tensor) FLW_COLS(uint16_t, true); else FLW_COLS(uint16_t, false);
+  }
 #undef FLW_COLS
   return check_launch("flw_quant_cols_e4m3");
 }
