@@ -668,9 +668,13 @@ def bench_linear_train(cfg, steps, warmup):
     C(lib.flw_quant_cols_e4m3(w.data_ptr(), _lib.BF16, N, K, K, _lib.SCALE_COLUMN, w8c.data_ptr(), N,
                               swc.data_ptr(), ws.data_ptr(), ws.numel(), stream), "w cols")
 
-    def mm(a8, sa, b8, sb, out, m, n, k):
-        C(lib.flw_fp8_scaled_mm(a8.data_ptr(), m, k, b8.data_ptr(), n, sa.data_ptr(), sa.numel(),
-                                sb.data_ptr(), sb.numel(), out.data_ptr(), n, stream), "mm")
+    mws = torch.empty(max(256, lib.flw_fp8_scaled_mm_workspace_bytes(M, N, K), lib.flw_fp8_scaled_mm_workspace_bytes(M, K, N),
+                          lib.flw_fp8_scaled_mm_workspace_bytes(N, K, Mp)), dtype=torch.uint8, device="cuda")
+
+    def mm(a8, sa, b8, sb, out, m, n, k):     # split over K into mws when [m, n] has few tiles
+        C(lib.flw_fp8_scaled_mm_ws(a8.data_ptr(), m, k, b8.data_ptr(), n, sa.data_ptr(), sa.numel(),
+                                   sb.data_ptr(), sb.numel(), out.data_ptr(), n, mws.data_ptr(), mws.numel(),
+                                   stream), "mm")
 
     calls = [
         ("fwd_quant", lambda: C(lib.flw_quant_rows_e4m3(x.data_ptr(), _lib.BF16, M, K, K, x8.data_ptr(),

@@ -64,6 +64,9 @@ SIGNATURES = {
     "flw_fp8_linear_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int]),
     "flw_fp8_linear": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                c_int64, c_int, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
+    "flw_fp8_scaled_mm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
+    "flw_fp8_scaled_mm_ws": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                     c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     "flw_fp8_scaled_mm": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "flw_fp8_scaled_mm_residual": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,

@@ -41,6 +41,8 @@ struct GemmParams {
   int tiles_m;         // output tiles along M
   const uint16_t* res; // optional bf16 residual [M, N] (row stride rs): y = bf16(res + bf16(..))
   int64_t rs;
+  float* part;         // split-K: fp32 partial sums [splits][M][N] instead of the bf16 epilogue
+  int splits;          // K ranges per output tile (1: no split)
 };
 
 // The epilogue value of one output: bf16(v), or bf16(residual + bf16(v)) -- x + linear(h) with
@@ -208,7 +210,7 @@ __device__ __forceinline__ v8i swz_frag(const uint8_t* tile, int rb, int kc, int
 
 // One 256 x 256 output tile: K loop over two LDS stages, then the scaled bf16 epilogue.
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
-                                          int n0, int wave, int lane) {
+                                          int n0, int wave, int lane, int sbase, int nst, int split) {
   const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
   // Loads: a stage is 2 x 256 rows x 128 bytes = 512 rows; wave w fills rows 64 w .. 64 w + 63
   // (waves 0-3: W, 4-7: X) with 8 instructions of 8 rows each. Lane i of instruction t covers
@@ -228,7 +230,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
   // drain the prefetch before every fragment read; the kernel orders them itself (an explicit
   // vmcnt wait for this wave's loads, then a workgroup barrier, before a stage is read).
   auto issue = [&](uint8_t* stage, int s) __attribute__((always_inline)) {
-    const uint32_t k0 = (uint32_t)s * kFBK;
+    const uint32_t k0 = (uint32_t)(sbase + s) * kFBK;
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8_t*)(stage + lbase);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
@@ -242,7 +244,6 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
 
-  const int nst = p.K / kFBK;
   issue(st0, 0);
 
   // Stage s in `cur`: prefetch stage s+1 into `nxt` (its readers finished at the end of step
@@ -279,6 +280,25 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
 
   // Epilogue: lane owns m = m0 + 64 wm + 32 j + lane % 32, n = n0 + 128 wn + 32 i + 8 g + 4 hh + 0..3
   const int hh = lane >> 5;
+  if (p.part) {                                   // split-K: unscaled fp32 partials, 16-byte stores
+    float* base = p.part + (int64_t)split * p.M * p.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int m = m0 + 64 * wm + 32 * j + (lane & 31);
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + 128 * wn + 32 * i + 8 * g + 4 * hh;
+          if (n >= p.N) continue;
+          const v16f& c = acc[i][j];
+          *reinterpret_cast<float4*>(base + (int64_t)m * p.N + n) =
+              make_float4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]);
+        }
+      }
+    return;
+  }
   float sxm[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -348,14 +368,47 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
   const int lane_w = lane;   // (kept for the loops below)
   (void)lane_w;
 
-  for (int t = L; t < ntiles; t += G) {
-    const int group = t / (kGroupM * p.tiles_n);
+  // Split-K: work item t = split * ntiles + tile; split s covers K stages [s nst / S, (s+1) nst / S).
+  const int nst_all = p.K / kFBK;
+  for (int t = L; t < ntiles * p.splits; t += G) {
+    const int split = t / ntiles, tt = t % ntiles;
+    const int group = tt / (kGroupM * p.tiles_n);
     const int first_m = group * kGroupM;
     const int gm = min(p.tiles_m - first_m, kGroupM);
-    const int tm = first_m + (t % (kGroupM * p.tiles_n)) % gm;
-    const int tn = (t % (kGroupM * p.tiles_n)) / gm;
-    gemm_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane);
+    const int tm = first_m + (tt % (kGroupM * p.tiles_n)) % gm;
+    const int tn = (tt % (kGroupM * p.tiles_n)) / gm;
+    const int s0 = split * nst_all / p.splits, s1 = (split + 1) * nst_all / p.splits;
+    gemm_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
   }
+}
+
+// Split-K finish: y[m, n..n+3] = bf16( (sum_s part[s][m][n]) * sx[m] * sw[n] ) (+ residual as in
+// the one-pass epilogue); one thread per 4 outputs.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_row = p.N / 4;
+  if (q >= (int64_t)p.M * per_row) return;
+  const int m = (int)(q / per_row), n = (int)(q % per_row) * 4;
+  float4 a = *reinterpret_cast<const float4*>(p.part + (int64_t)m * p.N + n);
+  for (int sp = 1; sp < p.splits; ++sp) {
+    const float4 b = *reinterpret_cast<const float4*>(p.part + ((int64_t)sp * p.M + m) * p.N + n);
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  }
+  const float sx = p.sx[(int64_t)m * p.sx_step];
+  const float sw[4] = {p.sw[(int64_t)n * p.sw_step], p.sw[(int64_t)(n + 1) * p.sw_step],
+                       p.sw[(int64_t)(n + 2) * p.sw_step], p.sw[(int64_t)(n + 3) * p.sw_step]};
+  float v[4] = {a.x * sx * sw[0], a.y * sx * sw[1], a.z * sx * sw[2], a.w * sx * sw[3]};
+  if (p.res) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.rs + n);
+    v[0] = round_bf16(v[0]) + __uint_as_float(r.x << 16);
+    v[1] = round_bf16(v[1]) + __uint_as_float(r.x & 0xFFFF0000u);
+    v[2] = round_bf16(v[2]) + __uint_as_float(r.y << 16);
+    v[3] = round_bf16(v[3]) + __uint_as_float(r.y & 0xFFFF0000u);
+  }
+  uint2 w;
+  w.x = pack_bf16x2(v[0], v[1]);
+  w.y = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(p.y + (int64_t)m * p.ys + n) = w;
 }
 
 // ---------------------------------------------------------------- W8A16: e4m3 weights x bf16 activations
@@ -555,9 +608,30 @@ static int compute_units() {
   return cache[dev];
 }
 
+// K ranges per output tile for the 256 x 256 kernel: split when the tiles alone would leave more
+// than half of the compute units idle and each range keeps at least 4 K stages of 128. (Measured
+// at the C2 shapes: the wgrad output [4096, 1024], 64 tiles, 96 -> 54 us with 4 ranges; the dgrad
+// output [8192, 1024], 128 tiles, gains nothing from 2.)
+static int splitk_of(int64_t tiles, int64_t K) {
+  const int cus = compute_units();
+  if (tiles * 2 >= cus) return 1;     // half the GPU or more busy: the finish pass would cost more
+  int sp = (int)(cus / tiles);
+  sp = sp > 8 ? 8 : sp;
+  while (sp > 1 && (K / kFBK) / sp < 4) --sp;
+  return sp < 1 ? 1 : sp;
+}
+
+static size_t splitk_bytes(int64_t M, int64_t N, int64_t K) {
+  if (K % kFBK != 0) return 0;
+  const int64_t tiles = ((N + kFBN - 1) / kFBN) * ((M + kFBM - 1) / kFBM);
+  const int sp = splitk_of(tiles, K);
+  return sp > 1 ? (size_t)sp * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
 static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
                      const float* sx, int64_t sx_count, const float* sw, int64_t sw_count,
-                     void* y, int64_t ys, hipStream_t s, const void* res = nullptr, int64_t rs = 0) {
+                     void* y, int64_t ys, hipStream_t s, const void* res = nullptr, int64_t rs = 0,
+                     void* workspace = nullptr, size_t workspace_bytes = 0) {
   FLW_REQUIRE(x8 && w8 && sx && sw && y, FLW_E_INVALID, "null pointer argument");
   FLW_REQUIRE(M > 0 && N > 0 && K > 0, FLW_E_INVALID, "empty GEMM");
   FLW_REQUIRE(K % 16 == 0, FLW_E_UNSUPPORTED, "K must be a multiple of 16, got %lld", (long long)K);
@@ -580,9 +654,26 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
     p.tiles_m = (int)((M + kFBM - 1) / kFBM);
     const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
     FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
-    // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per tile.
-    const int64_t grid = tiles < compute_units() ? tiles : compute_units();
-    (void)launch_timed(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
+    // Split-K into the caller's workspace when the output has too few tiles to fill the GPU.
+    p.splits = 1;
+    const size_t need = splitk_bytes(M, N, K);
+    if (need && workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0 && N % 4 == 0) {
+      p.splits = splitk_of(tiles, K);
+      p.part = static_cast<float*>(workspace);
+    }
+    // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per work item.
+    const int64_t items = tiles * p.splits;
+    const int64_t grid = items < compute_units() ? items : compute_units();
+    if (p.splits == 1) {
+      (void)launch_timed(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
+    } else {
+      const Timer tm = take_timer();
+      (void)launch_ext(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads),
+                       0, s, p, tm.start, nullptr);
+      const int64_t quads = M * (N / 4);
+      (void)launch_ext(reinterpret_cast<const void*>(&gemm_splitk_reduce_kernel), dim3((unsigned)((quads + 255) / 256)),
+                       dim3(256), 0, s, p, nullptr, tm.stop);
+    }
     return check_launch("flw_fp8_scaled_mm");
   }
   p.tiles_n = (int)((N + kGBN - 1) / kGBN);
@@ -629,6 +720,19 @@ extern "C" int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const 
                                  int64_t y_row_stride, void* stream) {
   return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y,
                    y_row_stride, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t flw_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return splitk_bytes(M, N, K);
+}
+
+extern "C" int flw_fp8_scaled_mm_ws(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
+                                    const float* x_scale, int64_t x_scale_count, const float* w_scale,
+                                    int64_t w_scale_count, void* y, int64_t y_row_stride, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y, y_row_stride,
+                   static_cast<hipStream_t>(stream), nullptr, 0, workspace, workspace_bytes);
 }
 
 extern "C" int flw_fp8_scaled_mm_residual(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,

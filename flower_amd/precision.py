@@ -142,13 +142,16 @@ def _quantize_rows(x2: torch.Tensor, recipe: str):
 
 
 def scaled_mm(a8: torch.Tensor, sa: torch.Tensor, b8: torch.Tensor, sb: torch.Tensor) -> torch.Tensor:
-    """bf16 [M, N] = (a8 [M, K] . b8 [N, K]^T) * sa[m] * sb[n] through flw_fp8_scaled_mm."""
+    """bf16 [M, N] = (a8 [M, K] . b8 [N, K]^T) * sa[m] * sb[n] through flw_fp8_scaled_mm_ws (split
+    over K into a workspace when [M, N] has too few output tiles to fill the GPU)."""
     lib = _lib.load()
     M, K = a8.shape
     N = b8.shape[0]
     y = torch.empty((M, N), dtype=torch.bfloat16, device=a8.device)
-    rc = lib.flw_fp8_scaled_mm(a8.data_ptr(), M, K, b8.data_ptr(), N, sa.data_ptr(), sa.numel(),
-                               sb.data_ptr(), sb.numel(), y.data_ptr(), N, _lib.stream_of(a8))
+    ws = _lib.workspace(lib.flw_fp8_scaled_mm_workspace_bytes(M, N, K), a8.device)
+    rc = lib.flw_fp8_scaled_mm_ws(a8.data_ptr(), M, K, b8.data_ptr(), N, sa.data_ptr(), sa.numel(),
+                                  sb.data_ptr(), sb.numel(), y.data_ptr(), N, ws.data_ptr(), ws.numel(),
+                                  _lib.stream_of(a8))
     _lib.check(rc, "fp8_scaled_mm")
     return y
 

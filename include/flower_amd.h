@@ -205,6 +205,18 @@ int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8
                       const float* x_scale, int64_t x_scale_count, const float* w_scale,
                       int64_t w_scale_count, void* y, int64_t y_row_stride, void* stream);
 
+/* flw_fp8_scaled_mm with a workspace for a split over K, for outputs with too few 256 x 256 tiles
+ * to fill the GPU (the FP8 wgrad of a linear: [N, K] outputs reduced over the tokens): each tile's
+ * K range is cut into up to 8 parts whose fp32 partial sums go to the workspace and are summed,
+ * scaled and rounded to bf16 by a second kernel. Same result contract as flw_fp8_scaled_mm
+ * (fp32 accumulation, summed in a different order). flw_fp8_scaled_mm_workspace_bytes returns 0
+ * when no split applies; with a smaller workspace the call runs unsplit. */
+size_t flw_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int flw_fp8_scaled_mm_ws(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
+                         const float* x_scale, int64_t x_scale_count, const float* w_scale,
+                         int64_t w_scale_count, void* y, int64_t y_row_stride, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* flw_fp8_scaled_mm with the block's residual add in the epilogue:
  * y = bf16(residual + bf16((x8 . w8^T) * x_scale[m] * w_scale[n])), i.e. `x + linear(h)` of
  * the decoder block (flower/models/base.py:698-722) with both terms rounded to bf16 as torch

@@ -55,6 +55,8 @@ def test_host_only_calls_work_without_a_gpu():
     assert rc == 1 and b"unknown GEMM mode" in lib.flw_last_error()
     rc = lib.flw_fp8_linear(16, 8, 80, 80, 16, 16, 16, 16, 1, 16, 16, None, 0, None)   # W8A16
     assert rc == 2 and b"multiple of 64" in lib.flw_last_error()
+    assert lib.flw_fp8_scaled_mm_workspace_bytes(8192, 4096, 1024) == 0    # 512 tiles: no split
+    assert lib.flw_fp8_scaled_mm_workspace_bytes(256, 256, 100) == 0       # K % 128: no split
     assert lib.flw_quant_cols_workspace_bytes(1000, 100) == 4 * 100 * 4   # 4 row chunks x 100 columns
     assert lib.flw_quant_cols_workspace_bytes(1000, 8) == 4 * 8 * 4
     rc = lib.flw_quant_cols_e4m3(16, 1, 100, 64, 64, _lib.SCALE_HEAD, 16, 112, 16, 16, 1 << 20, None)

@@ -50,6 +50,36 @@ def test_scaled_mm_matches_closed_form(M, N, K, sx_per_row, sw_per_col):
     assert_gemm_close(to_np(y), ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 256, 4096), (512, 1024, 2048), (4096, 1024, 8192), (300, 260, 1024),
+                                   (100, 36, 80)])
+def test_scaled_mm_split_k_matches_closed_form(M, N, K):
+    """flw_fp8_scaled_mm_ws: outputs with few 256 x 256 tiles are split over K into the workspace
+    (1 tile -> 8 ranges, 8 tiles -> 4, the C2 wgrad shape 64 tiles -> 4) and summed by the finish
+    kernel; shapes without a split (K % 128 != 0) take the plain path through the same call.
+    Against the closed form, and equal to the unsplit call within the GEMM tolerance."""
+    from flower_amd import _lib as L
+    lb = L.load()
+    x8, w8 = codes((M, K), 4), codes((N, K), 5)
+    rng = np.random.default_rng(6)
+    sx = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    tx8, tw8 = torch.from_numpy(x8).cuda(), torch.from_numpy(w8).cuda()
+    tsx, tsw = torch.from_numpy(sx).cuda(), torch.from_numpy(sw).cuda()
+    need = lb.flw_fp8_scaled_mm_workspace_bytes(M, N, K)
+    if K % 128 == 0 and M * N <= 8 * 256 * 256:
+        assert need > 0
+    ws = L.workspace(need, "cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    L.check(lb.flw_fp8_scaled_mm_ws(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), M, tsw.data_ptr(),
+                                    N, y.data_ptr(), N, ws.data_ptr(), ws.numel(), L.stream_of(y)), "mm_ws")
+    ref = scaled_mm(x8, w8, sx, sw)
+    assert_gemm_close(to_np(y), ref)
+    y1 = torch.empty_like(y)
+    L.check(lb.flw_fp8_scaled_mm(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), M, tsw.data_ptr(), N,
+                                 y1.data_ptr(), N, L.stream_of(y)), "mm")
+    assert_gemm_close(to_np(y), to_np(y1).astype(np.float64))
+
+
 def test_config2_fp8_linear_full_size():
     """W [4096 x 1024] ~ N(0, 0.02) bf16 per-channel e4m3; X [8192 x 1024]
     ~ N(0, 1) bf16 with 0.1% outliers x20; A8W8 output checked on sampled rows against the
