@@ -428,17 +428,32 @@ __global__ __launch_bounds__(kThreads) void cols_quant_t_kernel(const T* __restr
     const float s = (amax < kEps ? kEps : amax) / kE4m3Max;
     if (t < kCT) { sc[t] = s; rc[t] = 1.0f / s; }
     if (blockIdx.x == 0 && blockIdx.y == 0 && t == 0) scale_out[0] = s;
-  } else if (t < kCT) {
-    const int64_t c = cb0 + t;
+  } else {
+    // Fold the column partials with all 256 threads (4 row-chunk lanes per column, several loads
+    // in flight each): a single thread per column walking the chunks serialises their latency.
+    __shared__ uint32_t fold[kThreads / kCT][kCT];
+    const int cl = t & (kCT - 1), part = t / kCT;
+    const int64_t c = cb0 + cl;
     uint32_t m = 0;
-    if (c < cols)
-      for (int64_t k = 0; k < nchunks; ++k) m = m > partials[k * cols + c] ? m : partials[k * cols + c];
-    const float amax = __uint_as_float(m);
-    float s = amax / kE4m3Max;
-    s = s < kEps ? kEps : s;
-    sc[t] = s;
-    rc[t] = 1.0f / s;
-    if (blockIdx.y == 0 && c < cols) scale_out[c] = s;
+    if (c < cols) {
+#pragma unroll 4
+      for (int64_t k = part; k < nchunks; k += kThreads / kCT) {
+        const uint32_t a = partials[k * cols + c];
+        m = m > a ? m : a;
+      }
+    }
+    fold[part][cl] = m;
+    __syncthreads();
+    if (t < kCT) {
+#pragma unroll
+      for (int q = 1; q < kThreads / kCT; ++q) m = m > fold[q][t] ? m : fold[q][t];
+      const float amax = __uint_as_float(m);
+      float s = amax / kE4m3Max;
+      s = s < kEps ? kEps : s;
+      sc[t] = s;
+      rc[t] = 1.0f / s;
+      if (blockIdx.y == 0 && c < cols) scale_out[c] = s;
+    }
   }
   __syncthreads();
 
@@ -496,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void cols_quant_t_kernel(const T* __restr
 //   ACT_GELU:    h = bf16( (0.5 x) * (1 + erf(x / sqrt 2)) )                 (F.gelu, erf form)
 // then scale = max(amax|h| / 448, 1e-12), code = e4m3(h / scale). bf16 in and out; the bf16 h
 // is written too when h_out is given.
-constexpr int kActRmsnorm = 0, kActGelu = 1;
+constexpr int kActRmsnorm = 0, kActGelu = 1, kActNone = 2;   // kActNone: h = x (flw_quant_rows_e4m3)
 
 // erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7): erf(|x|) = 1 - poly(t) exp(-x^2),
 // t = 1 / (1 + p |x|); two transcendental and six fused multiply-adds instead of the device
@@ -565,7 +580,7 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
       for (int e = 0; e < 8; ++e) f[e] = round_bf16(round_bf16(f[e] * r) * g[e]);
       hb[i] = pack(f);
     }
-  } else {
+  } else if (ACT == kActGelu) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       float f[8];
@@ -772,6 +787,10 @@ extern "C" int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t 
   return launch_quant<1>(p, 1, dtype, static_cast<hipStream_t>(stream), "flw_fake_quant_e4m3", take_timer());
 }
 
+template <int ACT>
+static int rows_act_quant(const void* x, int64_t rows, int64_t cols, int64_t rs, const void* w, float eps,
+                          uint8_t* out, float* scale_out, void* h_out, hipStream_t s, const char* name);
+
 extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64_t cols,
                                    int64_t row_stride, uint8_t* out, float* scale_out, void* stream) {
   FLW_REQUIRE(x != nullptr && out != nullptr && scale_out != nullptr, FLW_E_INVALID, "null pointer");
@@ -783,6 +802,11 @@ extern "C" int flw_quant_rows_e4m3(const void* x, int dtype, int64_t rows, int64
   FLW_REQUIRE(((uintptr_t)out & 7) == 0 && (cols % 8 == 0 || dtype == FLW_F32), FLW_E_INVALID, "output must be 8-byte aligned");
   FLW_REQUIRE((rows + 3) / 4 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // bf16 rows of up to 4096 elements: read once and kept in registers between the amax and the
+  // codes (the generic kernel re-reads the row, which for long rows comes back from HBM).
+  if (dtype == FLW_BF16 && cols <= 4096 && row_stride >= cols && ((uintptr_t)out & 7) == 0)
+    return rows_act_quant<kActNone>(x, rows, cols, row_stride, nullptr, 0.0f, out, scale_out, nullptr, s,
+                                    "flw_quant_rows_e4m3");
   dim3 grid((unsigned)((rows + 3) / 4));
   const Timer tm = take_timer();
   if (dtype == FLW_F32)
@@ -859,10 +883,11 @@ static int rows_act_quant(const void* x, int64_t rows, int64_t cols, int64_t rs,
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(w);
   uint16_t* hp = static_cast<uint16_t*>(h_out);
+  const Timer tm = take_timer();
 #define FLW_ACT_CASE(N)                                                                               \
   if (nv <= N) {                                                                                      \
-    hipLaunchKernelGGL((rows_act_quant_kernel<ACT, N>), grid, dim3(kThreads), 0, s, xp, rows, (int)cols, \
-                       rs, wp, eps, out, scale_out, hp);                                              \
+    (void)launch_args(reinterpret_cast<const void*>(&rows_act_quant_kernel<ACT, N>), grid, dim3(kThreads), \
+                      0, s, tm.start, tm.stop, xp, rows, (int)cols, rs, wp, eps, out, scale_out, hp); \
     return check_launch(name);                                                                        \
   }
   FLW_ACT_CASE(2) FLW_ACT_CASE(4) FLW_ACT_CASE(8)
