@@ -43,6 +43,7 @@ struct GemmParams {
   int64_t rs;
   float* part;         // split-K: fp32 partial sums [splits][M][N] instead of the bf16 epilogue
   int splits;          // K ranges per output tile (1: no split)
+  int lds_epi;         // epilogue staged through LDS (N % 8 == 0, 16-byte aligned y / residual rows)
 };
 
 // The epilogue value of one output: bf16(v), or bf16(residual + bf16(v)) -- x + linear(h) with
@@ -208,6 +209,75 @@ __device__ __forceinline__ v8i swz_frag(const uint8_t* tile, int rb, int kc, int
   return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
 
+// Epilogue staged through LDS, shared by the 256 x 256 kernels (the stage buffers are free after
+// the K loop, whose last step ends with a barrier): the scaled bf16 tile, 256 rows x 512 bytes,
+// rows 0-127 in st0 and 128-255 in st1 (64 KB each), 16-byte chunk c of row r at c ^ (r & 31);
+// then every wave stores whole row segments with 16-byte stores (a full 512-byte row per 32
+// lanes) instead of 8-byte pieces of 32 rows, and adds the optional residual row-wise.
+// Wave layout of acc (wave = 2 wm + wn): lane owns m = 64 wm + 32 j + lane % 32 and
+// n = 128 wn + 32 i + 8 g + 4 (lane / 32) + 0..3. Needs N % 8 == 0 and 16-byte aligned rows.
+__device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const float (&sxm)[2], const float* sw,
+                                                int sw_step, uint16_t* y, int64_t ys, const uint16_t* res,
+                                                int64_t rs, int M, int N, uint8_t* st0, uint8_t* st1, int m0,
+                                                int n0, int wave, int lane) {
+  const int wn = wave & 1, wm = wave >> 1, hh = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float swn[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = min(n0 + 128 * wn + 32 * i + 8 * g + 4 * hh, N - 4);
+      if (sw_step) {
+        const float4 v = *reinterpret_cast<const float4*>(sw + n);
+        swn[4 * g] = v.x; swn[4 * g + 1] = v.y; swn[4 * g + 2] = v.z; swn[4 * g + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) swn[4 * g + e] = sw[0];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 64 * wm + 32 * j + (lane & 31);
+      uint8_t* rowp = (r < 128 ? st0 : st1) + (r & 127) * 512;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const v16f& c = acc[i][j];
+        const int ch = 16 * wn + 4 * i + g;      // 16-byte chunk (8 n) of the row
+        uint2 w;
+        w.x = pack_bf16x2(c[4 * g] * sxm[j] * swn[4 * g], c[4 * g + 1] * sxm[j] * swn[4 * g + 1]);
+        w.y = pack_bf16x2(c[4 * g + 2] * sxm[j] * swn[4 * g + 2], c[4 * g + 3] * sxm[j] * swn[4 * g + 3]);
+        *reinterpret_cast<uint2*>(rowp + 16 * (ch ^ (r & 31)) + 8 * hh) = w;
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
+  lds_barrier();
+  // Wave w stores rows 32 w .. 32 w + 31, two rows (2 x 512 bytes) per instruction.
+#pragma unroll 4
+  for (int q = 0; q < 16; ++q) {
+    const int r = 32 * wave + 2 * q + (lane >> 5), ch = lane & 31;
+    const int m = m0 + r, n = n0 + 8 * ch;
+    const uint4 v = *reinterpret_cast<const uint4*>((r < 128 ? st0 : st1) + (r & 127) * 512 + 16 * (ch ^ (r & 31)));
+    if (m < M && n < N) {
+      uint4 o = v;
+      if (res) {
+        const uint4 rr = *reinterpret_cast<const uint4*>(res + (int64_t)m * rs + n);
+        const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {rr.x, rr.y, rr.z, rr.w};
+        uint32_t ov[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          ov[e] = pack_bf16x2(__uint_as_float(a[e] << 16) + __uint_as_float(b[e] << 16),
+                              __uint_as_float(a[e] & 0xFFFF0000u) + __uint_as_float(b[e] & 0xFFFF0000u));
+        o = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+      }
+      *reinterpret_cast<uint4*>(y + (int64_t)m * ys + n) = o;
+    }
+  }
+  // The next tile's loads refill st0 / st1: every wave's reads of the staged tile are done.
+  __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
+  lds_barrier();
+}
+
 // One 256 x 256 output tile: K loop over two LDS stages, then the scaled bf16 epilogue.
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
                                           int n0, int wave, int lane, int sbase, int nst, int split) {
@@ -297,6 +367,16 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
               make_float4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]);
         }
       }
+    return;
+  }
+  if (p.lds_epi) {
+    float sxm[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = min(m0 + 64 * wm + 32 * j + (lane & 31), p.M - 1);
+      sxm[j] = p.sx[(int64_t)m * p.sx_step];
+    }
+    staged_epilogue(acc, sxm, p.sw, p.sw_step, p.y, p.ys, p.res, p.rs, p.M, p.N, st0, st1, m0, n0, wave, lane);
     return;
   }
   float sxm[2];
@@ -432,6 +512,7 @@ constexpr int kWK = 64;                           // K per stage
 constexpr int kWXBytes = 256 * 128;               // X tile per stage (32 KB)
 constexpr int kWWBytes = 256 * 64;                // W tile per stage (16 KB)
 constexpr int kWStageBytes = kWXBytes + kWWBytes;
+constexpr int kWStageAlloc = 65536;               // >= kWStageBytes, and half of a staged bf16 tile
 
 typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
 
@@ -445,6 +526,7 @@ struct W8A16Params {
   int64_t ys;
   int M, N, K;
   int tiles_n, tiles_m;
+  int lds_epi;         // epilogue staged through LDS (N % 8 == 0, 16-byte aligned y rows)
 };
 
 __device__ __forceinline__ int wswz_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
@@ -543,6 +625,11 @@ __device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, u
     if (s + 1 < nst) step(s + 1, st1, st0);
   }
 
+  if (p.lds_epi) {
+    const float one[2] = {1.0f, 1.0f};
+    staged_epilogue(acc, one, p.sw, p.sw_step, p.y, p.ys, nullptr, 0, p.M, p.N, st0, st1, m0, n0, wave, lane);
+    return;
+  }
   // Epilogue: lane owns m = m0 + 64 wm + 32 j + lane % 32, n = n0 + 128 wn + 32 i + 8 g + 4 h + 0..3
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -578,8 +665,9 @@ __device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, u
 }
 
 __global__ __launch_bounds__(kFThreads, 1) void w8a16_gemm_kernel(W8A16Params p) {
-  __shared__ __align__(16) uint8_t st0[kWStageBytes];
-  __shared__ __align__(16) uint8_t st1[kWStageBytes];
+  // 64 KB each (a stage uses 48 KB): the staged epilogue needs 2 x 64 KB.
+  __shared__ __align__(16) uint8_t st0[kWStageAlloc];
+  __shared__ __align__(16) uint8_t st1[kWStageAlloc];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x;
@@ -656,6 +744,8 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
     FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
     // Split-K into the caller's workspace when the output has too few tiles to fill the GPU.
     p.splits = 1;
+    p.lds_epi = N % 8 == 0 && ys % 8 == 0 && ((uintptr_t)y & 15) == 0 &&
+                (res == nullptr || (rs % 8 == 0 && ((uintptr_t)res & 15) == 0));
     const size_t need = splitk_bytes(M, N, K);
     if (need && workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0 && N % 4 == 0) {
       p.splits = splitk_of(tiles, K);
@@ -699,6 +789,7 @@ static int w8a16_mm(const uint16_t* x, int64_t M, int64_t K, int64_t xs, const u
   p.x = x; p.xs = xs; p.w8 = w8; p.sw = sw; p.sw_step = sw_count == 1 ? 0 : 1;
   p.y = static_cast<uint16_t*>(y); p.ys = ys;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.lds_epi = N % 8 == 0 && ys % 8 == 0 && ((uintptr_t)y & 15) == 0;
   p.tiles_n = (int)((N + kFBN - 1) / kFBN);
   p.tiles_m = (int)((M + kFBM - 1) / kFBM);
   const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;

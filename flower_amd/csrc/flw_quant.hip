@@ -486,13 +486,14 @@ __global__ __launch_bounds__(kThreads) void cols_quant_t_kernel(const T* __restr
     *reinterpret_cast<uint2*>(lt + cj * kCTStride + 8 * rg) = make_uint2(w[0], w[1]);
   }
   __syncthreads();
-  // Store: thread t writes column t / 4, rows 64 (t % 4) .. + 63 of the tile, as 4 x 16 bytes.
+  // Store: thread t writes column t / 4, rows 64 q + 16 (t % 4) .. +15 for q = 0..3, so that
+  // each store instruction writes 64 contiguous bytes of every column it touches.
   const int cl = t >> 2, part = t & 3;
   const int64_t c = cb0 + cl;
   if (c < cols) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int rr = 64 * part + 16 * q;
+      const int rr = 64 * q + 16 * part;
       const int64_t r = (int64_t)blockIdx.y * kRT + rr;
       if (r < ld) {
         const uint2 a = *reinterpret_cast<const uint2*>(lt + cl * kCTStride + rr);
