@@ -52,6 +52,9 @@ SIGNATURES = {
                                 c_int, c_void_p, c_int, _P64, c_int64, c_int64, c_int64, c_int64,
                                 c_int64, c_void_p]),
     "flw_fp8_swa_workspace_bytes": (c_size_t, [c_int64] * 4),
+    "flw_fp8_swa_attention_forward_amax": (c_int, [c_void_p, c_void_p, c_void_p, c_int, _P64, c_int64, c_int64,
+                                                   c_int64, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p,
+                                                   c_void_p, c_size_t, c_void_p]),
     "flw_fp8_swa_attention_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_int, _P64, c_int64,
                                               c_int64, c_int64, c_int64, c_int64, c_int, c_void_p,
                                               c_void_p, c_void_p, c_size_t, c_void_p]),
@@ -64,6 +67,8 @@ SIGNATURES = {
     "flw_fp8_linear_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int]),
     "flw_fp8_linear": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                c_int64, c_int, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
+    "flw_fp8_scaled_mm_group_amax": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                             c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "flw_fp8_scaled_mm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "flw_fp8_scaled_mm_ws": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                      c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),

@@ -161,12 +161,25 @@ class Fp8DecoderBlock(nn.Module):
 
         att = self.attn
         c1, s1 = codes_of("rmsnorm", x2, d, self.ln1)
-        qkv = linear(c1, s1, qkv_l).view(B, T, 3 * d)
+        amax = None
+        if att.granularity == "head" and d % 128 == 0:
+            # QKV projection with the per-head |q|, |k|, |v| maxima from its epilogue: the
+            # attention's quantiser then needs no amax pass.
+            w8, ws = qkv_l.weight_codes()
+            N, K = w8.shape
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            amax = torch.empty(N // att.head_dim, dtype=torch.int32, device=dev)
+            _lib.check(lib.flw_fp8_scaled_mm_group_amax(c1.data_ptr(), M, K, w8.data_ptr(), N, s1.data_ptr(), M,
+                                                        ws.data_ptr(), ws.numel(), y.data_ptr(), N, att.head_dim,
+                                                        amax.data_ptr(), stream), "qkv + amax")
+            qkv = y.view(B, T, 3 * d)
+        else:
+            qkv = linear(c1, s1, qkv_l).view(B, T, 3 * d)
         q, k, v = (att._split(t) for t in qkv.chunk(3, dim=-1))
         a = torch.empty((B, T, d), dtype=torch.bfloat16, device=dev)
         window = T if att.local_window is None else att.local_window
         fp8_swa_attention_forward(q, k, v, window, granularity=att.granularity,
-                                  out=a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2))
+                                  out=a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2), amax=amax)
         ca, sa = codes_of("plain", a.view(M, d), d)
         x1 = linear(ca, sa, out_l, residual=x2)
         c2, s2 = codes_of("rmsnorm", x1, d, self.ln2)

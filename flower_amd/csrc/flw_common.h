@@ -26,6 +26,14 @@ Timer take_timer();
 // Re-arm (part of) a taken pair for an entry point that calls other entry points in turn.
 void arm_timer(Timer t);
 
+// e4m3 quantisation of 1-3 (B, H, T, D) tensors of one shape (flw_quant.hip): amax pass + quantise
+// pass, or, with amax_given ([tensor][scale group] |x| max bit patterns from the producer), the
+// quantise pass alone.
+int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
+                 int64_t D, const int64_t* strides, int granularity, const int* layouts,
+                 uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
+                 hipStream_t stream, Timer tm, const uint32_t* amax_given = nullptr);
+
 // Launch of a kernel taking one parameter struct, optionally recording start / stop events.
 template <typename P>
 inline hipError_t launch_ext(const void* kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream,

@@ -44,6 +44,8 @@ struct GemmParams {
   float* part;         // split-K: fp32 partial sums [splits][M][N] instead of the bf16 epilogue
   int splits;          // K ranges per output tile (1: no split)
   int lds_epi;         // epilogue staged through LDS (N % 8 == 0, 16-byte aligned y / residual rows)
+  uint32_t* gmax;      // optional: max |y| (fp32 bit patterns) per group of gcols output columns
+  int gcols;           // power of two in [8, 256]
 };
 
 // The epilogue value of one output: bf16(v), or bf16(residual + bf16(v)) -- x + linear(h) with
@@ -216,10 +218,14 @@ __device__ __forceinline__ v8i swz_frag(const uint8_t* tile, int rb, int kc, int
 // lanes) instead of 8-byte pieces of 32 rows, and adds the optional residual row-wise.
 // Wave layout of acc (wave = 2 wm + wn): lane owns m = 64 wm + 32 j + lane % 32 and
 // n = 128 wn + 32 i + 8 g + 4 (lane / 32) + 0..3. Needs N % 8 == 0 and 16-byte aligned rows.
+// With gmax, the max |y| over the tile's rows for each group of gcols columns (the per-head amax of
+// a QKV projection, gcols = head_dim) is reduced in the workgroup and folded into gmax with one
+// atomic max per group and tile (bit patterns of non-negative floats order as unsigned integers).
 __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const float (&sxm)[2], const float* sw,
                                                 int sw_step, uint16_t* y, int64_t ys, const uint16_t* res,
                                                 int64_t rs, int M, int N, uint8_t* st0, uint8_t* st1, int m0,
-                                                int n0, int wave, int lane) {
+                                                int n0, int wave, int lane, uint32_t* gmax = nullptr,
+                                                int gcols = 0) {
   const int wn = wave & 1, wm = wave >> 1, hh = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -253,6 +259,7 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
   __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
   lds_barrier();
   // Wave w stores rows 32 w .. 32 w + 31, two rows (2 x 512 bytes) per instruction.
+  uint32_t lm = 0;                                // max |y| bf16 bits of this lane's chunks
 #pragma unroll 4
   for (int q = 0; q < 16; ++q) {
     const int r = 32 * wave + 2 * q + (lane >> 5), ch = lane & 31;
@@ -271,11 +278,44 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
         o = make_uint4(ov[0], ov[1], ov[2], ov[3]);
       }
       *reinterpret_cast<uint4*>(y + (int64_t)m * ys + n) = o;
+      if (gmax) {
+        const uint32_t w4[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = w4[e] & 0x7FFFu, hi = (w4[e] >> 16) & 0x7FFFu;
+          lm = lm > lo ? lm : lo;
+          lm = lm > hi ? lm : hi;
+        }
+      }
     }
   }
   // The next tile's loads refill st0 / st1: every wave's reads of the staged tile are done.
   __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
   lds_barrier();
+  if (gmax) {
+    // Lanes ch .. ch + gcols / 8 - 1 of each half-wave cover one group's columns.
+    const int lpg = gcols >> 3;
+    for (int o = 1; o < lpg; o <<= 1) {
+      const uint32_t t = (uint32_t)__shfl_xor((int)lm, o, 64);
+      lm = lm > t ? lm : t;
+    }
+    const uint32_t t = (uint32_t)__shfl_xor((int)lm, 32, 64);
+    lm = lm > t ? lm : t;
+    uint32_t* red = reinterpret_cast<uint32_t*>(st0);          // [8 waves][32 groups at most]
+    const int ch = lane & 31;
+    if (lane < 32 && (ch & (lpg - 1)) == 0) red[wave * 32 + ch / lpg] = lm;
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    lds_barrier();
+    const int ngr = 256 / gcols, tid = wave * 64 + lane;
+    if (tid < ngr && n0 + tid * gcols < N) {
+      uint32_t mx = 0;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) mx = mx > red[w * 32 + tid] ? mx : red[w * 32 + tid];
+      atomicMax(gmax + (n0 / gcols) + tid, mx << 16);     // bf16 bits -> fp32 bits
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    lds_barrier();
+  }
 }
 
 // One 256 x 256 output tile: K loop over two LDS stages, then the scaled bf16 epilogue.
@@ -376,7 +416,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
       const int m = min(m0 + 64 * wm + 32 * j + (lane & 31), p.M - 1);
       sxm[j] = p.sx[(int64_t)m * p.sx_step];
     }
-    staged_epilogue(acc, sxm, p.sw, p.sw_step, p.y, p.ys, p.res, p.rs, p.M, p.N, st0, st1, m0, n0, wave, lane);
+    staged_epilogue(acc, sxm, p.sw, p.sw_step, p.y, p.ys, p.res, p.rs, p.M, p.N, st0, st1, m0, n0, wave, lane,
+                    p.gmax, p.gcols);
     return;
   }
   float sxm[2];
@@ -683,6 +724,11 @@ __global__ __launch_bounds__(kFThreads, 1) void w8a16_gemm_kernel(W8A16Params p)
   }
 }
 
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* p, int n, uint32_t v) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 // Compute units of the current device (queried once per device).
 static int compute_units() {
   static int cache[64] = {0};
@@ -719,7 +765,8 @@ static size_t splitk_bytes(int64_t M, int64_t N, int64_t K) {
 static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
                      const float* sx, int64_t sx_count, const float* sw, int64_t sw_count,
                      void* y, int64_t ys, hipStream_t s, const void* res = nullptr, int64_t rs = 0,
-                     void* workspace = nullptr, size_t workspace_bytes = 0) {
+                     void* workspace = nullptr, size_t workspace_bytes = 0, uint32_t* gmax = nullptr,
+                     int gcols = 0) {
   FLW_REQUIRE(x8 && w8 && sx && sw && y, FLW_E_INVALID, "null pointer argument");
   FLW_REQUIRE(M > 0 && N > 0 && K > 0, FLW_E_INVALID, "empty GEMM");
   FLW_REQUIRE(K % 16 == 0, FLW_E_UNSUPPORTED, "K must be a multiple of 16, got %lld", (long long)K);
@@ -754,7 +801,18 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
     // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per work item.
     const int64_t items = tiles * p.splits;
     const int64_t grid = items < compute_units() ? items : compute_units();
-    if (p.splits == 1) {
+    if (gmax) {
+      FLW_REQUIRE(p.splits == 1 && p.lds_epi, FLW_E_UNSUPPORTED,
+                  "the group amax needs an unsplit GEMM with N %% 8 == 0 and 16-byte aligned rows");
+      p.gmax = gmax;
+      p.gcols = gcols;
+      const Timer tm = take_timer();
+      const int ng = (int)(N / gcols);
+      (void)launch_args(reinterpret_cast<const void*>(&fill_u32_kernel), dim3((unsigned)((ng + 255) / 256)),
+                        dim3(256), 0, s, tm.start, nullptr, gmax, ng, 0u);
+      (void)launch_ext(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads),
+                       0, s, p, nullptr, tm.stop);
+    } else if (p.splits == 1) {
       (void)launch_timed(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
     } else {
       const Timer tm = take_timer();
@@ -824,6 +882,19 @@ extern "C" int flw_fp8_scaled_mm_ws(const uint8_t* x8, int64_t M, int64_t K, con
                                     size_t workspace_bytes, void* stream) {
   return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y, y_row_stride,
                    static_cast<hipStream_t>(stream), nullptr, 0, workspace, workspace_bytes);
+}
+
+extern "C" int flw_fp8_scaled_mm_group_amax(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
+                                            int64_t N, const float* x_scale, int64_t x_scale_count,
+                                            const float* w_scale, int64_t w_scale_count, void* y,
+                                            int64_t y_row_stride, int64_t group_cols, uint32_t* amax_out,
+                                            void* stream) {
+  FLW_REQUIRE(amax_out != nullptr, FLW_E_INVALID, "null amax_out");
+  FLW_REQUIRE(group_cols >= 8 && group_cols <= 256 && (group_cols & (group_cols - 1)) == 0 && N % group_cols == 0,
+              FLW_E_INVALID, "group_cols must be a power of two in [8, 256] dividing N");
+  FLW_REQUIRE(K % kFBK == 0, FLW_E_UNSUPPORTED, "the group amax needs K %% %d == 0", kFBK);
+  return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y, y_row_stride,
+                   static_cast<hipStream_t>(stream), nullptr, 0, nullptr, 0, amax_out, (int)group_cols);
 }
 
 extern "C" int flw_fp8_scaled_mm_residual(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,

@@ -43,6 +43,7 @@ struct QuantParams {
   int64_t nchunks;             // chunks per slice
   uint32_t* partials;          // [tensor][d0*d1][nchunks] |x| max bit patterns
   int granularity;
+  const uint32_t* amax_given;  // optional [tensor][groups] |x| max bit patterns (no amax pass)
 };
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t m, uint32_t* lds4) {
@@ -196,7 +197,10 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
   const int64_t i0 = slice / p.d1, i1 = slice % p.d1;
   const uint32_t* part = p.partials + (int64_t)zi * p.d0 * p.d1 * p.nchunks;
 
-  const float amax = __uint_as_float(group_amax(p, part, slice, i1, red));
+  const int64_t ngroups = p.granularity == FLW_SCALE_TENSOR ? 1 : (p.granularity == FLW_SCALE_HEAD ? p.d1 : p.d0 * p.d1);
+  const float amax = p.amax_given
+      ? __uint_as_float(p.amax_given[zi * ngroups + group_index(p.granularity, slice, i1)])
+      : __uint_as_float(group_amax(p, part, slice, i1, red));
   float scale;
   if (MODE == 1 && kBf16) {
     // base.py:198-199 under bf16: clamp and /448 are bf16 tensor ops
@@ -668,6 +672,10 @@ static int launch_quant(const QuantParams& p, int ntensors, int dtype, hipStream
                                     : reinterpret_cast<const void*>(&amax_kernel<uint16_t>);
   const void* kq = dtype == FLW_F32 ? reinterpret_cast<const void*>(&quant_kernel<float, MODE>)
                                     : reinterpret_cast<const void*>(&quant_kernel<uint16_t, MODE>);
+  if (p.amax_given) {                     // amax from the producer: the quantise pass only
+    (void)launch_ext(kq, grid, dim3(kThreads), lds, s, p, tm.start, tm.stop);
+    return check_launch(name);
+  }
   (void)launch_ext(ka, grid, dim3(kThreads), 0, s, p, tm.start, nullptr);
   (void)launch_ext(kq, grid, dim3(kThreads), lds, s, p, nullptr, tm.stop);
   return check_launch(name);
@@ -683,11 +691,11 @@ static void set_tensor(QTensor& t, const void* x, int64_t sb, int64_t sh, int64_
 int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
                  int64_t D, const int64_t* strides, int granularity, const int* layouts,
                  uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
-                 hipStream_t stream, Timer tm) {
+                 hipStream_t stream, Timer tm, const uint32_t* amax_given) {
   FLW_REQUIRE(n >= 1 && n <= 3, FLW_E_INVALID, "1 to 3 tensors per call");
   FLW_REQUIRE(granularity >= FLW_SCALE_TENSOR && granularity <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", granularity);
-  FLW_REQUIRE(ws != nullptr && ws_bytes >= (size_t)n * partial_bytes(B, H, T), FLW_E_WORKSPACE,
-              "workspace needs %zu bytes", (size_t)n * partial_bytes(B, H, T));
+  FLW_REQUIRE(amax_given != nullptr || (ws != nullptr && ws_bytes >= (size_t)n * partial_bytes(B, H, T)),
+              FLW_E_WORKSPACE, "workspace needs %zu bytes", (size_t)n * partial_bytes(B, H, T));
   QuantParams p{};
   for (int i = 0; i < n; ++i) {
     int rc = check_tensor(xs[i], dtype, B, H, T, D, strides[3 * i], strides[3 * i + 1], strides[3 * i + 2]);
@@ -705,6 +713,7 @@ int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, 
   }
   p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D;
   p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(ws); p.granularity = granularity;
+  p.amax_given = amax_given;
   return launch_quant<0>(p, n, dtype, stream, "flw_quant_e4m3", tm);
 }
 

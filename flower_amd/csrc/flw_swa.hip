@@ -368,10 +368,6 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   }
 }
 
-int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
-                 int64_t D, const int64_t* strides, int granularity, const int* layouts,
-                 uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
-                 hipStream_t stream, Timer tm);
 
 template <int D>
 static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s, Timer tm) {
@@ -457,12 +453,10 @@ extern "C" size_t flw_fp8_swa_workspace_bytes(int64_t B, int64_t H, int64_t T, i
   return swa_ws_layout(B, H, T, D).total;
 }
 
-extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, int dtype,
-                                             const int64_t* strides, int64_t B, int64_t H,
-                                             int64_t T, int64_t D, int64_t window,
-                                             int granularity, void* out, float* scales_out,
-                                             void* workspace, size_t workspace_bytes,
-                                             void* stream) {
+static int attention_forward(const void* q, const void* k, const void* v, int dtype, const int64_t* strides,
+                             int64_t B, int64_t H, int64_t T, int64_t D, int64_t window, int granularity,
+                             void* out, float* scales_out, void* workspace, size_t workspace_bytes,
+                             void* stream, const uint32_t* amax) {
   FLW_REQUIRE(strides != nullptr && workspace != nullptr, FLW_E_INVALID, "null strides / workspace");
   FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
   FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
@@ -483,9 +477,29 @@ extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const
   // the attention kernel.
   const Timer tm = take_timer();
   int rc = quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, scs,
-                        ws + w.partials, w.total - w.partials, s, Timer{tm.start, nullptr});
+                        ws + w.partials, w.total - w.partials, s, Timer{tm.start, nullptr}, amax);
   if (rc) return rc;
   const int64_t s8[3] = {H * T * D, T * D, D};
   return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, granularity, out, dtype, strides + 9,
                  B, H, T, D, window, s, Timer{nullptr, tm.stop});
+}
+
+extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, int dtype,
+                                             const int64_t* strides, int64_t B, int64_t H,
+                                             int64_t T, int64_t D, int64_t window,
+                                             int granularity, void* out, float* scales_out,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  return attention_forward(q, k, v, dtype, strides, B, H, T, D, window, granularity, out, scales_out,
+                           workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int flw_fp8_swa_attention_forward_amax(const void* q, const void* k, const void* v, int dtype,
+                                                  const int64_t* strides, int64_t B, int64_t H, int64_t T,
+                                                  int64_t D, int64_t window, int granularity,
+                                                  const uint32_t* amax, void* out, float* scales_out,
+                                                  void* workspace, size_t workspace_bytes, void* stream) {
+  FLW_REQUIRE(amax != nullptr, FLW_E_INVALID, "null amax");
+  return attention_forward(q, k, v, dtype, strides, B, H, T, D, window, granularity, out, scales_out,
+                           workspace, workspace_bytes, stream, amax);
 }

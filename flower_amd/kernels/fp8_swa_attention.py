@@ -93,13 +93,17 @@ def fp8_swa_attention_forward(
     num_stages: int = 3,
     granularity: str = "tensor",
     out: torch.Tensor | None = None,
+    amax: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """FP8 sliding-window causal attention forward.
 
     q/k/v: (B, H, T, D) bf16 or fp32 on the GPU. Returns (B, H, T, D) in q's dtype. ``out`` (an
     extension; the reference has no such argument): a (B, H, T, D) tensor of q's dtype, any
     strides with D contiguous -- e.g. the (B, T, H, D) head view of a (B, T, H*D) buffer -- that
-    the kernel writes in place and that is returned.
+    the kernel writes in place and that is returned. ``amax`` (an extension): the |x| maxima of q,
+    k, v per scale group, as int32 fp32 bit patterns [3 * groups] on the GPU (from the producer,
+    e.g. ``flw_fp8_scaled_mm_group_amax`` on the QKV projection): the quantiser then skips its
+    amax pass; the result is the same as without it.
     ``window``: each query attends to the ``window`` keys at or behind it (window <= 0 gives
     an all-zero output, as the reference's masking does).
 
@@ -142,10 +146,20 @@ def fp8_swa_attention_forward(
     so = out.stride()[:3]
     ws = _lib.workspace(lib.flw_fp8_swa_workspace_bytes(B, H, T, D), q.device)
     strides = _lib.i64s(*sq, *sk, *sv, *so)
-    rc = lib.flw_fp8_swa_attention_forward(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, strides, B, H, T, D, int(window),
-        _lib.GRANULARITY[granularity], out.data_ptr(), None, ws.data_ptr(), ws.numel(),
-        _lib.stream_of(q))
+    if amax is None:
+        rc = lib.flw_fp8_swa_attention_forward(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, strides, B, H, T, D, int(window),
+            _lib.GRANULARITY[granularity], out.data_ptr(), None, ws.data_ptr(), ws.numel(),
+            _lib.stream_of(q))
+    else:
+        groups = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+        if (amax.dtype != torch.int32 or amax.numel() != 3 * groups or amax.device != q.device
+                or not amax.is_contiguous()):
+            raise ValueError(f"amax must be a contiguous int32 tensor of {3 * groups} bit patterns on q's device")
+        rc = lib.flw_fp8_swa_attention_forward_amax(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, strides, B, H, T, D, int(window),
+            _lib.GRANULARITY[granularity], amax.data_ptr(), out.data_ptr(), None, ws.data_ptr(), ws.numel(),
+            _lib.stream_of(q))
     _lib.check(rc, "fp8_swa_attention_forward")
     return out
 

@@ -147,6 +147,16 @@ int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, i
                                   float* scales_out, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* flw_fp8_swa_attention_forward with the amax of Q, K and V supplied by their producer (u32
+ * [3 * (1 | H | B*H)], |x| max fp32 bit patterns in the order q, k, v, e.g. from
+ * flw_fp8_scaled_mm_group_amax): the quantiser's amax pass is skipped; scales, codes and the
+ * output are those of flw_fp8_swa_attention_forward on the same inputs. */
+int flw_fp8_swa_attention_forward_amax(const void* q, const void* k, const void* v, int dtype,
+                                       const int64_t* strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                                       int64_t window, int granularity, const uint32_t* amax, void* out,
+                                       float* scales_out, void* workspace, size_t workspace_bytes,
+                                       void* stream);
+
 /* The producer of an FP8 linear's input fused with its per-row quantiser (flw_quant_rows_e4m3
  * semantics: scale = max(amax / 448, 1e-12) per row, codes = e4m3(h / scale), no clamp), one read
  * of the bf16 rows [rows, cols] (row stride in elements, cols <= 4096, multiples of 8):
@@ -211,6 +221,19 @@ int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8
  * scaled and rounded to bf16 by a second kernel. Same result contract as flw_fp8_scaled_mm
  * (fp32 accumulation, summed in a different order). flw_fp8_scaled_mm_workspace_bytes returns 0
  * when no split applies; with a smaller workspace the call runs unsplit. */
+/* flw_fp8_scaled_mm that also returns, for every group of group_cols consecutive output columns,
+ * max |y| over all rows (as the fp32 bit pattern of the bf16 value, u32 [N / group_cols]): the
+ * per-head amax of a QKV projection (group_cols = head_dim, groups ordered q heads, k heads,
+ * v heads), so that the Q / K / V quantiser needs no amax pass of its own. This is the "fuse
+ * quantisation into the producer" step of the path: `qkv_heads` (flower/models/base.py:618-639)
+ * feeds `_per_tensor_fp8` (flower/kernels/fp8_swa_attention.py:195-205), whose amax this
+ * replaces. group_cols: a power of two in [8, 256] dividing N; K % 128 == 0, N % 8 == 0,
+ * 16-byte aligned y rows. amax_out is overwritten (cleared by the call itself). */
+int flw_fp8_scaled_mm_group_amax(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
+                                 const float* x_scale, int64_t x_scale_count, const float* w_scale,
+                                 int64_t w_scale_count, void* y, int64_t y_row_stride, int64_t group_cols,
+                                 uint32_t* amax_out, void* stream);
+
 size_t flw_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int flw_fp8_scaled_mm_ws(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
                          const float* x_scale, int64_t x_scale_count, const float* w_scale,

@@ -151,3 +151,20 @@ def test_reference_swa_attention_api_matches_oracle():
     got = to_np(reference_swa_attention(q, k, v, 17))
     from oracle.swa import swa_dense
     np.testing.assert_allclose(got, swa_dense(to_np(q), to_np(k), to_np(v), 17), rtol=1e-4, atol=1e-5)
+
+
+def test_attention_with_producer_amax_is_identical():
+    """fp8_swa_attention_forward(amax=...) with the per-head |q|, |k|, |v| maxima supplied (as the
+    QKV GEMM epilogue supplies them) skips the amax pass and returns the same output bit for bit."""
+    from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
+    g = torch.Generator().manual_seed(21)
+    B, H, T, D, W = 2, 4, 300, 64, 96
+    q, k, v = (torch.randn(B, H, T, D, generator=g).mul(torch.rand(1, H, 1, 1, generator=g) * 4)
+               .to("cuda", torch.bfloat16) for _ in range(3))
+    plain = fp8_swa_attention_forward(q, k, v, W, granularity="head")
+    amax = torch.cat([t.float().abs().amax(dim=(0, 2, 3)) for t in (q, k, v)]).view(torch.int32).contiguous()
+    given = fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, given)
+    with pytest.raises(ValueError, match="amax"):
+        fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax[:5])

@@ -322,3 +322,45 @@ def test_scaled_mm_residual_epilogue(M, N, K):
     bad = np.abs(got - ref) > tol
     assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance"
     assert (got == ref).mean() > 0.95
+
+
+@pytest.mark.parametrize("M,N,K,gcols", [(300, 768, 256, 64), (1024, 3072, 1024, 64), (513, 512, 128, 8),
+                                         (256, 1024, 384, 256), (64, 192, 128, 64)])
+def test_group_amax_epilogue(M, N, K, gcols):
+    """flw_fp8_scaled_mm_group_amax: y identical to flw_fp8_scaled_mm's, and amax_out[g] equal to
+    max |y[:, g*gcols:(g+1)*gcols]| over all rows (fp32 bit pattern of the bf16 maximum), called
+    twice on one buffer (the call clears it itself)."""
+    from flower_amd import _lib as L
+    lb = L.load()
+    x8, w8 = codes((M, K), 11), codes((N, K), 12)
+    rng = np.random.default_rng(13)
+    sx = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    tx8, tw8 = torch.from_numpy(x8).cuda(), torch.from_numpy(w8).cuda()
+    tsx, tsw = torch.from_numpy(sx).cuda(), torch.from_numpy(sw).cuda()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    y0 = torch.empty_like(y)
+    amax = torch.full((N // gcols,), -1, dtype=torch.int32, device="cuda")
+    for _ in range(2):
+        L.check(lb.flw_fp8_scaled_mm_group_amax(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), M,
+                                                tsw.data_ptr(), N, y.data_ptr(), N, gcols, amax.data_ptr(),
+                                                L.stream_of(y)), "group amax")
+    L.check(lb.flw_fp8_scaled_mm(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), M, tsw.data_ptr(), N,
+                                 y0.data_ptr(), N, L.stream_of(y)), "mm")
+    assert torch.equal(y, y0)
+    want = y.float().abs().reshape(M, N // gcols, gcols).amax(dim=(0, 2)).view(torch.int32)
+    assert torch.equal(amax, want)
+
+
+def test_group_amax_rejects_bad_groups():
+    from flower_amd import _lib as L
+    lb = L.load()
+    t = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    s = torch.ones(1024, device="cuda")
+    p = t.data_ptr()
+    rc = lb.flw_fp8_scaled_mm_group_amax(p, 128, 128, p, 96, s.data_ptr(), 128, s.data_ptr(), 96, p, 96, 48, p,
+                                         L.stream_of(t))
+    assert rc == 1 and b"power of two" in lb.flw_last_error()
+    rc = lb.flw_fp8_scaled_mm_group_amax(p, 128, 80, p, 128, s.data_ptr(), 128, s.data_ptr(), 128, p, 128, 64, p,
+                                         L.stream_of(t))
+    assert rc == 2 and b"K %" in lb.flw_last_error()
