@@ -150,6 +150,19 @@ def _spin_up(step, seconds=SPIN_UP_S):
         torch.cuda.synchronize()
 
 
+def _wall_ms(step, steps):
+    """Mean wall time of `steps` back-to-back steps in ms, bracketed by device synchronisation,
+    with nothing else in the loop: the whole-job throughput (`value`). Kernel times come from a
+    separate loop with the dispatch-recorded event pairs, whose recording would otherwise sit
+    inside this interval."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
 def _arm(lib, pair):
     """The next entry point called records this event pair from its own dispatches
     (flw_time_next_launch -> hipExtLaunchKernel): start with its first kernel, stop with its last,
@@ -208,6 +221,7 @@ def bench_attention(cfg, steps, warmup):
     for _ in range(warmup):
         step.quant(stream)
         step.attend(stream)
+    wall_ms = _wall_ms(lambda: (step.quant(stream), step.attend(stream)), steps)
     ev, kev = _events(steps), _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -221,7 +235,7 @@ def bench_attention(cfg, steps, warmup):
     quant_ms = np.array([e[0].elapsed_time(e[1]) for e in ev])
     attn_ms = np.array([e[0].elapsed_time(e[1]) for e in kev])
     B, H, T, D = q.shape
-    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, quant_ms=float(np.mean(quant_ms)),
+    return dict(wall_s=wall, ms_per_step=wall_ms, quant_ms=float(np.mean(quant_ms)),
                 attn_ms=float(np.mean(attn_ms)), attn_ms_min=float(np.min(attn_ms)),
                 flops=4 * D * B * H * in_window_pairs(T, cfg["W"]),
                 quant_bytes=3 * B * H * T * D * (2 * q.element_size() + 1), dtype=q.dtype)
@@ -253,6 +267,7 @@ def bench_gemm(cfg, steps, warmup):
     for _ in range(warmup):
         quant()
         gemm()
+    wall_ms = _wall_ms(lambda: (quant(), gemm()), steps)
     kev = _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -271,7 +286,7 @@ def bench_gemm(cfg, steps, warmup):
         b.record()
     torch.cuda.synchronize()
     q_ms = np.array([a.elapsed_time(b) for a, b in qev])
-    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, quant_ms=float(q_ms.mean()),
+    return dict(wall_s=wall, ms_per_step=wall_ms, quant_ms=float(q_ms.mean()),
                 gemm_ms=float(g_ms.mean()), gemm_ms_min=float(g_ms.min()), flops=2 * M * N * K,
                 quant_bytes=M * K * (2 * 2 + 1) + 4 * M, gemm_bytes=M * K + N * K + 2 * M * N + 4 * (M + N),
                 x=x, w=w)
@@ -297,6 +312,7 @@ def bench_gemm_w8a16(cfg, steps, warmup):
     _spin_up(gemm)
     for _ in range(warmup):
         gemm()
+    wall_ms = _wall_ms(gemm, steps)
     kev = _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -306,7 +322,7 @@ def bench_gemm_w8a16(cfg, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     g_ms = np.array([e[0].elapsed_time(e[1]) for e in kev])
-    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, gemm_ms=float(g_ms.mean()),
+    return dict(wall_s=wall, ms_per_step=wall_ms, gemm_ms=float(g_ms.mean()),
                 gemm_ms_min=float(g_ms.min()), flops=2 * M * N * K,
                 gemm_bytes=2 * M * K + N * K + 2 * M * N + 4 * N, x=x, w=w)
 
@@ -510,16 +526,16 @@ def run_block(cfg, args):
         _spin_up(lambda: blk(x))
         for _ in range(args.warmup):
             blk(x)
+        wall_ms = _wall_ms(lambda: blk(x), args.steps)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
         for a, b in ev:
             a.record()
             blk(x)
             b.record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
     ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    wall = wall_ms * 1e-3 * args.steps
     value = flops / (wall / args.steps) / 1e12
     return {
         "metric": "FP8 decoder block forward TFLOPS (linear + in-window attention FLOPs), BASELINE config 5",
@@ -564,6 +580,7 @@ def bench_swa_bf16(cfg, steps, warmup):
     for _ in range(warmup):
         fwd()
         bwd()
+    wall_ms = _wall_ms(lambda: (fwd(), bwd()), steps)
     fev, bev = _events(steps), _events(steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -577,7 +594,7 @@ def bench_swa_bf16(cfg, steps, warmup):
     f_ms = np.array([a.elapsed_time(b) for a, b in fev])
     b_ms = np.array([a.elapsed_time(b) for a, b in bev])
     pairs = B * H * in_window_pairs(T, W)
-    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, fwd_ms=float(f_ms.mean()), fwd_ms_min=float(f_ms.min()),
+    return dict(wall_s=wall, ms_per_step=wall_ms, fwd_ms=float(f_ms.mean()), fwd_ms_min=float(f_ms.min()),
                 bwd_ms=float(b_ms.mean()), bwd_ms_min=float(b_ms.min()), fwd_flops=4 * D * pairs,
                 bwd_flops=10 * D * pairs)
 
@@ -699,6 +716,7 @@ def bench_linear_train(cfg, steps, warmup):
     _spin_up(step)
     for _ in range(warmup):
         step()
+    wall_ms = _wall_ms(step, steps)
     ev = [_events(steps) for _ in calls]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -729,7 +747,7 @@ def bench_linear_train(cfg, steps, warmup):
     bf16 = {"fwd_ms": float(np.median([a.elapsed_time(b) for a, b, _, _ in tev])),
             "dgrad_ms": float(np.median([b.elapsed_time(c_) for _, b, c_, _ in tev])),
             "wgrad_ms": float(np.median([c_.elapsed_time(d) for _, _, c_, d in tev]))}
-    return dict(wall_s=wall, ms_per_step=wall / steps * 1e3, ms=ms, bf16=bf16, flops_gemm=2 * M * N * K,
+    return dict(wall_s=wall, ms_per_step=wall_ms, ms=ms, bf16=bf16, flops_gemm=2 * M * N * K,
                 x=x, w=w, g=g)
 
 
