@@ -487,7 +487,7 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
 // ---------------------------------------------------------------- backward: dQ
 
 template <int D>
-__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dq_kernel(SwaB16Params p) {
+__global__ __launch_bounds__(256, D == 128 ? 1 : 3) void swa_bf16_dq_kernel(SwaB16Params p) {
   constexpr int KS = D / 16, NDB = D / 32, NAT = 64 * D * 2;
   __shared__ __align__(16) uint8_t lk[2][NAT];     // K tile: A operand of S^T, read transposed for dQ^T
   __shared__ __align__(16) uint8_t lv[2][NAT];     // V tile, natural (A operand of dP^T)
