@@ -12,9 +12,10 @@
 //
 // The softmax is VALU-bound (per score: one FMA, one v_exp_f32 at half rate, half a max3, half a
 // convert, one add; per tile D/64 rescale multiplies per score) while the MFMA work per tile is
-// about a third of that, so the loop is arranged to keep the VALU fed: the QK^T MFMAs of tile
-// j+1 are issued before the softmax of tile j, whose PV MFMAs then run under the next tile's
-// VALU work; two workgroups per CU give every SIMD a second wave to interleave.
+// about a third of that. The MFMA work of one wave runs under the VALU work of the other waves
+// of its SIMD (up to four workgroups per CU at D <= 64: 115 VGPRs, 24 KB of LDS each); issuing
+// the next tile's QK^T before the current softmax was measured slower (its extra accumulators
+// cost a wave per SIMD).
 //
 // K tiles are staged in LDS in MFMA-fragment order (a permutation of 16-byte chunks of the
 // row-major tile); V arrives already in that order from the quantiser (FLW_LAYOUT_VTILE), so every
