@@ -82,6 +82,7 @@ DATA = {
 # 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0).
 TRAFFIC = {
     "c3": {"swa_fwd": 167_982_080, "quant": 504_024_064},
+    "c4": {"swa_fwd": 167_974_912, "quant": 503_960_576},
     "c2": {"gemm": 117_834_752, "w8a16": 134_490_112},
     "swa_bf16_450m": {"bwd": 554_757_120, "fwd": 169_459_712},
 }
