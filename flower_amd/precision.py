@@ -237,7 +237,11 @@ class _Fp8LinearFn(torch.autograd.Function):
         x, weight = ctx.saved_tensors
         g2 = g.reshape(-1, g.shape[-1])
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        fp8 = ctx.recipe in ("rowwise", "tensorwise") and getattr(ctx.mod, "backward_fp8", True)
+        N, K = weight.shape
+        # FP8 gradient GEMMs need 16-aligned dims (the conversion filter guarantees them; a
+        # hand-built Fp8Linear may not): otherwise the bf16 pair below.
+        fp8 = (ctx.recipe in ("rowwise", "tensorwise") and getattr(ctx.mod, "backward_fp8", True)
+               and N % 16 == 0 and K % 16 == 0)
         gx = gw = None
         if fp8 and (need_x or need_w):
             x2 = x.reshape(-1, x.shape[-1])
