@@ -82,3 +82,33 @@ def test_operators_refuse_cpu_tensors():
         _per_tensor_fp8(x)
     with pytest.raises(RuntimeError, match="GPU"):
         _fake_quant_e4m3(x)
+
+
+def test_limits_and_empty_shapes_are_refused_on_the_host():
+    """Maximum sizes and empty inputs are turned into errors before any device work (fake,
+    16-byte aligned pointers; nothing is dereferenced)."""
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = _lib.load()
+    P = 1 << 20                                  # a fake aligned "device" address
+    s64 = _lib.i64s(64 * 64, 64, 64)
+    so = _lib.i64s(64 * 64, 64, 64)
+    # one (b, h) slice of k8 must span < 2^31 bytes: T = 2^25 rows of D = 64 -> 2^31
+    rc = lib.flw_fp8_swa_fwd(P, _lib.i64s(0, 0, 64), P, _lib.i64s(0, 0, 64), P, P, P, P, 0, P, 1,
+                             _lib.i64s(0, 0, 64), 1, 1, 1 << 25, 64, 16, None)
+    assert rc == 2 and b"2^31" in lib.flw_last_error()
+    rc = lib.flw_fp8_swa_fwd(P, s64, P, s64, P, P, P, P, 0, P, 1, so, 1, 1, 0, 64, 16, None)
+    assert rc == 1 and b"empty" in lib.flw_last_error()
+    rc = lib.flw_swa_bf16_fwd(P, P, P, 1, 1, 128, 96, 16, P, P, None)
+    assert rc == 2 and b"head_dim" in lib.flw_last_error()
+    rc = lib.flw_swa_bf16_fwd(P, P, P, 1, 1, 128, 64, 0, P, P, None)
+    assert rc == 1 and b"window" in lib.flw_last_error()
+    rc = lib.flw_fp8_scaled_mm(P, 64, 40, P, 64, P, 64, P, 64, P, 64, None)
+    assert rc == 2 and b"multiple of 16" in lib.flw_last_error()
+    rc = lib.flw_fp8_scaled_mm(P, 0, 64, P, 64, P, 64, P, 64, P, 64, None)
+    assert rc == 1 and b"empty" in lib.flw_last_error()
+    rc = lib.flw_quant_rows_e4m3(P, _lib.BF16, 16, 12, 12, P, P, None)
+    assert rc == 1 and b"multiples of 8" in lib.flw_last_error()
+    rc = lib.flw_quant_cols_e4m3(P, _lib.BF16, 0, 64, 64, _lib.SCALE_COLUMN, P, 16, P, P, 1 << 20, None)
+    assert rc == 1 and b"empty" in lib.flw_last_error()
