@@ -171,9 +171,10 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   }
   uint4 kreg[CPT], vreg[CPT];
 
-  // K and V tiles through buffer descriptors of the (b, h) slice: the per-thread offset is fixed,
-  // the tile offset is a scalar, and K rows past T read as zero (they only meet queries past T,
-  // whose rows are not stored). The host checks that the slice fits a 31-bit extent.
+  // K and V tiles through buffer descriptors of the (b, h) slice: a fixed per-thread offset plus
+  // the tile offset, both in the VGPR operand (the one the range check covers), so K rows past T
+  // read as zero (they only meet queries past T, whose rows are not stored) and no load leaves
+  // the slice. The host checks that the slice fits a 31-bit extent.
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(kbase), 0, (int)((int64_t)(T - 1) * p.kst + D), kBufferFlags);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
     for (int j = 0; j < CPT; ++j) {
       const int i = tid + 256 * j;
       if (KCH % 256 == 0 || i < KCH) {
-        const auto kv = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)koff[j], ks, 0);
+        const auto kv = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)(koff[j] + (uint32_t)ks), 0, 0);
         const auto vv = __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * i, vs, 0);
         kreg[j] = make_uint4(kv[0], kv[1], kv[2], kv[3]);
         vreg[j] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
