@@ -469,6 +469,162 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
   }
 }
 
+// One 256 (n) x 128 (m) output tile (or its K range under split-K), for outputs with fewer
+// 256 x 256 tiles than compute units (twice the tiles, so the grid covers more of the GPU): 8 waves in a 4 x 2 grid of 64 x 64 wave tiles
+// (2 x 2 MFMAs per 64-deep K chunk), a stage holding the 256 W rows and 128 X rows (48 of its
+// 64 KB), the same swizzle, barriers and accumulation order as gemm_tile (the results are
+// identical), and the epilogue staged through st0 (128 rows x 512 bytes).
+__device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
+                                              int n0, int wave, int lane, int sbase, int nst, int split) {
+  const int wn = wave & 3, wm = wave >> 2;        // 64 n rows, 64 m columns
+  // Loads: 384 rows of 128 bytes per stage; wave w fills rows 48 w .. 48 w + 47 with 6
+  // instructions of 8 rows, rows 256 .. 383 being X rows 0 .. 127. Instruction t of a wave reads
+  // one operand (256 is a multiple of 8), so its base address is a scalar.
+  uint32_t goff[6];
+#pragma unroll
+  for (int t = 0; t < 6; ++t) {
+    const int row0 = 48 * wave + 8 * t;
+    const bool xop = row0 >= 256;
+    const int r = (xop ? row0 - 256 : row0) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int grow = xop ? min(m0 + r, p.M - 1) : min(n0 + r, p.N - 1);
+    goff[t] = (uint32_t)grow * (uint32_t)p.K + 16u * (uint32_t)c;
+  }
+  auto issue = [&](uint8_t* stage, int s) __attribute__((always_inline)) {
+    const uint32_t k0 = (uint32_t)(sbase + s) * kFBK;
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8_t*)stage;
+#pragma unroll
+    for (int t = 0; t < 6; ++t) {
+      const int row0 = 48 * wave + 8 * t;
+      const bool xop = row0 >= 256;
+      const uint32_t dst = lds + (xop ? kFOpBytes + (row0 - 256) * 128 : row0 * 128);
+      const uint8_t* src = xop ? p.x8 : p.w8;
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :: "s"(dst), "v"(goff[t] + k0), "s"(src) : "memory", "m0");
+    }
+  };
+
+  v16f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+  issue(st0, 0);
+  auto step = [&](int s, const uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+    if (s + 1 < nst) {
+      issue(nxt, s + 1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(6));   // this wave's loads of stage s landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    lds_barrier();                                // ... and every wave's
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      v8i a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = swz_frag(cur, 2 * wn + i, kc, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = swz_frag(cur + kFOpBytes, 2 * wm + j, kc, lane);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = gemm_mfma(a[i], b[j], acc[i][j]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
+    lds_barrier();
+  };
+  for (int s = 0; s < nst; s += 2) {
+    step(s, st0, st1);
+    if (s + 1 < nst) step(s + 1, st1, st0);
+  }
+
+  // Epilogue: lane owns m = m0 + 64 wm + 32 j + lane % 32, n = n0 + 64 wn + 32 i + 8 g + 4 hh + 0..3;
+  // the scaled bf16 tile goes to st0 (row r = m - m0, 16-byte chunk c at c ^ (r & 31)), then
+  // wave w stores rows 16 w .. 16 w + 15, two 512-byte rows per instruction. Split-K: unscaled
+  // fp32 partials, 16-byte stores.
+  const int hh = lane >> 5;
+  if (p.part) {
+    float* base = p.part + (int64_t)split * p.M * p.N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int m = m0 + 64 * wm + 32 * j + (lane & 31);
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + 64 * wn + 32 * i + 8 * g + 4 * hh;
+          if (n >= p.N) continue;
+          const v16f& c = acc[i][j];
+          *reinterpret_cast<float4*>(base + (int64_t)m * p.N + n) =
+              make_float4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]);
+        }
+      }
+    return;
+  }
+  float sxm[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int m = min(m0 + 64 * wm + 32 * j + (lane & 31), p.M - 1);
+    sxm[j] = p.sx[(int64_t)m * p.sx_step];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float swn[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = min(n0 + 64 * wn + 32 * i + 8 * g + 4 * hh, p.N - 4);
+      if (p.sw_step) {
+        const float4 v = *reinterpret_cast<const float4*>(p.sw + n);
+        swn[4 * g] = v.x; swn[4 * g + 1] = v.y; swn[4 * g + 2] = v.z; swn[4 * g + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) swn[4 * g + e] = p.sw[0];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 64 * wm + 32 * j + (lane & 31);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const v16f& c = acc[i][j];
+        const int ch = 8 * wn + 4 * i + g;
+        uint2 w;
+        w.x = pack_bf16x2(c[4 * g] * sxm[j] * swn[4 * g], c[4 * g + 1] * sxm[j] * swn[4 * g + 1]);
+        w.y = pack_bf16x2(c[4 * g + 2] * sxm[j] * swn[4 * g + 2], c[4 * g + 3] * sxm[j] * swn[4 * g + 3]);
+        *reinterpret_cast<uint2*>(st0 + r * 512 + 16 * (ch ^ (r & 31)) + 8 * hh) = w;
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);             // lgkmcnt(0)
+  lds_barrier();
+#pragma unroll 4
+  for (int q = 0; q < 8; ++q) {
+    const int r = 16 * wave + 2 * q + (lane >> 5), ch = lane & 31;
+    const int m = m0 + r, n = n0 + 8 * ch;
+    const uint4 v = *reinterpret_cast<const uint4*>(st0 + r * 512 + 16 * (ch ^ (r & 31)));
+    if (m < p.M && n < p.N) {
+      uint4 o = v;
+      if (p.res) {
+        const uint4 rr = *reinterpret_cast<const uint4*>(p.res + (int64_t)m * p.rs + n);
+        const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {rr.x, rr.y, rr.z, rr.w};
+        uint32_t ov[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          ov[e] = pack_bf16x2(__uint_as_float(a[e] << 16) + __uint_as_float(b[e] << 16),
+                              __uint_as_float(a[e] & 0xFFFF0000u) + __uint_as_float(b[e] & 0xFFFF0000u));
+        o = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+      }
+      *reinterpret_cast<uint4*>(p.y + (int64_t)m * p.ys + n) = o;
+    }
+  }
+  // The next tile's loads refill st0: every wave's reads of the staged tile are done.
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  lds_barrier();
+}
+
+template <int TM>
 __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p) {
   // One array per stage: every LDS access below names its stage at compile time, so the
   // compiler can see that the direct-to-LDS loads in flight write the other stage.
@@ -476,7 +632,6 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
   __shared__ __align__(16) uint8_t st1[kFStageBytes];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
 
   // Persistent over tiles: workgroup b takes tiles L, L + G, L + 2G, ... (G = grid size), so
   // the output stores of one tile drain while the next tile computes. L = (b % 8) (G / 8) + b / 8
@@ -486,8 +641,6 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
   const int G = gridDim.x;
   const int L = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   const int ntiles = p.tiles_n * p.tiles_m;
-  const int lane_w = lane;   // (kept for the loops below)
-  (void)lane_w;
 
   // Split-K: work item t = split * ntiles + tile; split s covers K stages [s nst / S, (s+1) nst / S).
   const int nst_all = p.K / kFBK;
@@ -499,7 +652,8 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
     const int tm = first_m + (tt % (kGroupM * p.tiles_n)) % gm;
     const int tn = (tt % (kGroupM * p.tiles_n)) / gm;
     const int s0 = split * nst_all / p.splits, s1 = (split + 1) * nst_all / p.splits;
-    gemm_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
+    if constexpr (TM == 256) gemm_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
+    else gemm_tile_128(p, st0, st1, tm * TM, tn * kFBN, wave, lane, s0, s1 - s0, split);
   }
 }
 
@@ -798,8 +952,18 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
       p.splits = splitk_of(tiles, K);
       p.part = static_cast<float*>(workspace);
     }
+    // Fewer 256 x 256 tiles than compute units: 256 x 128 tiles (twice as many), and then half
+    // the K ranges of a split (the same number of work items, half the partials to fold).
+    const bool narrow = p.lds_epi && gmax == nullptr && tiles < compute_units();
+    if (narrow) {
+      p.tiles_m = (int)((M + 127) / 128);
+      p.splits = p.splits / 2 > 1 ? p.splits / 2 : 1;
+      if (p.splits == 1) p.part = nullptr;
+    }
+    const void* kern = narrow ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<128>)
+                              : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256>);
     // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per work item.
-    const int64_t items = tiles * p.splits;
+    const int64_t items = (int64_t)p.tiles_n * p.tiles_m * p.splits;
     const int64_t grid = items < compute_units() ? items : compute_units();
     if (gmax) {
       FLW_REQUIRE(p.splits == 1 && p.lds_epi, FLW_E_UNSUPPORTED,
@@ -810,13 +974,12 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
       const int ng = (int)(N / gcols);
       (void)launch_args(reinterpret_cast<const void*>(&fill_u32_kernel), dim3((unsigned)((ng + 255) / 256)),
                         dim3(256), 0, s, tm.start, nullptr, gmax, ng, 0u);
-      (void)launch_ext(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads),
-                       0, s, p, nullptr, tm.stop);
+      (void)launch_ext(kern, dim3((unsigned)grid), dim3(kFThreads), 0, s, p, nullptr, tm.stop);
     } else if (p.splits == 1) {
-      (void)launch_timed(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
+      (void)launch_timed(kern, dim3((unsigned)grid), dim3(kFThreads), s, p);
     } else {
       const Timer tm = take_timer();
-      (void)launch_ext(reinterpret_cast<const void*>(&fp8_gemm_256_kernel), dim3((unsigned)grid), dim3(kFThreads),
+      (void)launch_ext(kern, dim3((unsigned)grid), dim3(kFThreads),
                        0, s, p, tm.start, nullptr);
       const int64_t quads = M * (N / 4);
       (void)launch_ext(reinterpret_cast<const void*>(&gemm_splitk_reduce_kernel), dim3((unsigned)((quads + 255) / 256)),
