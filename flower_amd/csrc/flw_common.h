@@ -25,6 +25,8 @@ struct Timer {
 Timer take_timer();
 // Re-arm (part of) a taken pair for an entry point that calls other entry points in turn.
 void arm_timer(Timer t);
+// Compute units of the current device (cached per device; 256 if the query fails).
+int compute_units();
 
 // e4m3 quantisation of 1-3 (B, H, T, D) tensors of one shape (flw_quant.hip): amax pass + quantise
 // pass, or, with amax_given ([tensor][scale group] |x| max bit patterns from the producer), the
@@ -77,6 +79,18 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return (u & 0x7FFFFFFFu) > 0x7F800000u ? 0x7FC0u : r;
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
+
+// f32_to_bf16_bits of two values, packed lo | hi << 16, by the converter (v_cvt_pk_bf16_f32:
+// round to nearest even, one instruction for both) with NaN made 0x7FC0 as above (the converter
+// keeps NaN payloads).
+typedef __bf16 flw_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float flw_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+  uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector((flw_f32x2{a, b}), flw_bf16x2));
+  w = a != a ? (w & 0xFFFF0000u) | 0x7FC0u : w;
+  w = b != b ? (w & 0x0000FFFFu) | 0x7FC00000u : w;
+  return w;
+}
 
 // fp32 -> OCP e4m3fn code, round to nearest even, NOT saturating (|x| >= 464+ -> NaN 0x7F),
 // NaN / inf -> sign | 0x7F. Integer-exact; the low byte of the result is the code.

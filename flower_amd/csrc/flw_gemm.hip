@@ -884,17 +884,6 @@ __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* p, int n, uint3
 }
 
 // Compute units of the current device (queried once per device).
-static int compute_units() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
 
 // K ranges per output tile for the 256 x 256 kernel: split when the tiles alone would leave more
 // than half of the compute units idle and each range keeps at least 4 K stages of 128. (Measured

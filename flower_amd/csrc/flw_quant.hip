@@ -558,10 +558,8 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
   }
   auto unpack = [](const uint4& q, float* f) __attribute__((always_inline)) { Vec16<uint16_t>::unpack(q, f); };
   auto pack = [](const float* f) __attribute__((always_inline)) {
-    return make_uint4(f32_to_bf16_bits(f[0]) | (f32_to_bf16_bits(f[1]) << 16),
-                      f32_to_bf16_bits(f[2]) | (f32_to_bf16_bits(f[3]) << 16),
-                      f32_to_bf16_bits(f[4]) | (f32_to_bf16_bits(f[5]) << 16),
-                      f32_to_bf16_bits(f[6]) | (f32_to_bf16_bits(f[7]) << 16));
+    return make_uint4(bf16x2_rne(f[0], f[1]), bf16x2_rne(f[2], f[3]), bf16x2_rne(f[4], f[5]),
+                      bf16x2_rne(f[6], f[7]));
   };
   if (ACT == kActRmsnorm) {
     float ss = 0.0f;
@@ -581,9 +579,13 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
       float f[8], g[8];
       unpack(hb[i], f);
       Vec16<uint16_t>::load(w + 8 * v, g);
+      uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = round_bf16(round_bf16(f[e] * r) * g[e]);
-      hb[i] = pack(f);
+      for (int e = 0; e < 4; ++e) {       // bf16(bf16(x r) w), two values per conversion
+        const uint32_t t = bf16x2_rne(f[2 * e] * r, f[2 * e + 1] * r);
+        o[e] = bf16x2_rne(__uint_as_float(t << 16) * g[2 * e], __uint_as_float(t & 0xFFFF0000u) * g[2 * e + 1]);
+      }
+      hb[i] = make_uint4(o[0], o[1], o[2], o[3]);
     }
   } else if (ACT == kActGelu) {
 #pragma unroll
