@@ -85,11 +85,16 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to
 // keeps NaN payloads).
 typedef __bf16 flw_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float flw_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_rne_raw(float a, float b) {   // NaN payloads kept
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((flw_f32x2{a, b}), flw_bf16x2));
+}
+// Every NaN half of a packed bf16 pair made 0x7FC0.
+__device__ __forceinline__ uint32_t bf16x2_canon_nan(uint32_t w) {
+  w = (w & 0x7FFFu) > 0x7F80u ? (w & 0xFFFF0000u) | 0x7FC0u : w;
+  return (w & 0x7FFF0000u) > 0x7F800000u ? (w & 0x0000FFFFu) | 0x7FC00000u : w;
+}
 __device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
-  uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector((flw_f32x2{a, b}), flw_bf16x2));
-  w = a != a ? (w & 0xFFFF0000u) | 0x7FC0u : w;
-  w = b != b ? (w & 0x0000FFFFu) | 0x7FC00000u : w;
-  return w;
+  return bf16x2_canon_nan(bf16x2_rne_raw(a, b));
 }
 
 // fp32 -> OCP e4m3fn code, round to nearest even, NOT saturating (|x| >= 464+ -> NaN 0x7F),

@@ -557,9 +557,10 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
     hb[i] = v < nvec ? *reinterpret_cast<const uint4*>(src + 8 * v) : make_uint4(0, 0, 0, 0);
   }
   auto unpack = [](const uint4& q, float* f) __attribute__((always_inline)) { Vec16<uint16_t>::unpack(q, f); };
+  // NaN halves keep their payload here and are made 0x7FC0 below, only in rows whose amax is NaN.
   auto pack = [](const float* f) __attribute__((always_inline)) {
-    return make_uint4(bf16x2_rne(f[0], f[1]), bf16x2_rne(f[2], f[3]), bf16x2_rne(f[4], f[5]),
-                      bf16x2_rne(f[6], f[7]));
+    return make_uint4(bf16x2_rne_raw(f[0], f[1]), bf16x2_rne_raw(f[2], f[3]), bf16x2_rne_raw(f[4], f[5]),
+                      bf16x2_rne_raw(f[6], f[7]));
   };
   if (ACT == kActRmsnorm) {
     float ss = 0.0f;
@@ -582,8 +583,8 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {       // bf16(bf16(x r) w), two values per conversion
-        const uint32_t t = bf16x2_rne(f[2 * e] * r, f[2 * e + 1] * r);
-        o[e] = bf16x2_rne(__uint_as_float(t << 16) * g[2 * e], __uint_as_float(t & 0xFFFF0000u) * g[2 * e + 1]);
+        const uint32_t t = bf16x2_rne_raw(f[2 * e] * r, f[2 * e + 1] * r);
+        o[e] = bf16x2_rne_raw(__uint_as_float(t << 16) * g[2 * e], __uint_as_float(t & 0xFFFF0000u) * g[2 * e + 1]);
       }
       hb[i] = make_uint4(o[0], o[1], o[2], o[3]);
     }
@@ -598,19 +599,24 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
       __builtin_amdgcn_sched_barrier(0);        // one vector's erf at a time: bounded registers
     }
   }
-  uint32_t m = 0;
+  // |h| maxima as 16-bit halves (v_pk_max_u16 over the bf16 bit patterns: NaN above inf).
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 m2 = {0, 0};
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const uint32_t q[4] = {hb[i].x, hb[i].y, hb[i].z, hb[i].w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = (q[e] << 16) & 0x7FFFFFFFu, hi = q[e] & 0x7FFF0000u;
-      m = m > lo ? m : lo;
-      m = m > hi ? m : hi;
-    }
+    for (int e = 0; e < 4; ++e) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, q[e] & 0x7FFF7FFFu));
   }
+  uint32_t m = (uint32_t)(m2[0] > m2[1] ? m2[0] : m2[1]) << 16;
   m = wave_max_u32(m);
   const float amax = __uint_as_float(m);
+  if (ACT != kActNone && __builtin_isnan(amax)) {   // wave-uniform, rare: NaN h as 0x7FC0
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      hb[i] = make_uint4(bf16x2_canon_nan(hb[i].x), bf16x2_canon_nan(hb[i].y), bf16x2_canon_nan(hb[i].z),
+                         bf16x2_canon_nan(hb[i].w));
+  }
   float sc = amax / kE4m3Max;
   sc = sc < kEps ? kEps : sc;
   if (lane == 0) scale_out[row] = sc;

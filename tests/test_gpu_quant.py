@@ -491,3 +491,42 @@ def test_gelu_quant_rows(rows, cols):
     want_c, want_s = rowwise_fp8(got)
     np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
     np.testing.assert_array_equal(to_np(sc), want_s.reshape(-1))
+
+
+@pytest.mark.parametrize("act", ["rmsnorm", "gelu"])
+def test_fused_row_quantisers_nan_rows(act):
+    """A NaN in a row: h carries the canonical bf16 NaN 0x7FC0 (torch's float -> bf16 rounding) where
+    it is NaN, and that row's scale and codes follow the per-row quantiser on the kernel's own h;
+    the other rows are unaffected."""
+    L = lib()
+    lb = L.load()
+    rows, cols = 8, 1024
+    g = torch.Generator().manual_seed(99)
+    x = (torch.randn(rows, cols, generator=g) * 3).to(torch.bfloat16)
+    xn = x.clone()
+    xn[3, 17] = float("nan")
+    w = (1 + 0.2 * torch.randn(cols, generator=g)).to(torch.bfloat16).cuda()
+    outs = []
+    for inp in (x, xn):
+        tx = inp.cuda()
+        codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+        sc = torch.empty(rows, dtype=torch.float32, device="cuda")
+        h = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
+        if act == "rmsnorm":
+            rc = lb.flw_rmsnorm_quant_rows_e4m3(tx.data_ptr(), rows, cols, cols, w.data_ptr(), 1e-6, codes.data_ptr(),
+                                                sc.data_ptr(), h.data_ptr(), L.stream_of(tx))
+        else:
+            rc = lb.flw_gelu_quant_rows_e4m3(tx.data_ptr(), rows, cols, cols, codes.data_ptr(), sc.data_ptr(),
+                                             h.data_ptr(), L.stream_of(tx))
+        L.check(rc, act)
+        torch.cuda.synchronize()
+        outs.append((codes.cpu(), sc.cpu(), h.cpu()))
+    (c0, s0, h0), (c1, s1, h1) = outs
+    keep = torch.arange(rows) != 3
+    assert torch.equal(c0[keep], c1[keep]) and torch.equal(s0[keep], s1[keep]) and torch.equal(h0[keep], h1[keep])
+    hb = h1[3].view(torch.int16).numpy().astype(np.uint16)
+    nan = np.isnan(h1[3].float().numpy())
+    assert nan.any() and (hb[nan] == 0x7FC0).all()
+    assert np.isnan(s1[3].item())
+    want_c, _ = rowwise_fp8(h1[3:4].float().numpy())
+    np.testing.assert_array_equal(c1[3:4].numpy(), want_c)
