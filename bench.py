@@ -59,6 +59,10 @@ WORKLOADS = {
     "c3": dict(B=4, H=16, T=8192, D=64, W=1024, granularity="head", inputs="lognormal_heads"),
     "c4": dict(B=1, H=16, T=32768, D=64, W=4096, granularity="head", inputs="student_t_channels"),
     "c1": dict(B=1, H=8, T=1024, D=64, W=256, granularity="tensor", inputs="randn_fp32"),
+    # the reference's own published FP8 measurement shape (fp8_swa_attention.py:39-46: 0.431 ms
+    # on an RTX 5090, per-tensor scales) -- other hardware, so context only, not a baseline
+    "ref_fp8": dict(B=1, H=20, T=4096, D=64, W=2048, granularity="tensor", inputs="randn_bf16",
+                    label="the reference's published FP8 measurement shape B1 H20 T4096 D64 W2048"),
     "c2": dict(M=8192, N=4096, K=1024, outlier_frac=0.001, outlier_scale=20.0, w_std=0.02),
     "c5": dict(B=1, T=32768, d_model=1024, num_heads=16, ffn_dim=4096, W=4096, w_std=0.02),
     # the C2 linear as a training step: forward + FP8 dgrad + FP8 wgrad (rowwise recipe)
@@ -72,6 +76,7 @@ DATA = {
     "lognormal_heads": "synthetic (seeded; bf16 N(0,1) x a lognormal(0,1) factor per head)",
     "student_t_channels": "synthetic (seeded; bf16 N(0,1), 4 of 64 channels Student-t nu=4)",
     "randn_fp32": "synthetic (seeded; fp32 N(0,1))",
+    "randn_bf16": "synthetic (seeded; bf16 N(0,1))",
     "c2": "synthetic (seeded; bf16 x N(0,1) with 0.1% outliers x20; weight N(0,0.02), random init)",
     "c5": "synthetic (seeded; bf16 x N(0,1); every Linear weight N(0,0.02), random init)",
     "swa_bf16": "synthetic (seeded; bf16 q, k, v, dO ~ N(0,1))",
@@ -104,6 +109,8 @@ def make_inputs(cfg, seed=0):
             chi2 = torch.randn(B, H, T, 4, 4, generator=g).square().sum(-1)
             x[..., ch] = z / (chi2 / 4.0).sqrt()
             out.append(x.to(torch.bfloat16))
+        elif cfg["inputs"] == "randn_bf16":
+            out.append(torch.randn(B, H, T, D, generator=g).to(torch.bfloat16))
         else:
             out.append(torch.randn(B, H, T, D, generator=g))
     return out
@@ -449,7 +456,7 @@ def run_attention(cfg, args):
         "vs_baseline": None,
         "dtype": "fp8_e4m3 (fp32 accumulate)",
         "data": DATA[cfg["inputs"]],
-        "config": {"workload": f"fp8_swa_attention_forward, BASELINE {args.workload.upper()}",
+        "config": {"workload": "fp8_swa_attention_forward, " + cfg.get("label", f"BASELINE {args.workload.upper()}"),
                    "B": cfg["B"], "H": cfg["H"], "T": cfg["T"], "D": cfg["D"], "window": cfg["W"],
                    "causal": True, "scales": cfg["granularity"], "input_dtype": dt},
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP8_PEAK_TFLOPS,
