@@ -411,8 +411,9 @@ def main():
                          "the HBM byte counters of a rocprofv3 --pmc run")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs on exactly one GPU (every box here has one); how the path "
-              "would shard across GPUs is described in DESIGN.md. Use --gpus 1.", file=sys.stderr)
+        print("bench.py: this build runs on exactly one GPU (every box here has one); it measures "
+              "one GPU's share of the work (attention shards by batch and head with no "
+              "communication). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
