@@ -166,4 +166,21 @@ template <> struct Vec16<uint16_t> {   // bf16
   }
 };
 
+// LDS pointer type: the 32-bit LDS address of a __shared__ object is (uint32_t)(lds_u8_t*)p.
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
+// (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt / lgkmcnt left free).
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// Workgroup barrier without the release fence __syncthreads() carries (which would drain every
+// outstanding global load, i.e. the whole prefetch, at each K step). Callers wait for the loads
+// they need with an explicit vmcnt first; the empty asm statements keep the compiler from moving
+// memory operations across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace flw

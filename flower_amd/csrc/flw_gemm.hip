@@ -177,23 +177,8 @@ constexpr int kGroupM = 4;                        // m-tiles per tile group (L2 
 constexpr int kFOpBytes = 256 * kFBK;             // one operand tile per stage (32 KB)
 constexpr int kFStageBytes = 2 * kFOpBytes;       // W tile then X tile
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
-// (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt / lgkmcnt left free).
-constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-
-// Workgroup barrier without the release fence __syncthreads() carries (which would drain every
-// outstanding global load, i.e. the whole prefetch, at each K step). Callers wait for the loads
-// they need with an explicit vmcnt first; the empty asm statements keep the compiler from moving
-// memory operations across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
