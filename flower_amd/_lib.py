@@ -33,6 +33,10 @@ SIGNATURES = {
     "flw_vtile_bytes": (c_size_t, [c_int64] * 4),
     "flw_quant_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                                c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "flw_amax_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                              c_int64, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "flw_quant_e4m3_amax": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                    c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "flw_quant_qkv_e4m3": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                    c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_size_t, c_void_p]),

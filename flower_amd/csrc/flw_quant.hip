@@ -733,6 +733,41 @@ int quant_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_
                       ws_bytes, stream, take_timer());
 }
 
+// One workgroup per scale group (grid.x) folds that group's amax partials into amax_out.
+__global__ __launch_bounds__(kThreads) void amax_fold_kernel(QuantParams p, uint32_t* __restrict__ amax_out) {
+  __shared__ uint32_t red[kThreads / 64];
+  const int64_t g = blockIdx.x;
+  const int64_t slice = p.granularity == FLW_SCALE_BH ? g : 0;
+  const int64_t i1 = p.granularity == FLW_SCALE_HEAD ? g : slice % p.d1;
+  const uint32_t m = group_amax(p, p.partials, slice, i1, red);
+  if (threadIdx.x == 0) amax_out[g] = m;
+}
+
+// The amax pass alone: |x| max per scale group, as the bit patterns of non-negative fp32 values.
+int amax_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t sb,
+              int64_t sh, int64_t st, int granularity, uint32_t* amax_out, void* ws,
+              size_t ws_bytes, hipStream_t stream) {
+  int rc = check_tensor(x, dtype, B, H, T, D, sb, sh, st);
+  if (rc) return rc;
+  FLW_REQUIRE(granularity >= FLW_SCALE_TENSOR && granularity <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", granularity);
+  FLW_REQUIRE(amax_out != nullptr, FLW_E_INVALID, "null amax output");
+  FLW_REQUIRE(ws != nullptr && ws_bytes >= partial_bytes(B, H, T), FLW_E_WORKSPACE, "workspace needs %zu bytes",
+              partial_bytes(B, H, T));
+  QuantParams p{};
+  set_tensor(p.t[0], x, sb, sh, st, D, FLW_LAYOUT_BHTD, nullptr, nullptr, nullptr);
+  p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D;
+  p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(ws); p.granularity = granularity;
+  const int64_t G = granularity == FLW_SCALE_TENSOR ? 1 : (granularity == FLW_SCALE_HEAD ? H : B * H);
+  const void* ka = dtype == FLW_F32 ? reinterpret_cast<const void*>(&amax_kernel<float>)
+                                    : reinterpret_cast<const void*>(&amax_kernel<uint16_t>);
+  const Timer tm = take_timer();
+  (void)launch_ext(ka, dim3((unsigned)p.nchunks, (unsigned)(B * H), 1u), dim3(kThreads), 0, stream, p,
+                   tm.start, nullptr);
+  (void)launch_args(reinterpret_cast<const void*>(&amax_fold_kernel), dim3((unsigned)G), dim3(kThreads), 0,
+                    stream, nullptr, tm.stop, p, amax_out);
+  return check_launch("flw_amax_e4m3");
+}
+
 // ---------------------------------------------------------------- diagnostics
 
 // mode 0: IEEE x / s;  mode 1: the quantiser's reciprocal-and-correct quotient.
@@ -765,6 +800,23 @@ extern "C" int flw_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, in
                               size_t workspace_bytes, void* stream) {
   return quant_bhtd(x, dtype, B, H, T, D, stride_b, stride_h, stride_t, granularity, layout, out,
                     scale_out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int flw_amax_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                             int64_t stride_b, int64_t stride_h, int64_t stride_t, int granularity,
+                             uint32_t* amax_out, void* workspace, size_t workspace_bytes, void* stream) {
+  return amax_bhtd(x, dtype, B, H, T, D, stride_b, stride_h, stride_t, granularity, amax_out, workspace,
+                   workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int flw_quant_e4m3_amax(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                                   int64_t stride_b, int64_t stride_h, int64_t stride_t, int granularity,
+                                   int layout, const uint32_t* amax, uint8_t* out, float* scale_out,
+                                   void* stream) {
+  FLW_REQUIRE(amax != nullptr, FLW_E_INVALID, "null amax");
+  const int64_t strides[3] = {stride_b, stride_h, stride_t};
+  return quant_bhtd_n(1, &x, dtype, B, H, T, D, strides, granularity, &layout, &out, &scale_out, nullptr, 0,
+                      static_cast<hipStream_t>(stream), take_timer(), amax);
 }
 
 extern "C" int flw_quant_qkv_e4m3(const void* q, const void* k, const void* v, int dtype, int64_t B,

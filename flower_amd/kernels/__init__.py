@@ -1,6 +1,7 @@
 """HIP (gfx950) kernels behind the reference's ``flower.kernels`` operator API."""
 
-from .fp8_swa_attention import (E4M3_MAX, _per_tensor_fp8, fp8_swa_attention_forward,
-                                reference_swa_attention)
+from .fp8_swa_attention import (E4M3_MAX, _per_tensor_fp8, amax_e4m3, fp8_swa_attention_forward,
+                                quantize_e4m3_with_amax, reference_swa_attention)
 
-__all__ = ["E4M3_MAX", "_per_tensor_fp8", "fp8_swa_attention_forward", "reference_swa_attention"]
+__all__ = ["E4M3_MAX", "_per_tensor_fp8", "amax_e4m3", "fp8_swa_attention_forward",
+           "quantize_e4m3_with_amax", "reference_swa_attention"]

@@ -48,16 +48,8 @@ def _prepare(x: torch.Tensor):
     return x, s
 
 
-def _per_tensor_fp8(x: torch.Tensor, granularity: str = "tensor"):
-    """e4m3 quantisation with an amax scale: (x_e4m3, scale).
-
-    scale = max(amax, 1e-12) / 448 in fp32; codes = e4m3(clamp(x / scale, -448, 448)), with IEEE
-    division and round-to-nearest-even. ``scale`` is a float32 device tensor of 1 (tensor),
-    H (head) or B*H (bh) elements; ``float(scale)`` is the reference's Python float.
-    Accepts any shape for per-tensor scaling; per-head / per-(b, h) need (B, H, T, D).
-    """
-    lib = _lib.load()
-    _lib.require_gpu(x)
+def _as_bhtd(x: torch.Tensor, granularity: str):
+    """x as a (B, H, T, D) tensor with 16-byte rows, its strides and its scale-group count."""
     if x.numel() == 0:
         raise ValueError("cannot quantise an empty tensor")
     shape = x.shape
@@ -68,9 +60,23 @@ def _per_tensor_fp8(x: torch.Tensor, granularity: str = "tensor"):
         x4 = x.reshape(1, 1, -1, last)
     else:
         raise ValueError(f"expected (B, H, T, D) for {granularity} scales, got {tuple(shape)}")
-    x4, (sb, sh, st) = _prepare(x4)
+    x4, strides = _prepare(x4)
     B, H, T, D = x4.shape
-    G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+    return x4, strides, {"tensor": 1, "head": H, "bh": B * H}[granularity]
+
+
+def _per_tensor_fp8(x: torch.Tensor, granularity: str = "tensor"):
+    """e4m3 quantisation with an amax scale: (x_e4m3, scale).
+
+    scale = max(amax, 1e-12) / 448 in fp32; codes = e4m3(clamp(x / scale, -448, 448)), with IEEE
+    division and round-to-nearest-even. ``scale`` is a float32 device tensor of 1 (tensor),
+    H (head) or B*H (bh) elements; ``float(scale)`` is the reference's Python float.
+    Accepts any shape for per-tensor scaling; per-head / per-(b, h) need (B, H, T, D).
+    """
+    lib = _lib.load()
+    _lib.require_gpu(x)
+    x4, (sb, sh, st), G = _as_bhtd(x, granularity)
+    B, H, T, D = x4.shape
     out = torch.empty((B, H, T, D), dtype=torch.uint8, device=x.device)
     scale = torch.empty(G, dtype=torch.float32, device=x.device)
     ws = _lib.workspace(lib.flw_quant_workspace_bytes(B, H, T, D), x.device)
@@ -78,7 +84,47 @@ def _per_tensor_fp8(x: torch.Tensor, granularity: str = "tensor"):
                             _lib.GRANULARITY[granularity], _lib.LAYOUT_BHTD, out.data_ptr(),
                             scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
     _lib.check(rc, "_per_tensor_fp8")
-    return out.view(torch.float8_e4m3fn).reshape(shape), scale
+    return out.view(torch.float8_e4m3fn).reshape(x.shape), scale
+
+
+def amax_e4m3(x: torch.Tensor, granularity: str = "tensor") -> torch.Tensor:
+    """The amax pass of ``_per_tensor_fp8`` alone (fp8_swa_attention.py:201): |x| max per scale
+    group as a float32 device tensor of 1, H or B*H elements (NaN propagates).
+
+    For a tensor split across shards: each shard's amax, combined with an all_reduce(MAX) (it can
+    run on ``amax.view(torch.int32)``: non-negative floats order like their bit patterns), then
+    ``quantize_e4m3_with_amax`` on every shard gives the codes and scale of the whole tensor.
+    """
+    lib = _lib.load()
+    _lib.require_gpu(x)
+    x4, (sb, sh, st), G = _as_bhtd(x, granularity)
+    B, H, T, D = x4.shape
+    amax = torch.empty(G, dtype=torch.float32, device=x.device)
+    ws = _lib.workspace(lib.flw_quant_workspace_bytes(B, H, T, D), x.device)
+    rc = lib.flw_amax_e4m3(x4.data_ptr(), _lib.dtype_code(x.dtype), B, H, T, D, sb, sh, st,
+                           _lib.GRANULARITY[granularity], amax.data_ptr(), ws.data_ptr(), ws.numel(),
+                           _lib.stream_of(x))
+    _lib.check(rc, "amax_e4m3")
+    return amax
+
+
+def quantize_e4m3_with_amax(x: torch.Tensor, amax: torch.Tensor, granularity: str = "tensor"):
+    """``_per_tensor_fp8`` with the amax given (a float32 device tensor of 1, H or B*H elements,
+    e.g. ``amax_e4m3`` combined across shards): (x_e4m3, scale), the quantise pass only."""
+    lib = _lib.load()
+    _lib.require_gpu(x)
+    x4, (sb, sh, st), G = _as_bhtd(x, granularity)
+    if amax.dtype != torch.float32 or amax.numel() != G or amax.device != x.device:
+        raise ValueError(f"amax must be a float32 tensor of {G} elements on {x.device}")
+    amax = amax.contiguous()
+    B, H, T, D = x4.shape
+    out = torch.empty((B, H, T, D), dtype=torch.uint8, device=x.device)
+    scale = torch.empty(G, dtype=torch.float32, device=x.device)
+    rc = lib.flw_quant_e4m3_amax(x4.data_ptr(), _lib.dtype_code(x.dtype), B, H, T, D, sb, sh, st,
+                                 _lib.GRANULARITY[granularity], _lib.LAYOUT_BHTD, amax.data_ptr(),
+                                 out.data_ptr(), scale.data_ptr(), _lib.stream_of(x))
+    _lib.check(rc, "quantize_e4m3_with_amax")
+    return out.view(torch.float8_e4m3fn).reshape(x.shape), scale
 
 
 def fp8_swa_attention_forward(

@@ -64,6 +64,24 @@ int flw_time_next_launch(void* start_event, void* stop_event);
 /* Workspace for flw_quant_e4m3 / flw_fake_quant_e4m3 on a (B, H, T, D) tensor (amax partials). */
 size_t flw_quant_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
 
+/* The amax pass of `_per_tensor_fp8` (flower/kernels/fp8_swa_attention.py:201,
+ * `x.abs().amax().float()`) on its own: |x| max per scale group (granularity: 1, H or B*H groups)
+ * written to amax_out as the bit patterns of the fp32 values. Non-negative floats order like
+ * their bit patterns, so shards can combine their amax with an integer all_reduce(MAX) before
+ * quantising with flw_quant_e4m3_amax; NaN propagates (its pattern is above +inf's).
+ * workspace: flw_quant_workspace_bytes(B, H, T, D). x as for flw_quant_e4m3. */
+int flw_amax_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                  int64_t stride_b, int64_t stride_h, int64_t stride_t, int granularity,
+                  uint32_t* amax_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* flw_quant_e4m3 with the amax given (amax: the groups' |x| max bit patterns, e.g. from
+ * flw_amax_e4m3, combined across shards): the quantise pass only, no workspace. Same scale and
+ * code arithmetic, so flw_quant_e4m3_amax(x, flw_amax_e4m3(x)) == flw_quant_e4m3(x) bit for bit. */
+int flw_quant_e4m3_amax(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                        int64_t stride_b, int64_t stride_h, int64_t stride_t, int granularity,
+                        int layout, const uint32_t* amax, uint8_t* out, float* scale_out,
+                        void* stream);
+
 /* Bytes of a FLW_LAYOUT_VTILE buffer for a (B, H, T, D) tensor: B*H*ceil(T/64)*64*D. */
 size_t flw_vtile_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
 

@@ -112,3 +112,10 @@ def test_limits_and_empty_shapes_are_refused_on_the_host():
     assert rc == 1 and b"multiples of 8" in lib.flw_last_error()
     rc = lib.flw_quant_cols_e4m3(P, _lib.BF16, 0, 64, 64, _lib.SCALE_COLUMN, P, 16, P, P, 1 << 20, None)
     assert rc == 1 and b"empty" in lib.flw_last_error()
+    rc = lib.flw_quant_e4m3_amax(P, _lib.BF16, 1, 2, 64, 64, 8192, 4096, 64, _lib.SCALE_HEAD,
+                                 _lib.LAYOUT_BHTD, None, P, P, None)
+    assert rc == 1 and b"null amax" in lib.flw_last_error()
+    rc = lib.flw_amax_e4m3(P, _lib.BF16, 1, 2, 64, 64, 8192, 4096, 64, _lib.SCALE_HEAD, P, P, 4, None)
+    assert rc == 3 and b"workspace" in lib.flw_last_error()
+    rc = lib.flw_amax_e4m3(P, _lib.BF16, 1, 2, 64, 64, 8192, 4096, 64, 7, P, P, 1 << 20, None)
+    assert rc == 1 and b"granularity" in lib.flw_last_error()

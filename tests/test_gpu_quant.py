@@ -530,3 +530,67 @@ def test_fused_row_quantisers_nan_rows(act):
     assert np.isnan(s1[3].item())
     want_c, _ = rowwise_fp8(h1[3:4].float().numpy())
     np.testing.assert_array_equal(c1[3:4].numpy(), want_c)
+
+
+# ------------------------------------------------------------------ amax pass / given amax
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("gran", ["tensor", "head", "bh"])
+def test_amax_pass_alone_matches_oracle(gran, dtype):
+    """flw_amax_e4m3: |x| max per scale group, bit-exact against the oracle's amax (the amax of
+    per_tensor_fp8, fp8_swa_attention.py:201), on a strided (B, T, H, D) view."""
+    from flower_amd.kernels import amax_e4m3
+    from oracle.quant import _amax, group_axes
+    x = (seeded((2, 300, 3, 64), 41) * torch.exp(seeded((1, 1, 3, 1), 42))).to(dtype)
+    xv = x.cuda().transpose(1, 2)                    # (B, H, T, D), non-contiguous
+    got = amax_e4m3(xv, gran)
+    ref = _amax(to_np(x.transpose(1, 2)), group_axes(4, gran)).reshape(-1)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(got).view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("gran", ["tensor", "head", "bh"])
+def test_quantise_with_given_amax_equals_the_two_pass_quantiser(gran):
+    """flw_quant_e4m3_amax(x, flw_amax_e4m3(x)) == flw_quant_e4m3(x), codes and scales bit for
+    bit, and both equal the oracle (near-tie inputs, where x / s rounding decides codes)."""
+    from flower_amd.kernels import _per_tensor_fp8, amax_e4m3, quantize_e4m3_with_amax
+    x = near_ties((2, 3, 200, 64), 43).cuda()
+    c1, s1 = _per_tensor_fp8(x, gran)
+    c2, s2 = quantize_e4m3_with_amax(x, amax_e4m3(x, gran), gran)
+    torch.cuda.synchronize()
+    assert torch.equal(c1.view(torch.uint8), c2.view(torch.uint8))
+    assert torch.equal(s1.view(torch.int32), s2.view(torch.int32))
+    codes, scale = per_tensor_fp8(to_np(x), gran)
+    assert np.array_equal(to_np(c2.view(torch.uint8)), codes)
+    assert np.array_equal(to_np(s2).view(np.uint32), np.asarray(scale, np.float32).reshape(-1).view(np.uint32))
+
+
+@pytest.mark.parametrize("gran", ["tensor", "head"])
+def test_sequence_shards_quantised_with_the_combined_amax_match_the_whole(gran):
+    """A sequence-sharded tensor (two T ranges, as two ranks would hold it): each shard's amax,
+    combined by MAX on the int32 view (what an all_reduce(MAX) over RCCL would do), then each
+    shard quantised with the combined amax, gives exactly the whole tensor's codes and scale.
+    A NaN in one shard reaches the combined amax and every shard's scale."""
+    from flower_amd.kernels import _per_tensor_fp8, amax_e4m3, quantize_e4m3_with_amax
+    x = (seeded((1, 4, 512, 64), 44) * torch.exp(seeded((1, 4, 1, 1), 45))).to(torch.bfloat16).cuda()
+    parts = [x[:, :, :192], x[:, :, 192:]]
+    amax = torch.maximum(*(amax_e4m3(p, gran).view(torch.int32) for p in parts)).view(torch.float32)
+    codes = [quantize_e4m3_with_amax(p, amax, gran) for p in parts]
+    whole_c, whole_s = _per_tensor_fp8(x, gran)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([c.view(torch.uint8) for c, _ in codes], dim=2), whole_c.view(torch.uint8))
+    for _, s in codes:
+        assert torch.equal(s.view(torch.int32), whole_s.view(torch.int32))
+    y = x.clone()
+    y[0, 1, 300, 5] = float("nan")
+    a = [amax_e4m3(p, gran) for p in (y[:, :, :192], y[:, :, 192:])]
+    comb = torch.maximum(*(t.view(torch.int32) for t in a)).view(torch.float32)
+    torch.cuda.synchronize()
+    assert torch.isnan(comb[0 if gran == "tensor" else 1])
+
+
+def test_given_amax_is_validated():
+    from flower_amd.kernels import quantize_e4m3_with_amax
+    x = seeded((1, 2, 64, 64), 46).cuda()
+    with pytest.raises(ValueError, match="float32 tensor of 2"):
+        quantize_e4m3_with_amax(x, torch.ones(3, device="cuda"), "head")
