@@ -86,7 +86,7 @@ DATA = {
 # (summaries under profiles/). FETCH_SIZE is scaled by 2.0: a plain 256 MiB device copy reads back
 # 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0).
 TRAFFIC = {
-    "c3": {"swa_fwd": 167_982_080, "quant": 504_024_064},
+    "c3": {"swa_fwd": 167_986_176, "quant": 504_024_064},
     "c4": {"swa_fwd": 167_974_912, "quant": 503_960_576},
     "c2": {"gemm": 117_834_752, "w8a16": 134_490_112},
     "swa_bf16_450m": {"bwd": 554_757_120, "fwd": 169_459_712},
@@ -126,6 +126,18 @@ def make_gemm_inputs(cfg, seed=0):
     x.view(-1)[pos] *= cfg["outlier_scale"]
     w = torch.randn(N, K, generator=g) * cfg["w_std"]
     return x.to(torch.bfloat16), w.to(torch.bfloat16)
+
+
+def host_threads() -> int:
+    """Host threads the CPU baseline runs on: the cores this process may use (its CPU affinity,
+    i.e. os.cpu_count() where no affinity limit applies), further capped by OMP_NUM_THREADS when
+    the launcher sets it (a shared GPU box grants each job a share of the host that way). The
+    number is reported with the baseline."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 def in_window_pairs(T, W):
@@ -341,7 +353,7 @@ def cpu_baseline(cfg, budget_s=20.0):
     from threadpoolctl import threadpool_limits
     from oracle.quant import dequant, per_tensor_fp8
     from oracle.swa import swa_banded
-    cores = min(16, os.cpu_count() or 1)
+    cores = host_threads()
     B, H, T, D, W = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["W"]
     q, k, v = (t.float().numpy() for t in make_inputs(cfg))
     gran = cfg["granularity"]
@@ -376,7 +388,7 @@ def cpu_baseline_gemm(x, w, budget_s=15.0, weight_only=False):
     from threadpoolctl import threadpool_limits
     from oracle.gemm import fp8_linear_a8w8, fp8_linear_w8a16
     from oracle.quant import rowwise_fp8
-    cores = min(16, os.cpu_count() or 1)
+    cores = host_threads()
     xf, wf = x.float().cpu().numpy(), w.float().cpu().numpy()
     w8, sw = rowwise_fp8(wf)
     rows, t_total = 0, 0.0
@@ -613,7 +625,7 @@ def cpu_baseline_swa_bf16(cfg, budget_s=20.0):
     the backward) on the host, (b, h) slice by slice until the time budget, scaled linearly."""
     from threadpoolctl import threadpool_limits
     from oracle.swa_grad import swa_backward, swa_forward_lse
-    cores = min(16, os.cpu_count() or 1)
+    cores = host_threads()
     B, H, T, D, W = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["W"]
     g = torch.Generator().manual_seed(0)
     q, k, v, do = (torch.randn(1, 1, T, D, generator=g).to(torch.bfloat16).double().numpy() for _ in range(4))
@@ -766,7 +778,7 @@ def cpu_baseline_linear_train(x, w, g, budget_s=15.0):
     from threadpoolctl import threadpool_limits
     from oracle.gemm import fp8_linear_a8w8, fp8_linear_backward
     from oracle.quant import rowwise_fp8
-    cores = min(16, os.cpu_count() or 1)
+    cores = host_threads()
     xf, wf, gf = (t.float().cpu().numpy() for t in (x, w, g))
     w8, sw = rowwise_fp8(wf)
     rows, t_total = 0, 0.0

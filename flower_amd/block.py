@@ -162,9 +162,13 @@ class Fp8DecoderBlock(nn.Module):
         att = self.attn
         c1, s1 = codes_of("rmsnorm", x2, d, self.ln1)
         amax = None
-        if att.granularity == "head" and d % 128 == 0:
+        if att.granularity == "head" and d % 128 == 0 and M * d < 2 ** 32 and 3 * d * d < 2 ** 32:
             # QKV projection with the per-head |q|, |k|, |v| maxima from its epilogue: the
-            # attention's quantiser then needs no amax pass.
+            # attention's quantiser then needs no amax pass. Nothing may transform q / k between
+            # the GEMM and the quantiser (no QK-norm or RoPE in this block), or these maxima
+            # would not be those of the quantised tensors. The epilogue exists only in the
+            # 256 x 256 GEMM (K % 128 == 0, operands < 2^32 bytes); other shapes take the
+            # quantiser's own amax pass.
             w8, ws = qkv_l.weight_codes()
             N, K = w8.shape
             y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)

@@ -961,6 +961,9 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
     }
     return check_launch("flw_fp8_scaled_mm");
   }
+  // The general kernel has no group-amax epilogue: refuse rather than leave amax_out unwritten.
+  FLW_REQUIRE(gmax == nullptr, FLW_E_UNSUPPORTED,
+              "the group amax needs K %% %d == 0 and M*K, N*K < 2^32 (the 256 x 256 kernel)", kFBK);
   p.tiles_n = (int)((N + kGBN - 1) / kGBN);
   const int64_t tiles = (int64_t)p.tiles_n * ((M + kGBM - 1) / kGBM);
   FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");

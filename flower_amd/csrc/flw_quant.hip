@@ -212,6 +212,14 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
   if (writes_scale(p.granularity, slice, i0)) t.scale_out[group_index(p.granularity, slice, i1)] = scale;
   const bool fast = MODE == 0 && __builtin_isfinite(amax);   // uniform over the workgroup
   const float rcp = 1.0f / scale;                            // IEEE: correctly rounded
+  // A given amax is the caller's claim about the data (a producer's epilogue maximum, or a
+  // maximum combined across shards). The fast path relies on |x| <= amax (then |x / s| <= 448
+  // and the clamp is inert), so with a given amax every vector is checked against it, and a
+  // vector holding a larger |x|, an inf or a NaN takes the exact path (IEEE division, clamp,
+  // software rounding): the reference's clamp(x / s, -448, 448) then the cast, whatever amax
+  // was given. A negative amax admits no value to the fast path.
+  const bool check_given = p.amax_given != nullptr;
+  const uint32_t given_bits = amax > 0.0f ? __float_as_uint(amax) : 0u;
 
   const int64_t r0 = bx * kRowsPerChunk;
   const int64_t r1 = min(p.d2, r0 + kRowsPerChunk);
@@ -241,7 +249,14 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
       if (v >= nvec_p) continue;
       if (MODE == 0) {
         uint32_t w[V::N / 4];
-        codes_of<V::N>(f[u], scale, rcp, fast, w);
+        bool fast_v = fast;
+        if (check_given) {
+          uint32_t m = 0;
+#pragma unroll
+          for (int i = 0; i < V::N; ++i) { const uint32_t a = abs_bits(f[u][i]); m = m > a ? m : a; }
+          fast_v = fast_v && m <= given_bits;
+        }
+        codes_of<V::N>(f[u], scale, rcp, fast_v, w);
         if (!vtile) {
           uint8_t* dst = t.out8 + (slice * p.d2 + r0) * p.d3 + v * V::N;
           if (V::N == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
@@ -988,3 +1003,4 @@ extern "C" int flw_diag_quotient(const float* x, int64_t n, const float* scales,
                      static_cast<hipStream_t>(stream), x, n, scales, n_scales, out, mode);
   return check_launch("flw_diag_quotient");
 }
+

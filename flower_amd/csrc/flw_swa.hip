@@ -13,7 +13,7 @@
 // The softmax is VALU-bound (per score: one FMA, one v_exp_f32 at half rate, half a max3, half a
 // convert, one add; per tile D/64 rescale multiplies per score) while the MFMA work per tile is
 // about a third of that. The MFMA work of one wave runs under the VALU work of the other waves
-// of its SIMD (up to four workgroups per CU at D <= 64: 115 VGPRs, 24 KB of LDS each); issuing
+// of its SIMD (four workgroups per CU at D <= 64: 118 VGPRs, 24 KB of LDS each); issuing
 // the next tile's QK^T before the current softmax was measured slower (its extra accumulators
 // cost a wave per SIMD).
 //
@@ -107,7 +107,8 @@ struct Scores {
   v16f s0, s1;
 };
 
-// Three workgroups (12 waves) per CU for D <= 64, two for D = 128 (its O^T needs 64 VGPRs).
+// At D <= 64 the kernel takes 118 VGPRs, so four workgroups (16 waves) share a CU; the launch bound
+// only asks for three. D = 128 asks for two (its O^T needs 64 VGPRs more).
 template <int D, typename OutT>
 __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParams p) {
   constexpr int NDC = D >= 64 ? D / 64 : 1;   // 64-deep K chunks of the QK^T product

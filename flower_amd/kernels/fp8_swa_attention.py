@@ -147,9 +147,11 @@ def fp8_swa_attention_forward(
     extension; the reference has no such argument): a (B, H, T, D) tensor of q's dtype, any
     strides with D contiguous -- e.g. the (B, T, H, D) head view of a (B, T, H*D) buffer -- that
     the kernel writes in place and that is returned. ``amax`` (an extension): the |x| maxima of q,
-    k, v per scale group, as int32 fp32 bit patterns [3 * groups] on the GPU (from the producer,
-    e.g. ``flw_fp8_scaled_mm_group_amax`` on the QKV projection): the quantiser then skips its
-    amax pass; the result is the same as without it.
+    k, v per scale group [3 * groups] on the GPU, float32 (as ``amax_e4m3`` returns them) or
+    their int32 bit patterns (as ``flw_fp8_scaled_mm_group_amax`` writes them for the QKV
+    projection): the quantiser then skips its amax pass, and the result is the same as without
+    it. A given amax below the data's own maximum still gives the reference's clamp-then-cast
+    codes for that amax (values beyond it saturate at 448).
     ``window``: each query attends to the ``window`` keys at or behind it (window <= 0 gives
     an all-zero output, as the reference's masking does).
 
@@ -199,9 +201,12 @@ def fp8_swa_attention_forward(
             _lib.stream_of(q))
     else:
         groups = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+        if amax.dtype == torch.float32:
+            amax = amax.view(torch.int32)
         if (amax.dtype != torch.int32 or amax.numel() != 3 * groups or amax.device != q.device
                 or not amax.is_contiguous()):
-            raise ValueError(f"amax must be a contiguous int32 tensor of {3 * groups} bit patterns on q's device")
+            raise ValueError(f"amax must be a contiguous float32 tensor (or its int32 bit patterns) of "
+                             f"{3 * groups} elements on q's device")
         rc = lib.flw_fp8_swa_attention_forward_amax(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, strides, B, H, T, D, int(window),
             _lib.GRANULARITY[granularity], amax.data_ptr(), out.data_ptr(), None, ws.data_ptr(), ws.numel(),

@@ -1,14 +1,18 @@
 """bf16 causal sliding-window attention, forward + backward, on the HIP library (gfx950).
 
 Mirrors flower/kernels/swa_attention.py: ``swa_attention(q, k, v, window, *, fwd_cfg, dkdv_cfg,
-dq_cfg)`` (:243-261) is differentiable; the forward saves L = m + log(l) per query (:77-160) and
-the backward computes Delta = rowsum(dO * O), then dK / dV (one program per key block walking the
-query blocks that see it) and dQ (one per query block walking its keys), :162-320. The Triton
-launch-geometry tuples are accepted and ignored (the HIP kernels use their own tiling).
+dq_cfg)`` (:362-380) is differentiable (``_SlidingWindowAttention``, :307-359); the forward saves
+L = m + log(l) per query (``_swa_fwd``, :84-160) and the backward computes Delta = rowsum(dO * O)
+(``_swa_bwd_preprocess``, :163-182), then dK / dV (one program per key block walking the query
+blocks that see it, ``_swa_bwd_dkdv``, :184-242) and dQ (one per query block walking its keys,
+``_swa_bwd_dq``, :244-305). The Triton launch-geometry tuples are accepted and ignored (the HIP
+kernels use their own tiling).
 
-Errors as in the reference: ValueError for a non-(B, H, T, D) input, a head_dim outside
-{32, 64, 128} or a window <= 0 (:255-260). This build computes in bf16 only: other dtypes raise
-TypeError. No CPU fallback.
+Errors as in the reference (:373-379): ValueError for a non-(B, H, T, D) input, a head_dim outside
+{32, 64, 128} or a window <= 0. The products run on bf16 MFMA: bf16 inputs are used as they are;
+fp32 inputs (which the reference's Triton dots take at TF32 on its hardware) are rounded to bf16
+on entry, and the output and the gradients come back in fp32. Other dtypes raise TypeError. No
+CPU fallback.
 """
 
 from __future__ import annotations
@@ -56,7 +60,7 @@ class _SlidingWindowAttention(torch.autograd.Function):
 
 def swa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, *,
                   fwd_cfg=_FWD_CFG, dkdv_cfg=_DKDV_CFG, dq_cfg=_DQ_CFG) -> torch.Tensor:
-    """Causal sliding-window attention. q/k/v: (B, H, T, D) bf16 on the GPU. Differentiable."""
+    """Causal sliding-window attention. q/k/v: (B, H, T, D) bf16 or fp32 on the GPU. Differentiable."""
     del fwd_cfg, dkdv_cfg, dq_cfg
     try:
         _lib.load()
@@ -70,9 +74,16 @@ def swa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int
         raise ValueError("window must be positive; use flex for full-context attention")
     if k.shape != q.shape or v.shape != q.shape:
         raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
-    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
-        raise TypeError("swa_attention computes in bf16; got " + str(q.dtype))
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("swa_attention takes bfloat16 or float32 inputs; got " + str(q.dtype))
     _lib.require_gpu(q, k, v)
+    if q.dtype == torch.float32:
+        # bf16 MFMA products; the casts are differentiable, so the gradients return in fp32
+        out = _SlidingWindowAttention.apply(q.to(torch.bfloat16), k.to(torch.bfloat16),
+                                            v.to(torch.bfloat16), window)
+        return out.to(torch.float32)
     return _SlidingWindowAttention.apply(q, k, v, window)
 
 

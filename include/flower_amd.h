@@ -76,7 +76,9 @@ int flw_amax_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int
 
 /* flw_quant_e4m3 with the amax given (amax: the groups' |x| max bit patterns, e.g. from
  * flw_amax_e4m3, combined across shards): the quantise pass only, no workspace. Same scale and
- * code arithmetic, so flw_quant_e4m3_amax(x, flw_amax_e4m3(x)) == flw_quant_e4m3(x) bit for bit. */
+ * code arithmetic, so flw_quant_e4m3_amax(x, flw_amax_e4m3(x)) == flw_quant_e4m3(x) bit for bit.
+ * An amax below the data's own |x| max still gives the reference's clamp(x / s, -448, 448)-then-
+ * cast codes for that amax: values past it saturate at +-448 (inf too), NaN stays NaN. */
 int flw_quant_e4m3_amax(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
                         int64_t stride_b, int64_t stride_h, int64_t stride_t, int granularity,
                         int layout, const uint32_t* amax, uint8_t* out, float* scale_out,
@@ -246,7 +248,9 @@ int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8
  * quantisation into the producer" step of the path: `qkv_heads` (flower/models/base.py:618-639)
  * feeds `_per_tensor_fp8` (flower/kernels/fp8_swa_attention.py:195-205), whose amax this
  * replaces. group_cols: a power of two in [8, 256] dividing N; K % 128 == 0, N % 8 == 0,
- * 16-byte aligned y rows. amax_out is overwritten (cleared by the call itself). */
+ * 16-byte aligned y rows, M * K and N * K < 2^32 (other shapes return FLW_E_UNSUPPORTED; the
+ * caller then takes the quantiser's own amax pass). amax_out is overwritten (cleared by the call
+ * itself). */
 int flw_fp8_scaled_mm_group_amax(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
                                  const float* x_scale, int64_t x_scale_count, const float* w_scale,
                                  int64_t w_scale_count, void* y, int64_t y_row_stride, int64_t group_cols,

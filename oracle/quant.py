@@ -74,14 +74,22 @@ def scale_a2(amax: np.ndarray) -> np.ndarray:
     return (amax / QMAX).astype(F32)
 
 
-def per_tensor_fp8(x: np.ndarray, granularity: str = "tensor"):
+def per_tensor_fp8(x: np.ndarray, granularity: str = "tensor", amax: np.ndarray | None = None):
     """``_per_tensor_fp8`` (and its per-head / per-(b,h) extension).
 
     x: float32 array holding fp32 or bf16 values. Returns (codes uint8 same shape,
-    scale float32 with keepdims shape of the group).
+    scale float32 with keepdims shape of the group). ``amax`` (optional, one value per scale
+    group, e.g. a producer's maximum or one combined across shards) replaces the amax of x in
+    the scale; the clamp then bounds every quotient it leaves above 448.
     """
     xf = x.astype(F32)
-    scale = scale_a2(_amax(xf, group_axes(xf.ndim, granularity)))
+    axes = group_axes(xf.ndim, granularity)
+    if amax is None:
+        amax = _amax(xf, axes)
+    else:
+        shape = [1 if i in axes else n for i, n in enumerate(xf.shape)]
+        amax = np.asarray(amax, F32).reshape(shape)
+    scale = scale_a2(amax)
     y = (xf / scale).astype(F32)
     y = np.where(y > QMAX, QMAX, np.where(y < -QMAX, -QMAX, y))   # clamp, NaN propagates
     return f32_to_e4m3(y), scale

@@ -181,7 +181,7 @@ def test_reference_swa_attention_api_matches_oracle():
 def test_attention_with_producer_amax_is_identical():
     """fp8_swa_attention_forward(amax=...) with the per-head |q|, |k|, |v| maxima supplied (as the
     QKV GEMM epilogue supplies them) skips the amax pass and returns the same output bit for bit."""
-    from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
+    from flower_amd.kernels.fp8_swa_attention import amax_e4m3, fp8_swa_attention_forward
     g = torch.Generator().manual_seed(21)
     B, H, T, D, W = 2, 4, 300, 64, 96
     q, k, v = (torch.randn(B, H, T, D, generator=g).mul(torch.rand(1, H, 1, 1, generator=g) * 4)
@@ -189,7 +189,11 @@ def test_attention_with_producer_amax_is_identical():
     plain = fp8_swa_attention_forward(q, k, v, W, granularity="head")
     amax = torch.cat([t.float().abs().amax(dim=(0, 2, 3)) for t in (q, k, v)]).view(torch.int32).contiguous()
     given = fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax)
+    # the same maxima as float32 (the dtype amax_e4m3 returns) are accepted too
+    amax_f = torch.cat([amax_e4m3(t, "head") for t in (q, k, v)])
+    given_f = fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax_f)
     torch.cuda.synchronize()
     assert torch.equal(plain, given)
+    assert torch.equal(plain, given_f)
     with pytest.raises(ValueError, match="amax"):
         fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax[:5])

@@ -594,3 +594,28 @@ def test_given_amax_is_validated():
     x = seeded((1, 2, 64, 64), 46).cuda()
     with pytest.raises(ValueError, match="float32 tensor of 2"):
         quantize_e4m3_with_amax(x, torch.ones(3, device="cuda"), "head")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("factor", [0.5, 1.0, -1.0])
+@pytest.mark.parametrize("gran", ["tensor", "head", "bh"])
+def test_given_amax_below_the_data_max_clamps_like_the_reference(gran, factor, dtype):
+    """A given amax smaller than the data's |x| max (a stale or wrong producer maximum): every
+    quotient above 448 is clamped exactly as clamp(x / s, -448, 448) then the cast, with inf, NaN
+    and a 1e30 among the inputs, bit-exact against the oracle with the same amax swapped in."""
+    from flower_amd.kernels import quantize_e4m3_with_amax
+    from oracle.quant import _amax, group_axes
+    x = near_ties((2, 3, 200, 64), 47)
+    axes = group_axes(4, gran)
+    given = (_amax(x.numpy(), axes).reshape(-1) * np.float32(factor)).astype(np.float32)
+    x[0, 1, 3, :4] = torch.tensor([float("inf"), float("-inf"), float("nan"), -float("nan")])
+    x[1, 2, 5, 8] = 1e30
+    x = x.to(dtype)
+    xd = x.cuda()
+    codes, scale = quantize_e4m3_with_amax(xd, torch.from_numpy(given).cuda(), gran)
+    want_c, want_s = per_tensor_fp8(to_np(x), gran, amax=given)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(codes.view(torch.uint8)), want_c)
+    assert np.array_equal(to_np(scale).view(np.uint32), np.asarray(want_s, np.float32).reshape(-1).view(np.uint32))
+    if factor == 0.5:
+        assert int(((codes.view(torch.uint8) & 0x7F) == 0x7E).sum()) > 1000

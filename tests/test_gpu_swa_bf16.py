@@ -87,7 +87,30 @@ def test_rejections():
     with pytest.raises(ValueError, match="head_dim"):
         swa_attention(*(torch.randn(1, 2, 128, 96, device="cuda", dtype=torch.bfloat16) for _ in range(3)), 16)
     with pytest.raises(TypeError):
-        swa_attention(q.float(), k.float(), v.float(), 16)
+        swa_attention(q.half(), k.half(), v.half(), 16)
+
+
+def test_fp32_inputs_are_accepted_and_differentiable():
+    """fp32 inputs, as the reference's swa_attention accepts them (swa_attention.py:362-380): the
+    products run on the bf16 values, so the output equals the bf16 call on the rounded inputs
+    (in fp32), and the fp32 gradients equal the bf16 call's gradients widened."""
+    from flower_amd.kernels.swa_attention import swa_attention
+    base = [t.float() for t in inputs(1, 2, 256, 64, seed=5)]
+    g = torch.randn(1, 2, 256, 64, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    q, k, v = (t.cuda().requires_grad_(True) for t in base)
+    out = swa_attention(q, k, v, 100)
+    assert out.dtype == torch.float32
+    out.backward(g.float().cuda())
+    qb, kb, vb = (t.cuda().to(torch.bfloat16).requires_grad_(True) for t in base)
+    ob = swa_attention(qb, kb, vb, 100)
+    ob.backward(g.cuda())
+    assert torch.equal(out.detach(), ob.detach().float())
+    for a, b in ((q, qb), (k, kb), (v, vb)):
+        assert a.grad.dtype == torch.float32
+        assert torch.equal(a.grad, b.grad.float())
+    ref, _ = oracle_fwd(*(t.to(torch.bfloat16) for t in base), 100)
+    mean_rel, max_rel = rel(out.detach().cpu(), ref)
+    assert mean_rel < 0.01 and max_rel < 2e-2
 
 
 def test_450m_shape_against_oracle_and_identities():

@@ -89,6 +89,28 @@ def test_per_tensor_fp8_matches_reference_formula(name, make, granularity):
                                   np.asarray(want_scale, np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("factor", [0.5, 1.0, 3.0, -1.0])
+@pytest.mark.parametrize("granularity", ["tensor", "head", "bh"])
+def test_per_tensor_fp8_with_a_given_amax_matches_clamp_then_cast(factor, granularity):
+    """A given amax (a producer's or a cross-shard maximum, possibly below the data's own |x|
+    max) replaces amax in the scale; the reference's clamp(x / s, -448, 448) then bounds the
+    quotients, and inf / NaN inputs go through the cast as torch casts them. Checked against
+    fp8_swa_attention.py:203-205's expressions in torch with the amax swapped in."""
+    x = near_tie_input((2, 4, 64, 32), 7)
+    dims = (0, 1, 2, 3) if granularity == "tensor" else group_axes(4, granularity)
+    given = (np.max(np.abs(x), axis=dims, keepdims=True) * np.float32(factor)).astype(np.float32)
+    x[0, 1, 3, :4] = [np.inf, -np.inf, np.nan, -np.nan]
+    x[1, 2, 5, 7] = 1e30
+    xt = torch.from_numpy(x)
+    scale = torch.from_numpy(given).float().clamp(min=1e-12) / 448.0
+    want = (xt.float() / scale).clamp(-448.0, 448.0).to(E4M3).view(torch.uint8).numpy()
+    codes, sc = per_tensor_fp8(x, granularity, amax=given.reshape(-1))
+    np.testing.assert_array_equal(codes, want)
+    np.testing.assert_array_equal(sc.reshape(-1).view(np.uint32), scale.numpy().reshape(-1).view(np.uint32))
+    if factor == 0.5:
+        assert (codes & 0x7F == 0x7E).sum() > 100        # the clamp is exercised
+
+
 @pytest.mark.parametrize("name,make", CASES)
 @pytest.mark.parametrize("granularity", ["tensor", "head"])
 def test_fake_quant_fp32_matches_reference_formula(name, make, granularity):
