@@ -113,13 +113,19 @@ class Fp8DecoderBlock(nn.Module):
                 and isinstance(gelu, nn.GELU) and gelu.approximate == "none"
                 and self.ln1.weight.dtype == self.ln2.weight.dtype == torch.bfloat16)
 
-    def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
+    def _forward_fused(self, x: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
         """The same block with the work around the FP8 GEMMs fused into the library's kernels:
         RMSNorm -> per-row e4m3 in one pass (flw_rmsnorm_quant_rows_e4m3), the attention writing
         its (B, T, H, D) output in place, the residual adds in the GEMM epilogues
         (flw_fp8_scaled_mm_residual), GELU -> per-row e4m3 in one pass (flw_gelu_quant_rows_e4m3).
         Every rounding step of the unfused composition is kept (bf16 norm / GELU outputs, bf16
-        linear outputs before each residual add)."""
+        linear outputs before each residual add).
+
+        ``trace`` (a dict, for stage-by-stage checks): receives every intermediate of the call --
+        the row codes / scales of each linear's input ("c1"/"s1", "ca"/"sa", "c2"/"s2",
+        "cg"/"sg"), the normed / activated rows the fused quantisers also write out when tracing
+        ("h1", "h2", "hg"), the QKV output "qkv" with its epilogue maxima "amax", the attention
+        output "attn", "x1" and the FF1 output "f". The kernels and the result are the same."""
         lib = _lib.load()
         B, T, d = x.shape
         M = B * T
@@ -130,15 +136,19 @@ class Fp8DecoderBlock(nn.Module):
             x2 = x2.contiguous()
         qkv_l, out_l, ff1_l, ff2_l = self._linears()
 
-        def codes_of(kind, src, cols, norm=None):
+        def codes_of(kind, src, cols, norm=None, h_name=None):
             c = torch.empty((M, cols), dtype=torch.uint8, device=dev)
             sc = torch.empty(M, dtype=torch.float32, device=dev)
+            h = None
+            if trace is not None and h_name is not None:
+                h = trace[h_name] = torch.empty((M, cols), dtype=torch.bfloat16, device=dev)
+            hp = None if h is None else h.data_ptr()
             if kind == "rmsnorm":
                 rc = lib.flw_rmsnorm_quant_rows_e4m3(src.data_ptr(), M, cols, cols, norm.weight.data_ptr(),
-                                                     float(norm.eps), c.data_ptr(), sc.data_ptr(), None, stream)
+                                                     float(norm.eps), c.data_ptr(), sc.data_ptr(), hp, stream)
             elif kind == "gelu":
                 rc = lib.flw_gelu_quant_rows_e4m3(src.data_ptr(), M, cols, cols, c.data_ptr(), sc.data_ptr(),
-                                                  None, stream)
+                                                  hp, stream)
             else:
                 rc = lib.flw_quant_rows_e4m3(src.data_ptr(), _lib.BF16, M, cols, cols, c.data_ptr(),
                                              sc.data_ptr(), stream)
@@ -160,7 +170,7 @@ class Fp8DecoderBlock(nn.Module):
             return y
 
         att = self.attn
-        c1, s1 = codes_of("rmsnorm", x2, d, self.ln1)
+        c1, s1 = codes_of("rmsnorm", x2, d, self.ln1, "h1")
         amax = None
         if att.granularity == "head" and d % 128 == 0 and M * d < 2 ** 32 and 3 * d * d < 2 ** 32:
             # QKV projection with the per-head |q|, |k|, |v| maxima from its epilogue: the
@@ -186,9 +196,12 @@ class Fp8DecoderBlock(nn.Module):
                                   out=a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2), amax=amax)
         ca, sa = codes_of("plain", a.view(M, d), d)
         x1 = linear(ca, sa, out_l, residual=x2)
-        c2, s2 = codes_of("rmsnorm", x1, d, self.ln2)
+        c2, s2 = codes_of("rmsnorm", x1, d, self.ln2, "h2")
         f = linear(c2, s2, ff1_l)
-        cg, sg = codes_of("gelu", f, f.shape[1])
+        cg, sg = codes_of("gelu", f, f.shape[1], h_name="hg")
+        if trace is not None:
+            trace.update(c1=c1, s1=s1, qkv=qkv, amax=amax, attn=a, ca=ca, sa=sa, x1=x1, c2=c2, s2=s2, f=f,
+                         cg=cg, sg=sg)
         return linear(cg, sg, ff2_l, residual=x1).view(B, T, d)
 
 

@@ -10,6 +10,7 @@ Gates (written here; FP8 e4m3 is far coarser than the fp32 reference):
   - inside fp8_weight_cache the block output is bit-identical to the uncached one.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -111,3 +112,109 @@ def test_fused_forward_matches_the_unfused_composition():
     rel = float((d_f - d_p).norm() / d_p.norm())
     print(f"fused vs unfused delta rel: {rel:.2e}")
     assert rel < 1e-2
+
+
+def _ulp_bf16(a, b):
+    from oracle.e4m3 import f32_to_bf16_bits
+    ia = f32_to_bf16_bits(np.asarray(a, np.float32)).astype(np.int32)
+    ib = f32_to_bf16_bits(np.asarray(b, np.float32)).astype(np.int32)
+    return np.abs(ia - ib)
+
+
+def _gemm_close(got, ref, what):
+    tol = 2.0 ** -7 * np.abs(ref) + 1e-3 * np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), (what, int(bad.sum()), float(np.abs(got - ref).max()))
+
+
+def test_config5_full_shape_stage_by_stage():
+    """BASELINE config 5 at its full shape: B1 T32768 d1024 H16 (D64) ffn4096 W4096, every linear
+    from the FP8 weight cache (base.py:698-722 block, base.py:514-525 GELU MLP), fused forward.
+    Each stage is checked on the kernels' own inputs:
+      (i)   attention, two heads, against the oracle's FP8 simulator on the oracle's per-head codes
+            of the block's own q / k / v (the QKV output);
+      (ii)  256 sampled rows of every linear (QKV, O + residual, FF1, FF2 + residual) against the
+            float64 closed form on the kernel's codes and scales (rounded to bf16, then the
+            residual added in bf16);
+      (iii) the RMSNorm, attention-output and GELU row quantisers: codes and scales bit-exact
+            against the per-row recipe on their own h, and h within 1 bf16 ulp of the oracle's
+            RMSNorm / GELU on the sampled rows;
+      (iv)  the QKV epilogue's per-head maxima equal to max |q|, |k|, |v| of its own output.
+    The traced call returns the same bits as the untraced one."""
+    from flower_amd.block import Fp8DecoderBlock, init_block_
+    from flower_amd.precision import fp8_weight_cache
+    from oracle.block import gelu, rmsnorm
+    from oracle.e4m3 import round_bf16
+    from oracle.gemm import scaled_mm
+    from oracle.quant import rowwise_fp8
+
+    B, T, d, H, ffn, W = 1, 32768, 1024, 16, 4096, 4096
+    D, M = d // H, B * T
+    blk = Fp8DecoderBlock(d, H, ffn, W)
+    init_block_(blk, std=0.02, seed=55)
+    blk = blk.to("cuda", torch.bfloat16)
+    x = torch.randn(B, T, d, generator=torch.Generator().manual_seed(56)).to("cuda", torch.bfloat16)
+    print("[c5] fused forward at B1 T32768 d1024 H16 ffn4096 W4096", flush=True)
+    with fp8_weight_cache(blk):
+        tr = {}
+        out = blk._forward_fused(x, trace=tr)
+        plain = blk(x)
+        wq = [lin.weight_codes() for lin in blk._linears()]
+        torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    assert tr["amax"] is not None                       # the producer-amax route is the one tested
+
+    rows = np.sort(np.random.default_rng(57).choice(M, 256, replace=False))
+    ridx = torch.from_numpy(rows).cuda()
+    cpu = lambda t: to_np(t.index_select(0, ridx))     # noqa: E731  sampled rows on the host
+    x2 = x.view(M, d)
+    w8 = [(to_np(w.view(torch.uint8)), to_np(s)) for w, s in wq]
+
+    # (iv) per-head maxima of the QKV output, bit for bit (bf16 values as fp32 patterns)
+    qkv = tr["qkv"].view(M, 3 * d)
+    want_amax = qkv.view(M, 3 * H, D).float().abs().amax(dim=(0, 2))
+    assert torch.equal(tr["amax"], want_amax.view(torch.int32))
+
+    # (iii) row quantisers: codes / scales on their own h; h against the oracle on sampled rows
+    for c, s, h in (("c1", "s1", "h1"), ("c2", "s2", "h2"), ("cg", "sg", "hg")):
+        want_c, want_s = rowwise_fp8(cpu(tr[h]))
+        np.testing.assert_array_equal(cpu(tr[c]), want_c, err_msg=c)
+        np.testing.assert_array_equal(to_np(tr[s])[rows], want_s.reshape(-1), err_msg=s)
+    want_c, want_s = rowwise_fp8(cpu(tr["attn"].view(M, d)))
+    np.testing.assert_array_equal(cpu(tr["ca"]), want_c)
+    np.testing.assert_array_equal(to_np(tr["sa"])[rows], want_s.reshape(-1))
+    for h, want in (("h1", rmsnorm(cpu(x2), to_np(blk.ln1.weight), blk.ln1.eps)),
+                    ("h2", rmsnorm(cpu(tr["x1"]), to_np(blk.ln2.weight), blk.ln2.eps))):
+        dd = _ulp_bf16(cpu(tr[h]), want)
+        assert dd.max() <= 1 and (dd > 0).mean() < 1e-3, (h, dd.max(), (dd > 0).mean())
+    got, want = cpu(tr["hg"]), gelu(cpu(tr["f"]))
+    big = np.abs(want) > 1e-4
+    dd = _ulp_bf16(got[big], want[big])
+    assert dd.max() <= 1 and (dd > 0).mean() < 0.02, ("hg", dd.max(), (dd > 0).mean())
+    assert np.abs(got[~big] - want[~big]).max() < 2e-6
+
+    # (ii) the four linears on their own codes
+    def closed(cname, sname, wi):
+        return round_bf16(scaled_mm(cpu(tr[cname]), w8[wi][0], to_np(tr[sname])[rows], w8[wi][1]))
+    _gemm_close(cpu(qkv), closed("c1", "s1", 0), "qkv")
+    _gemm_close(cpu(tr["f"]), closed("c2", "s2", 2), "ff1")
+    for yname, res, cn, sn, wi in (("x1", x2, "ca", "sa", 1), ("out", tr["x1"], "cg", "sg", 3)):
+        y = cpu(out.view(M, d)) if yname == "out" else cpu(tr[yname])
+        prod = closed(cn, sn, wi)
+        ref = round_bf16(prod + cpu(res))
+        tol = (2.0 ** -7 * (np.abs(prod) + np.abs(ref))
+               + 1e-3 * np.sqrt(np.mean(prod.astype(np.float64) ** 2)))
+        assert (np.abs(y - ref) <= tol).all(), (yname, float(np.abs(y - ref).max()))
+
+    # (i) attention on the block's own q / k / v, two heads, per-head codes of the whole tensor
+    q, k, v = (blk.attn._split(t) for t in tr["qkv"].chunk(3, dim=-1))
+    quant = [per_tensor_fp8(to_np(t.contiguous()), "head") for t in (q, k, v)]
+    attn = to_np(tr["attn"].view(B, T, H, D).transpose(1, 2))
+    for h in (2, 11):
+        sl = slice(h, h + 1)
+        ref = fp8_swa_simulate(quant[0][0][:, sl], quant[1][0][:, sl], quant[2][0][:, sl], quant[0][1][:, sl],
+                               quant[1][1][:, sl], quant[2][1][:, sl], W, chunk=1024)
+        mx, mean = rel_errors(attn[:, sl], ref)
+        print(f"[c5] attention head {h}: max-rel {mx:.2e} mean-rel {mean:.2e}", flush=True)
+        assert mx <= 2e-2 and mean <= 5e-3, (h, mx, mean)
+    assert torch.isfinite(out).all()
