@@ -40,6 +40,10 @@ SIGNATURES = {
     "flw_quant_qkv_e4m3": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                    c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_size_t, c_void_p]),
+    "flw_noalloc_scratch_bytes": (c_size_t, []),
+    "flw_quant_qkv_e4m3_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
+                                           c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                           c_void_p]),
     "flw_fake_quant_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64,
                                     c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_size_t,
                                     c_void_p]),

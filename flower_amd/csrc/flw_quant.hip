@@ -19,6 +19,8 @@
 // exact software rounding (flw_diag_* entry points and their tests). A group whose amax is NaN or
 // infinite takes the exact path (IEEE division, clamp, software rounding) so that NaN and inf
 // propagate exactly as in the reference.
+#include <mutex>
+
 #include "flw_common.h"
 
 namespace flw {
@@ -1004,3 +1006,74 @@ extern "C" int flw_diag_quotient(const float* x, int64_t n, const float* scales,
   return check_launch("flw_diag_quotient");
 }
 
+// ---------------------------------------------------------------- allocation-free QKV quantiser
+//
+// flw_quant_qkv_e4m3 without a workspace argument, for callers that cannot allocate (code under
+// graph capture, tight serving loops): the amax partials live in a file-scope device array, one
+// copy per GPU, held until the process ends. Its device address is looked up once per device
+// (hipGetSymbolAddress with that device current) and only that address is handed to the kernels
+// -- the array's name in host code is a host-side stand-in, not a device address. Every entry of
+// the partials is written by the amax pass before the quantise pass reads it, so the array needs
+// no clearing between calls; two calls that overlap on one GPU (different streams) share the
+// array and race.
+namespace flw {
+
+constexpr size_t kNoAllocScratchBytes = 1u << 20;   // 262,144 amax partials
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) uint32_t scratch[kNoAllocScratchBytes / sizeof(uint32_t)];
+
+static int scratch_of_stream(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (stream != nullptr) {
+    FLW_REQUIRE(hipStreamGetDevice(stream, &dev) == hipSuccess, FLW_E_LAUNCH, "hipStreamGetDevice failed");
+  } else {
+    FLW_REQUIRE(hipGetDevice(&dev) == hipSuccess, FLW_E_LAUNCH, "hipGetDevice failed");
+  }
+  FLW_REQUIRE(dev >= 0 && dev < kMaxDevices, FLW_E_UNSUPPORTED, "device %d out of range", dev);
+  static void* ptrs[kMaxDevices] = {};
+  static std::mutex mu;
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    int cur = -1;
+    FLW_REQUIRE(hipGetDevice(&cur) == hipSuccess, FLW_E_LAUNCH, "hipGetDevice failed");
+    if (cur != dev) FLW_REQUIRE(hipSetDevice(dev) == hipSuccess, FLW_E_LAUNCH, "hipSetDevice(%d) failed", dev);
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    FLW_REQUIRE(e == hipSuccess && p != nullptr, FLW_E_LAUNCH, "hipGetSymbolAddress(scratch): %s",
+                hipGetErrorString(e));
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return FLW_OK;
+}
+
+}  // namespace flw
+
+extern "C" size_t flw_noalloc_scratch_bytes(void) { return flw::kNoAllocScratchBytes; }
+
+extern "C" int flw_quant_qkv_e4m3_noalloc(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                                          int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                                          int granularity, uint8_t* q8, uint8_t* k8, uint8_t* v_tiles,
+                                          float* scales_out, void* stream) {
+  FLW_REQUIRE(strides != nullptr && scales_out != nullptr, FLW_E_INVALID, "null strides / scales");
+  FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty or negative shape");
+  FLW_REQUIRE(B * H <= 65535 && T < ((int64_t)1 << 40), FLW_E_UNSUPPORTED, "B*H must be <= 65535");
+  const size_t need = 3 * partial_bytes(B, H, T);
+  FLW_REQUIRE(need <= kNoAllocScratchBytes, FLW_E_UNSUPPORTED,
+              "allocation-free quantiser: 3 * B * H * ceil(T / 256) amax partials must fit its %zu-byte "
+              "scratch (this shape needs %zu bytes); use flw_quant_qkv_e4m3 with a workspace",
+              kNoAllocScratchBytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = scratch_of_stream(s, &ws);
+  if (rc) return rc;
+  const int64_t G = granularity == FLW_SCALE_TENSOR ? 1 : (granularity == FLW_SCALE_HEAD ? H : B * H);
+  const void* xs[3] = {q, k, v};
+  const int layouts[3] = {FLW_LAYOUT_BHTD, FLW_LAYOUT_BHTD, FLW_LAYOUT_VTILE};
+  uint8_t* outs[3] = {q8, k8, v_tiles};
+  float* sc[3] = {scales_out, scales_out + G, scales_out + 2 * G};
+  return quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, sc, ws,
+                      kNoAllocScratchBytes, s, take_timer());
+}

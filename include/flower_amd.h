@@ -106,6 +106,19 @@ int flw_quant_qkv_e4m3(const void* q, const void* k, const void* v, int dtype, i
                        uint8_t* q8, uint8_t* k8, uint8_t* v_tiles, float* scales_out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* flw_quant_qkv_e4m3 without a workspace: no counterpart in the reference. For callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the amax partials live in a library-owned device array of
+ * flw_noalloc_scratch_bytes() bytes (1 MiB) per GPU, held until the process ends; the call itself
+ * allocates nothing. Limit: 3 * B * H * ceil(T / 256) * 4 bytes of partials must fit the array
+ * (FLW_E_UNSUPPORTED otherwise). Outputs and their contract are those of flw_quant_qkv_e4m3. Calls
+ * that overlap on one GPU (e.g. on two streams) share the array and race; serialise them. */
+size_t flw_noalloc_scratch_bytes(void);
+int flw_quant_qkv_e4m3_noalloc(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                               int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                               int granularity, uint8_t* q8, uint8_t* k8, uint8_t* v_tiles,
+                               float* scales_out, void* stream);
+
 /* Straight-through fake quantisation forward value, replacing `_fake_quant_e4m3`
  * (flower/models/base.py:167-203): out = x + (e4m3(x / s) * s - x), every step rounded to the
  * input dtype exactly as the reference's op sequence rounds (s itself in the input dtype).
