@@ -25,6 +25,8 @@
 // K/V from its own L2.
 #include <math.h>
 
+#include <algorithm>
+
 #include <type_traits>
 
 #include "flw_common.h"
@@ -61,6 +63,8 @@ struct SwaParams {
   void* out;
   int64_t osb, osh, ost;      // element strides of out
   int H, T, W, nM, nwg;
+  int ramp;                   // query tiles per slice whose band starts at key 0 (fewer key tiles)
+  int group_slices;           // slices per dispatch group (one XCD's share when it is whole slices)
 };
 
 template <typename OutT> struct Store4;
@@ -128,7 +132,22 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   const int nwg = p.nwg;
   int L = (int)__builtin_amdgcn_workgroup_id_x();
   if ((nwg & 7) == 0) L = (L & 7) * (nwg >> 3) + (L >> 3);   // contiguous work per XCD
-  const int bh = L / p.nM, mt = L % p.nM;
+  // Inside a group of slices (one XCD's share), the full-band query tiles come first, slice by
+  // slice (consecutive tiles share K / V tiles in that XCD's L2), then the causal-ramp tiles in
+  // decreasing length, so the short work items fill the end of the grid as the long ones drain.
+  int bh, mt;
+  {
+    const int gs = p.group_slices, nfull_t = p.nM - p.ramp;
+    const int gi = L / (gs * p.nM), i = L % (gs * p.nM);
+    if (i < gs * nfull_t) {
+      bh = gi * gs + i / nfull_t;
+      mt = p.ramp + i % nfull_t;
+    } else {
+      const int j = i - gs * nfull_t;
+      bh = gi * gs + j % gs;
+      mt = p.ramp - 1 - j / gs;
+    }
+  }
   const int b = bh / p.H, h = bh % p.H;
   const int T = p.T, W = p.W;
   const int m0 = mt * kBM;
@@ -412,6 +431,8 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.out = out; p.osb = ost[0]; p.osh = ost[1]; p.ost = ost[2];
   p.H = (int)H; p.T = (int)T; p.W = (int)W; p.nM = (int)nM;
   p.nwg = (int)(B * H * nM);
+  p.ramp = W > 0 ? (int)std::min<int64_t>(nM, (W - 1) / kBM + 1) : 0;
+  p.group_slices = ((B * H) % 8 == 0 && (p.nwg & 7) == 0) ? (int)(B * H / 8) : (int)(B * H);
   dim3 grid((unsigned)p.nwg);
   if (D == 32) launch_d<32>(p, out_dtype, grid, stream, tm);
   else if (D == 64) launch_d<64>(p, out_dtype, grid, stream, tm);
