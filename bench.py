@@ -4,10 +4,11 @@
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
-lognormal(0, 1) factor (seeded), per-head e4m3 scales. One step = the whole operator: amax +
-e4m3 quantisation of Q, K and V (V into the MFMA tile layout, one launch pair for the three) and
-the fused FP8 attention kernel, on inputs already resident in HBM. Everything runs through the
-C ABI of libflower_amd.so on torch's current stream.
+lognormal(0, 1) factor (seeded), per-head e4m3 scales. One step = the whole operator as
+flw_fp8_swa_attention_forward runs it: one amax + e4m3 quantise launch pair for Q, K and V (V into
+the MFMA tile layout; Q's codes deferred: the pair writes Q's scale and reciprocal only) and the
+fused FP8 attention kernel, which reads Q in bf16 and quantises it on load, on inputs already
+resident in HBM. Everything runs through the C ABI of libflower_amd.so on torch's current stream.
 
 Before the W warm-up steps, the step runs untimed for SPIN_UP_S seconds (clock spin-up).
 
@@ -16,8 +17,9 @@ Printed (one JSON line):
   roofline   -- the attention kernel alone (a HIP event pair per launch, recorded from the
                 kernel's own dispatch on the stream it runs on, via flw_time_next_launch): achieved TFLOP/s against MI355X dense FP8 MFMA peak
                 (5.0 PFLOP/s); traffic = its measured HBM bytes per launch (TRAFFIC below)
-  quant      -- the quantise launch pair: algorithmic bytes (2 reads + 1 write per element) /
-                their time (event pair recorded by the pair's own dispatches), against 8 TB/s HBM
+  quant      -- the quantise launch pair: algorithmic bytes (Q, K, V read by the amax pass; K, V
+                read again and their codes written by the quantise pass) / their time (event pair
+                recorded by the pair's own dispatches), against 8 TB/s HBM
   cpu_baseline -- the CPU oracle of the FP8-simulated reference path (e4m3 quantise, dequantise,
                 banded fp32 softmax attention) on a bounded sample of the same workload, host
                 cores, scaled linearly to the same unit.
@@ -192,7 +194,10 @@ def _arm(lib, pair):
 
 
 class AttentionStep:
-    """The operator as C-ABI launches: one quantise pair for Q/K/V, then the attention kernel."""
+    """The operator as C-ABI launches, as flw_fp8_swa_attention_forward runs it: one quantise pass
+    pair over Q, K, V with Q's codes deferred (flw_quant_qkv_e4m3_deferq: the amax pass reads all
+    three, the quantise pass writes K / V codes and the scales), then the attention kernel, which
+    reads Q in bf16 and quantises it on load (flw_fp8_swa_fwd_qx)."""
 
     def __init__(self, q, k, v, cfg):
         from flower_amd import _lib
@@ -204,32 +209,35 @@ class AttentionStep:
         self.gran = _lib.GRANULARITY[cfg["granularity"]]
         G = {0: 1, 1: H, 2: B * H}[self.gran]
         dev = q.device
-        self.q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device=dev)
+        self.q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device=dev)   # non-finite groups only
         self.k8 = torch.empty_like(self.q8)
         self.vt = torch.empty(self.lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device=dev)
         self.sc = torch.empty(3 * G, dtype=torch.float32, device=dev)
+        self.qr = torch.empty(G, dtype=torch.float32, device=dev)
         self.G = G
         self.ws = _lib.workspace(3 * self.lib.flw_quant_workspace_bytes(B, H, T, D), dev)
         self.out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
         self.dt = _lib.dtype_code(q.dtype)
         self.s8 = _lib.i64s(H * T * D, T * D, D)
         self.so = _lib.i64s(*self.out.stride()[:3])
+        self.sq = _lib.i64s(*q.stride()[:3])
         self.sx = _lib.i64s(*q.stride()[:3], *k.stride()[:3], *v.stride()[:3])
 
     def quant(self, stream):
         B, H, T, D = self.shape
-        rc = self.lib.flw_quant_qkv_e4m3(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
-                                         B, H, T, D, self.sx, self.gran, self.q8.data_ptr(),
-                                         self.k8.data_ptr(), self.vt.data_ptr(), self.sc.data_ptr(),
-                                         self.ws.data_ptr(), self.ws.numel(), stream)
+        rc = self.lib.flw_quant_qkv_e4m3_deferq(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
+                                                B, H, T, D, self.sx, self.gran, self.q8.data_ptr(),
+                                                self.k8.data_ptr(), self.vt.data_ptr(), self.sc.data_ptr(),
+                                                self.qr.data_ptr(), self.ws.data_ptr(), self.ws.numel(), stream)
         self.L.check(rc, "quant")
 
     def attend(self, stream):
         B, H, T, D = self.shape
         G, base = self.G, self.sc.data_ptr()
-        rc = self.lib.flw_fp8_swa_fwd(self.q8.data_ptr(), self.s8, self.k8.data_ptr(), self.s8,
-                                      self.vt.data_ptr(), base, base + 4 * G, base + 8 * G, self.gran,
-                                      self.out.data_ptr(), self.dt, self.so, B, H, T, D, self.W, stream)
+        rc = self.lib.flw_fp8_swa_fwd_qx(self.q.data_ptr(), self.sq, self.q8.data_ptr(), self.qr.data_ptr(),
+                                         self.k8.data_ptr(), self.s8, self.vt.data_ptr(), base, base + 4 * G,
+                                         base + 8 * G, self.gran, self.out.data_ptr(), self.dt, self.so,
+                                         B, H, T, D, self.W, stream)
         self.L.check(rc, "swa")
 
 
@@ -258,7 +266,8 @@ def bench_attention(cfg, steps, warmup):
     return dict(wall_s=wall, ms_per_step=wall_ms, quant_ms=float(np.mean(quant_ms)),
                 attn_ms=float(np.mean(attn_ms)), attn_ms_min=float(np.min(attn_ms)),
                 flops=4 * D * B * H * in_window_pairs(T, cfg["W"]),
-                quant_bytes=3 * B * H * T * D * (2 * q.element_size() + 1), dtype=q.dtype)
+                # amax pass: Q, K, V read; quantise pass: K, V read, their codes written
+                quant_bytes=B * H * T * D * (5 * q.element_size() + 2), dtype=q.dtype)
 
 
 def bench_gemm(cfg, steps, warmup):

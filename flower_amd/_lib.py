@@ -40,6 +40,10 @@ SIGNATURES = {
     "flw_quant_qkv_e4m3": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                    c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_size_t, c_void_p]),
+    "flw_qk_norm_rope_quant_e4m3": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
+                                            c_int64, _P64, c_int, c_float, c_void_p, c_void_p, c_int, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                            c_void_p]),
     "flw_noalloc_scratch_bytes": (c_size_t, []),
     "flw_quant_qkv_e4m3_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                            c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
@@ -59,6 +63,12 @@ SIGNATURES = {
     "flw_fp8_swa_fwd": (c_int, [c_void_p, _P64, c_void_p, _P64, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_int, c_void_p, c_int, _P64, c_int64, c_int64, c_int64, c_int64,
                                 c_int64, c_void_p]),
+    "flw_fp8_swa_fwd_qx": (c_int, [c_void_p, _P64, c_void_p, c_void_p, c_void_p, _P64, c_void_p, c_void_p,
+                                   c_void_p, c_void_p, c_int, c_void_p, c_int, _P64, c_int64, c_int64, c_int64,
+                                   c_int64, c_int64, c_void_p]),
+    "flw_quant_qkv_e4m3_deferq": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
+                                          c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                          c_void_p, c_size_t, c_void_p]),
     "flw_fp8_swa_workspace_bytes": (c_size_t, [c_int64] * 4),
     "flw_fp8_swa_attention_forward_amax": (c_int, [c_void_p, c_void_p, c_void_p, c_int, _P64, c_int64, c_int64,
                                                    c_int64, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p,

@@ -1,21 +1,30 @@
-"""Attention-side operators of the reference's model code, on the HIP library.
+"""Attention-side operators and modules of the reference's model code, on the HIP library.
 
-``_fake_quant_e4m3``  -- flower/models/base.py:167-203: straight-through e4m3
-                         quantise-dequantise of Q/K/V (the ``model.fp8_attention_sim`` probe).
-                         Forward value computed by one HIP amax pass + one fused
-                         quantise/dequantise pass, rounded to x.dtype step by step exactly as the
-                         reference's torch op sequence; backward is the identity.
-``causal_mask``       -- base.py:418-423, the boolean (T, T) band mask (plain torch).
-``fp8_attention``     -- the ``attn_precision: fp8`` route (config.py:373): Q/K/V after QK-norm
-                         and RoPE go through the fused FP8 SWA kernel.
+``_fake_quant_e4m3``    -- flower/models/base.py:167-203: straight-through e4m3
+                           quantise-dequantise of Q/K/V (the ``model.fp8_attention_sim`` probe).
+                           Forward value computed by one HIP amax pass + one fused
+                           quantise/dequantise pass, rounded to x.dtype step by step exactly as the
+                           reference's torch op sequence; backward is the identity.
+``causal_mask``         -- base.py:418-423, the boolean (T, T) band mask (plain torch).
+``HeadRMSNorm``         -- base.py:341-357, parameter-free QK-norm (torch ops, the reference maths).
+``RotaryEmbedding``     -- base.py:436-483, RoPE with cached fp32 cos / sin tables.
+``CausalSelfAttention`` -- base.py:553-665 with the ``attn_precision`` switch (config.py:373):
+                           "fp8" routes the heads through the FP8 sliding-window kernel, with the
+                           QK-norm, RoPE and the e4m3 quantisation of Q/K/V fused in one HIP pass
+                           pair (the reference's quantisation point, "after QK-norm and RoPE",
+                           base.py:634-637); "bf16" through the HIP bf16 sliding-window kernel.
+``fp8_attention``       -- the FP8 route on (B, H, T, D) Q/K/V that are already normed and rotated.
 """
 
 from __future__ import annotations
 
 import torch
+import torch.nn as nn
 
 from . import _lib
-from .kernels.fp8_swa_attention import fp8_swa_attention_forward
+from .kernels.fp8_swa_attention import (fp8_swa_attention_forward, fp8_swa_attention_from_codes,
+                                        qk_norm_rope_quant_e4m3)
+from .kernels.swa_attention import swa_attention
 
 
 class _FakeQuantE4M3(torch.autograd.Function):
@@ -73,3 +82,171 @@ def fp8_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, local_windo
     """Forward-only FP8 attention for (B, H, T, D) Q/K/V; ``local_window=None`` is full causal."""
     window = q.shape[2] if local_window is None else local_window
     return fp8_swa_attention_forward(q, k, v, window, granularity=granularity)
+
+
+class HeadRMSNorm(nn.Module):
+    """Parameter-free RMSNorm over the head dimension (QK-norm), base.py:341-357."""
+
+    def __init__(self, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        rms = x.float().pow(2).mean(dim=-1, keepdim=True).add(self.eps).rsqrt()
+        return (x.float() * rms).to(dtype=x.dtype)
+
+
+class RotaryEmbedding(nn.Module):
+    """RoPE with cached cos / sin tables (base.py:436-483): pairs (2i, 2i+1) rotate by
+    position * base^(-2i / head_dim); the fp32 tables are built once on the CPU and cast to the
+    activations' dtype at use, as the reference does, so the fused kernel and the torch path see
+    the same table values."""
+
+    def __init__(self, head_dim: int, max_seq_len: int, base: float = 10000.0) -> None:
+        super().__init__()
+        if head_dim % 2 != 0:
+            raise ValueError("RoPE requires even head_dim")
+        self._base = base
+        self._head_dim = head_dim
+        cos, sin = self._tables(max_seq_len)
+        self.register_buffer("cos", cos, persistent=False)
+        self.register_buffer("sin", sin, persistent=False)
+        self._cast = {}
+
+    def _tables(self, seq_len: int):
+        inv_freq = 1.0 / (self._base ** (torch.arange(0, self._head_dim, 2).float() / self._head_dim))
+        freqs = torch.outer(torch.arange(seq_len).float(), inv_freq)
+        shape = (1, 1, seq_len, self._head_dim)
+        return (freqs.cos().repeat_interleave(2, dim=-1).view(shape),
+                freqs.sin().repeat_interleave(2, dim=-1).view(shape))
+
+    def _extend_cache(self, seq_len: int) -> None:
+        """Tables for longer sequences, built lazily (base.py:471-476)."""
+        cos, sin = self._tables(seq_len)
+        self.register_buffer("cos", cos, persistent=False)
+        self.register_buffer("sin", sin, persistent=False)
+        self._cast = {}
+
+    @staticmethod
+    def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+        x1 = x[..., ::2]
+        x2 = x[..., 1::2]
+        return torch.stack((-x2, x1), dim=-1).flatten(-2)
+
+    def tables(self, seq_len: int, dtype: torch.dtype, device) -> tuple[torch.Tensor, torch.Tensor]:
+        """(cos, sin) as contiguous [seq_len, head_dim] tensors of ``dtype`` on ``device``."""
+        if seq_len > self.cos.shape[-2]:
+            self._extend_cache(seq_len)
+        key = (seq_len, dtype, torch.device(device), self.cos.data_ptr())
+        hit = self._cast.get(key)
+        if hit is None:
+            hit = tuple(t[0, 0, :seq_len].to(device=device, dtype=dtype).contiguous() for t in (self.cos, self.sin))
+            self._cast = {key: hit}
+        return hit
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        cos, sin = self.tables(q.shape[-2], q.dtype, q.device)
+        return q * cos + self._rotate_half(q) * sin, k * cos + self._rotate_half(k) * sin
+
+
+class CausalSelfAttention(nn.Module):
+    """The reference's attention module (base.py:553-665) on this build's kernels.
+
+    ``config`` carries the reference's fields: d_model, num_heads, max_seq_len, rope_base,
+    use_bias (default True), qk_norm (False), fp8_attention_sim (False) and attn_precision
+    ("bf16" | "fp8", config.py:373; validated as config.py:464-465), plus this build's
+    ``fp8_attention_granularity`` ("head" by default: one e4m3 scale per head for each of Q, K, V).
+
+    attn_precision "fp8": forward-only, like the FP8 kernel (fp8_swa_attention.py:230-234: raises
+    RuntimeError if gradients would be needed). The qkv projection, then ONE HIP pass pair that
+    applies QK-norm and RoPE to q and k and quantises q', k', v to e4m3 (the reference's
+    quantisation point, base.py:634-637, "exactly the tensors a real FP8 attention kernel would
+    consume"), then the FP8 sliding-window kernel writing the (B, T, H, D) output in place, then
+    ``out``. ``forward_unfused`` is the same route with the heads built by ``qkv_heads`` in torch.
+    attn_precision "bf16": ``qkv_heads`` then the differentiable HIP bf16 sliding-window kernel
+    (a full causal window when ``local_window`` is None). The reference's flex / SDPA choice and
+    its RBF distance bias (local_attn_kernel_bias "rbf") are not offered: rbf raises ValueError.
+    """
+
+    def __init__(self, config, local_window: int | None = None) -> None:
+        super().__init__()
+        if config.d_model % config.num_heads != 0:
+            raise ValueError("d_model must be divisible by num_heads")
+        precision = getattr(config, "attn_precision", "bf16")
+        if precision not in {"bf16", "fp8"}:
+            raise ValueError(f"attn_precision must be bf16|fp8, got {precision!r}")
+        if getattr(config, "local_attn_kernel_bias", "none") != "none":
+            raise ValueError("local_attn_kernel_bias 'rbf' is not supported by the HIP attention kernels")
+        self.num_heads = config.num_heads
+        self.head_dim = config.d_model // config.num_heads
+        self.local_window = local_window
+        self.attn_precision = precision
+        self.fp8_granularity = getattr(config, "fp8_attention_granularity", "head")
+        self.rope = RotaryEmbedding(self.head_dim, getattr(config, "max_seq_len", 8192),
+                                    base=getattr(config, "rope_base", 10000.0))
+        bias = bool(getattr(config, "use_bias", True))
+        self.qkv = nn.Linear(config.d_model, config.d_model * 3, bias=bias)
+        self.out = nn.Linear(config.d_model, config.d_model, bias=bias)
+        self.out._is_residual_out = True
+        self.qk_norm = HeadRMSNorm() if bool(getattr(config, "qk_norm", False)) else None
+        self.fp8_attention_sim = bool(getattr(config, "fp8_attention_sim", False))
+
+    def _split(self, x: torch.Tensor) -> torch.Tensor:
+        bsz, seq_len, _ = x.shape
+        return x.view(bsz, seq_len, self.num_heads, self.head_dim).transpose(1, 2)
+
+    def _window(self, seq_len: int) -> int:
+        return seq_len if self.local_window is None else self.local_window
+
+    def qkv_heads(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """Project to per-head (q, k, v), apply QK-norm, then RoPE (base.py:618-639)."""
+        q, k, v = self.qkv(x).chunk(3, dim=-1)
+        q, k, v = self._split(q), self._split(k), self._split(v)
+        if self.qk_norm is not None:
+            q, k = self.qk_norm(q), self.qk_norm(k)
+        q, k = self.rope(q, k)
+        if self.fp8_attention_sim:
+            q, k, v = _fake_quant_e4m3(q), _fake_quant_e4m3(k), _fake_quant_e4m3(v)
+        return q, k, v
+
+    def _check_forward_only(self, x: torch.Tensor) -> None:
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            raise RuntimeError(
+                "attn_precision='fp8' is forward-only and has no backward (fp8_swa_attention_forward); "
+                "run it under torch.no_grad() / inference_mode or with frozen parameters.")
+
+    def forward(self, x: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
+        if self.attn_precision == "fp8":
+            return self._forward_fp8(x, trace)
+        q, k, v = self.qkv_heads(x)
+        out = swa_attention(q, k, v, self._window(x.shape[1]))
+        return self.out(out.transpose(1, 2).reshape(x.shape))
+
+    def _forward_fp8(self, x: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
+        """qkv -> fused QK-norm + RoPE + e4m3 quantisation -> FP8 SWA -> out. ``trace`` (a dict,
+        for checks) receives the projection "qkv", the transformed "q" / "k", the codes and scales,
+        and the attention output "attn"."""
+        self._check_forward_only(x)
+        B, T, d = x.shape
+        y = self.qkv(x)
+        q, k, v = (self._split(t) for t in y.chunk(3, dim=-1))
+        cos, sin = self.rope.tables(T, y.dtype, y.device)
+        res = qk_norm_rope_quant_e4m3(q, k, v, qk_norm=self.qk_norm is not None,
+                                      eps=self.qk_norm.eps if self.qk_norm is not None else 0.0,
+                                      rope_cos=cos, rope_sin=sin, granularity=self.fp8_granularity,
+                                      return_transformed=trace is not None)
+        q8, k8, vt, scales = res[:4]
+        a = torch.empty((B, T, d), dtype=y.dtype, device=y.device)
+        fp8_swa_attention_from_codes(q8, k8, vt, scales, self._window(T), granularity=self.fp8_granularity,
+                                     out=a.view(B, T, self.num_heads, self.head_dim).transpose(1, 2))
+        if trace is not None:
+            trace.update(qkv=y, q=res[4], k=res[5], q8=q8, k8=k8, v_tiles=vt, scales=scales, attn=a)
+        return self.out(a)
+
+    def forward_unfused(self, x: torch.Tensor) -> torch.Tensor:
+        """The FP8 route composed from the reference's pieces: ``qkv_heads`` in torch, then
+        ``fp8_swa_attention_forward`` (its own quantisation), then ``out``."""
+        self._check_forward_only(x)
+        q, k, v = self.qkv_heads(x)
+        out = fp8_swa_attention_forward(q, k, v, self._window(x.shape[1]), granularity=self.fp8_granularity)
+        return self.out(out.transpose(1, 2).reshape(x.shape))

@@ -31,10 +31,21 @@ int compute_units();
 // e4m3 quantisation of 1-3 (B, H, T, D) tensors of one shape (flw_quant.hip): amax pass + quantise
 // pass, or, with amax_given ([tensor][scale group] |x| max bit patterns from the producer), the
 // quantise pass alone.
+// Optional pre-quantisation transform of the first two tensors (q, k): HeadRMSNorm and / or RoPE
+// (tables [T, D] in the input dtype), the transformed values written to qout / kout if non-null.
+struct QkTransform {
+  int norm = 0;
+  float eps = 0.0f;
+  const void* rcos = nullptr;
+  const void* rsin = nullptr;
+  void* qout = nullptr;
+  void* kout = nullptr;
+};
 int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
                  int64_t D, const int64_t* strides, int granularity, const int* layouts,
                  uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
-                 hipStream_t stream, Timer tm, const uint32_t* amax_given = nullptr);
+                 hipStream_t stream, Timer tm, const uint32_t* amax_given = nullptr,
+                 const QkTransform* xf = nullptr, float* q_rcp_deferred = nullptr);
 
 // Launch of a kernel taking one parameter struct, optionally recording start / stop events.
 template <typename P>
@@ -122,6 +133,22 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
                    : __uint_as_float(((e + 120u) << 23) | (m << 20));
   v = ((c & 0x7Fu) == 0x7Fu) ? __uint_as_float(0x7FC00000u) : v;   // NaN, by its bit pattern
   return __uint_as_float(__float_as_uint(v) | s);
+}
+
+// x / s from r = RN(1 / s): one product and two FMAs, the correctly rounded quotient whenever
+// |x / s| >= 2^-20 (below that the correction can underflow, but every such quotient is an e4m3
+// zero); the sign is copied from x so that -0 and tiny negatives keep the reference's sign. Used
+// by the quantisers and by the attention kernel's quantise-on-load of Q, so both produce the same
+// codes.
+__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
+  const float q0 = x * r;
+  const float e = fmaf(-q0, s, x);
+  return __builtin_copysignf(fmaf(e, r, q0), x);
+}
+
+// Finite test on the bit pattern (holds in translation units built without NaN semantics).
+__device__ __forceinline__ bool finite_bits(float x) {
+  return (__float_as_uint(x) & 0x7F800000u) != 0x7F800000u;
 }
 
 // |x| as an unsigned bit pattern: ordered like |x| for finite values, NaN above +inf, so an

@@ -37,6 +37,19 @@ struct QTensor {
   float* scale_out;            // 1 | d1 | d0*d1
   int layout;
   int rows_packed;             // s2 == D: a chunk is one contiguous run of memory
+  // Optional transform applied before the amax and the codes (XFORM kernels only): the
+  // HeadRMSNorm and RoPE of CausalSelfAttention.qkv_heads, with the transformed values also
+  // written to tout (contiguous (B, H, T, D), input dtype) when it is not null.
+  int norm;                    // HeadRMSNorm over each row of D
+  float eps;
+  const void* rcos;            // RoPE tables [T, D] in the input dtype, or null
+  const void* rsin;
+  void* tout;
+  // Deferred codes (the attention kernel quantises this tensor on load): the scale and its
+  // reciprocal RN(1 / scale) (to rcp_out) are written, and codes only for scale groups whose amax
+  // is not finite (the exact path, which the attention kernel leaves to this kernel).
+  int defer;
+  float* rcp_out;
 };
 
 struct QuantParams {
@@ -67,7 +80,57 @@ __device__ __forceinline__ int64_t vec_offset(const QTensor& t, int64_t r0, int6
   return row * t.s2 + cv * n;
 }
 
+// Rounding to the tensor's dtype (bf16: round to nearest even, NaN quietened; fp32: identity).
 template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (sizeof(T) == 2) return round_bf16(x);
+  return x;
+}
+
+// The pre-attention transform of CausalSelfAttention.qkv_heads (flower/models/base.py:630-637) on
+// one 16-byte vector (column block cv of row `row` of a slice), every step rounded to the tensor's
+// dtype as the reference's torch ops round it:
+//   HeadRMSNorm (base.py:355-357): h = dtype(x * (1 / sqrt(mean(x^2) + eps))), fp32 maths; the
+//     row's sum of squares is reduced over the vpr lanes that hold the row (aligned groups);
+//   RoPE (base.py:478-483, rotate_half :465-469): out[2i]   = dtype(dtype(h[2i] c) + dtype(-h[2i+1] s)),
+//     out[2i+1] = dtype(dtype(h[2i+1] c) + dtype(h[2i] s)), c / s from the [T, D] tables.
+// Every lane of a vpr group must call this together (valid or not: invalid lanes carry
+// zeros and read no table).
+template <typename T>
+__device__ __forceinline__ void qk_transform(const QTensor& t, float* f, int64_t row, int64_t cv, int vpr,
+                                             int64_t d3, bool valid) {
+  // Separate products and sums, as the reference's separate torch ops round them: no FMA
+  // contraction in this function (hipcc contracts a * b + c by default, which would change the
+  // fp32 results).
+#pragma clang fp contract(off)
+  constexpr int N = Vec16<T>::N;
+  if (t.norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ss = fmaf(f[i], f[i], ss);
+    for (int o = 1; o < vpr; o <<= 1) ss = ss + __shfl_xor(ss, o, 64);
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)d3 + t.eps);   // IEEE sqrt and division
+#pragma unroll
+    for (int i = 0; i < N; ++i) f[i] = round_to<T>(f[i] * r);
+  }
+  if (t.rcos != nullptr && valid) {
+    float c[N], sn[N];
+    const int64_t off = row * d3 + cv * N;
+    Vec16<T>::load(static_cast<const T*>(t.rcos) + off, c);
+    Vec16<T>::load(static_cast<const T*>(t.rsin) + off, sn);
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      const float a0 = round_to<T>(f[i] * c[i]);
+      const float b0 = round_to<T>(-f[i + 1] * sn[i]);
+      const float a1 = round_to<T>(f[i + 1] * c[i + 1]);
+      const float b1 = round_to<T>(f[i] * sn[i + 1]);
+      f[i] = round_to<T>(a0 + b0);
+      f[i + 1] = round_to<T>(a1 + b1);
+    }
+  }
+}
+
+template <typename T, bool XFORM = false>
 __global__ __launch_bounds__(kThreads) void amax_kernel(QuantParams p) {
   using V = Vec16<T>;
   __shared__ uint32_t red[kThreads / 64];
@@ -90,6 +153,13 @@ __global__ __launch_bounds__(kThreads) void amax_kernel(QuantParams p) {
       } else {
 #pragma unroll
         for (int i = 0; i < V::N; ++i) f[u][i] = 0.0f;
+      }
+    }
+    if (XFORM && (t.norm || t.rcos != nullptr)) {          // uniform over the workgroup
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t v = v0 + (int64_t)u * kThreads;
+        qk_transform<T>(t, f[u], r0 + v / vpr, v % vpr, (int)vpr, p.d3, v < nvec);
       }
     }
 #pragma unroll
@@ -142,14 +212,6 @@ __device__ __forceinline__ float clamp448(float y) {
   return y < -kE4m3Max ? -kE4m3Max : y;
 }
 
-// x / s from r = RN(1 / s): one product and two FMAs, the correctly rounded quotient whenever
-// |x / s| >= 2^-20 (below that the correction can underflow, but every such quotient is an e4m3
-// zero); the sign is copied from x so that -0 and tiny negatives keep the reference's sign.
-__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
-  const float q0 = x * r;
-  const float e = fmaf(-q0, s, x);
-  return __builtin_copysignf(fmaf(e, r, q0), x);
-}
 
 // Byte offset of element (key kk, dim d) inside a 64 x D VTILE tile.
 __device__ __forceinline__ uint32_t vtile_offset(uint32_t kk, uint32_t d) {
@@ -184,7 +246,8 @@ __device__ __forceinline__ void codes_of(const float* f, float s, float r, bool 
 }
 
 // MODE 0: e4m3 codes with the _per_tensor_fp8 recipe. MODE 1: _fake_quant_e4m3 forward value.
-template <typename T, int MODE>
+// XFORM: the q / k transform of qk_transform first (MODE 0 only).
+template <typename T, int MODE, bool XFORM = false>
 __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
   using V = Vec16<T>;
   constexpr bool kBf16 = sizeof(T) == 2;
@@ -211,9 +274,13 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
   } else {
     scale = (amax < kEps ? kEps : amax) / kE4m3Max;     // IEEE fp32 division
   }
-  if (writes_scale(p.granularity, slice, i0)) t.scale_out[group_index(p.granularity, slice, i1)] = scale;
   const bool fast = MODE == 0 && __builtin_isfinite(amax);   // uniform over the workgroup
   const float rcp = 1.0f / scale;                            // IEEE: correctly rounded
+  if (writes_scale(p.granularity, slice, i0)) {
+    t.scale_out[group_index(p.granularity, slice, i1)] = scale;
+    if (MODE == 0 && t.rcp_out != nullptr) t.rcp_out[group_index(p.granularity, slice, i1)] = rcp;
+  }
+  if (MODE == 0 && t.defer && fast) return;                  // codes made by the attention kernel
   // A given amax is the caller's claim about the data (a producer's epilogue maximum, or a
   // maximum combined across shards). The fast path relies on |x| <= amax (then |x / s| <= 448
   // and the clamp is inert), so with a given amax every vector is checked against it, and a
@@ -243,6 +310,25 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
       } else {
 #pragma unroll
         for (int i = 0; i < V::N; ++i) f[u][i] = 0.0f;
+      }
+    }
+    if (XFORM && (t.norm || t.rcos != nullptr)) {          // uniform over the workgroup
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t v = v0 + (int64_t)u * kThreads;
+        qk_transform<T>(t, f[u], r0 + v / vpr, v % vpr, (int)vpr, p.d3, v < nvec);
+        if (t.tout != nullptr && v < nvec) {
+          T* dst = static_cast<T*>(t.tout) + (slice * p.d2 + r0) * p.d3 + v * V::N;
+          if constexpr (sizeof(T) == 2) {
+            *reinterpret_cast<uint4*>(dst) = make_uint4(
+                f32_to_bf16_bits(f[u][0]) | (f32_to_bf16_bits(f[u][1]) << 16),
+                f32_to_bf16_bits(f[u][2]) | (f32_to_bf16_bits(f[u][3]) << 16),
+                f32_to_bf16_bits(f[u][4]) | (f32_to_bf16_bits(f[u][5]) << 16),
+                f32_to_bf16_bits(f[u][6]) | (f32_to_bf16_bits(f[u][7]) << 16));
+          } else {
+            *reinterpret_cast<float4*>(dst) = make_float4(f[u][0], f[u][1], f[u][2], f[u][3]);
+          }
+        }
       }
     }
 #pragma unroll
@@ -690,13 +776,21 @@ template <int MODE>
 static int launch_quant(const QuantParams& p, int ntensors, int dtype, hipStream_t s, const char* name,
                         Timer tm) {
   dim3 grid((unsigned)p.nchunks, (unsigned)(p.d0 * p.d1), (unsigned)ntensors);
-  bool any_vtile = false;
-  for (int i = 0; i < ntensors; ++i) any_vtile |= p.t[i].layout == FLW_LAYOUT_VTILE;
+  bool any_vtile = false, xform = false;
+  for (int i = 0; i < ntensors; ++i) {
+    any_vtile |= p.t[i].layout == FLW_LAYOUT_VTILE;
+    xform |= p.t[i].norm != 0 || p.t[i].rcos != nullptr;
+  }
   const size_t lds = MODE == 0 && any_vtile ? (size_t)(kRowsPerChunk * p.d3) : 0;
-  const void* ka = dtype == FLW_F32 ? reinterpret_cast<const void*>(&amax_kernel<float>)
-                                    : reinterpret_cast<const void*>(&amax_kernel<uint16_t>);
-  const void* kq = dtype == FLW_F32 ? reinterpret_cast<const void*>(&quant_kernel<float, MODE>)
-                                    : reinterpret_cast<const void*>(&quant_kernel<uint16_t, MODE>);
+  const bool f32 = dtype == FLW_F32;
+  const void* ka = xform ? (f32 ? reinterpret_cast<const void*>(&amax_kernel<float, true>)
+                                : reinterpret_cast<const void*>(&amax_kernel<uint16_t, true>))
+                         : (f32 ? reinterpret_cast<const void*>(&amax_kernel<float>)
+                                : reinterpret_cast<const void*>(&amax_kernel<uint16_t>));
+  const void* kq = xform ? (f32 ? reinterpret_cast<const void*>(&quant_kernel<float, MODE, MODE == 0>)
+                                : reinterpret_cast<const void*>(&quant_kernel<uint16_t, MODE, MODE == 0>))
+                         : (f32 ? reinterpret_cast<const void*>(&quant_kernel<float, MODE>)
+                                : reinterpret_cast<const void*>(&quant_kernel<uint16_t, MODE>));
   if (p.amax_given) {                     // amax from the producer: the quantise pass only
     (void)launch_ext(kq, grid, dim3(kThreads), lds, s, p, tm.start, tm.stop);
     return check_launch(name);
@@ -716,7 +810,8 @@ static void set_tensor(QTensor& t, const void* x, int64_t sb, int64_t sh, int64_
 int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, int64_t T,
                  int64_t D, const int64_t* strides, int granularity, const int* layouts,
                  uint8_t* const* outs, float* const* scale_outs, void* ws, size_t ws_bytes,
-                 hipStream_t stream, Timer tm, const uint32_t* amax_given) {
+                 hipStream_t stream, Timer tm, const uint32_t* amax_given, const QkTransform* xf,
+                 float* q_rcp_deferred) {
   FLW_REQUIRE(n >= 1 && n <= 3, FLW_E_INVALID, "1 to 3 tensors per call");
   FLW_REQUIRE(granularity >= FLW_SCALE_TENSOR && granularity <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", granularity);
   FLW_REQUIRE(amax_given != nullptr || (ws != nullptr && ws_bytes >= (size_t)n * partial_bytes(B, H, T)),
@@ -735,6 +830,20 @@ int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, 
     }
     set_tensor(p.t[i], xs[i], strides[3 * i], strides[3 * i + 1], strides[3 * i + 2], D, layouts[i], outs[i],
                nullptr, scale_outs[i]);
+    if (xf != nullptr && i < 2) {
+      FLW_REQUIRE(layouts[i] == FLW_LAYOUT_BHTD, FLW_E_INVALID, "q / k transforms need BHTD codes");
+      p.t[i].norm = xf->norm;
+      p.t[i].eps = xf->eps;
+      p.t[i].rcos = xf->rcos;
+      p.t[i].rsin = xf->rsin;
+      p.t[i].tout = i == 0 ? xf->qout : xf->kout;
+    }
+  }
+  if (q_rcp_deferred != nullptr) {
+    FLW_REQUIRE(amax_given == nullptr && xf == nullptr && layouts[0] == FLW_LAYOUT_BHTD, FLW_E_INVALID,
+                "deferred Q codes need the amax pass, no transform and BHTD codes");
+    p.t[0].defer = 1;
+    p.t[0].rcp_out = q_rcp_deferred;
   }
   p.d0 = B; p.d1 = H; p.d2 = T; p.d3 = D;
   p.nchunks = nchunks_of(T); p.partials = static_cast<uint32_t*>(ws); p.granularity = granularity;
@@ -849,6 +958,50 @@ extern "C" int flw_quant_qkv_e4m3(const void* q, const void* k, const void* v, i
   float* sc[3] = {scales_out, scales_out + G, scales_out + 2 * G};
   return quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, sc, workspace,
                       workspace_bytes, static_cast<hipStream_t>(stream), take_timer());
+}
+
+extern "C" int flw_quant_qkv_e4m3_deferq(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                                         int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                                         int granularity, uint8_t* q8, uint8_t* k8, uint8_t* v_tiles,
+                                         float* scales_out, float* q_rcp_out, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  FLW_REQUIRE(strides != nullptr && scales_out != nullptr && q_rcp_out != nullptr, FLW_E_INVALID,
+              "null strides / scales / q_rcp_out");
+  const int64_t G = granularity == FLW_SCALE_TENSOR ? 1 : (granularity == FLW_SCALE_HEAD ? H : B * H);
+  const void* xs[3] = {q, k, v};
+  const int layouts[3] = {FLW_LAYOUT_BHTD, FLW_LAYOUT_BHTD, FLW_LAYOUT_VTILE};
+  uint8_t* outs[3] = {q8, k8, v_tiles};
+  float* sc[3] = {scales_out, scales_out + G, scales_out + 2 * G};
+  return quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, sc, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream), take_timer(), nullptr, nullptr, q_rcp_out);
+}
+
+extern "C" int flw_qk_norm_rope_quant_e4m3(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                                           int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                                           int qk_norm, float eps, const void* rope_cos, const void* rope_sin,
+                                           int granularity, uint8_t* q8, uint8_t* k8, uint8_t* v_tiles,
+                                           float* scales_out, void* q_out, void* k_out, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  FLW_REQUIRE(strides != nullptr && scales_out != nullptr, FLW_E_INVALID, "null strides / scales");
+  FLW_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), FLW_E_INVALID, "pass both RoPE tables or neither");
+  FLW_REQUIRE(D % 2 == 0, FLW_E_INVALID, "RoPE needs an even head_dim");
+  FLW_REQUIRE(((uintptr_t)rope_cos & 15) == 0 && ((uintptr_t)rope_sin & 15) == 0 && ((uintptr_t)q_out & 15) == 0 &&
+              ((uintptr_t)k_out & 15) == 0, FLW_E_INVALID, "RoPE tables and q_out / k_out must be 16-byte aligned");
+  FLW_REQUIRE(!(eps < 0.0f) && eps == eps, FLW_E_INVALID, "eps must be a non-negative number");
+  const int64_t G = granularity == FLW_SCALE_TENSOR ? 1 : (granularity == FLW_SCALE_HEAD ? H : B * H);
+  const void* xs[3] = {q, k, v};
+  const int layouts[3] = {FLW_LAYOUT_BHTD, FLW_LAYOUT_BHTD, FLW_LAYOUT_VTILE};
+  uint8_t* outs[3] = {q8, k8, v_tiles};
+  float* sc[3] = {scales_out, scales_out + G, scales_out + 2 * G};
+  QkTransform xf;
+  xf.norm = qk_norm != 0;
+  xf.eps = eps;
+  xf.rcos = rope_cos;
+  xf.rsin = rope_sin;
+  xf.qout = q_out;
+  xf.kout = k_out;
+  return quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, sc, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream), take_timer(), nullptr, &xf);
 }
 
 extern "C" int flw_fake_quant_e4m3(const void* x, int dtype, int64_t B, int64_t H, int64_t T,

@@ -65,6 +65,11 @@ struct SwaParams {
   int H, T, W, nM, nwg;
   int ramp;                   // query tiles per slice whose band starts at key 0 (fewer key tiles)
   int group_slices;           // slices per dispatch group (one XCD's share when it is whole slices)
+  // Optional: Q in the output's dtype (element strides), quantised on load with the reciprocals
+  // qr (RN(1 / q scale)) for scale groups whose scale is finite; q8 serves the others.
+  const void* qx;
+  int64_t xsb, xsh, xst;
+  const float* qr;
 };
 
 template <typename OutT> struct Store4;
@@ -160,9 +165,36 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   const float c = q_s * k_s * rsd * kLog2e;
 
   // Q fragments: B operand of S^T = K Q^T; lane (qcol, hh) holds Q[q][64 dc + 32 hh + 0..31].
+  // With Q given in its input dtype, the lane quantises its 32 values here with the quantiser's
+  // arithmetic (x / s as x * RN(1/s) plus one FMA correction, then v_cvt_pk_fp8_f32), so the
+  // codes are the ones the quantise pass would have written; groups whose scale is not finite
+  // (NaN / inf amax, the exact path) were coded by the quantiser and are read from q8.
   v8i qf[NDC];
-  {
-    const int qi = q0 + qcol < T ? q0 + qcol : T - 1;
+  const int qi_ld = q0 + qcol < T ? q0 + qcol : T - 1;
+  if (p.qx != nullptr && finite_bits(q_s)) {                  // uniform over the workgroup
+    const float qrcp = p.qr[si];
+    const OutT* qx = static_cast<const OutT*>(p.qx) + b * p.xsb + h * p.xsh + (int64_t)qi_ld * p.xst;
+    using QV = Vec16<OutT>;
+#pragma unroll
+    for (int dc = 0; dc < NDC; ++dc) {
+      if (D == 32 && hh) {
+        qf[dc] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        continue;
+      }
+      float f[32];
+#pragma unroll
+      for (int j = 0; j < 32 / QV::N; ++j) QV::load(qx + 64 * dc + 32 * hh + j * QV::N, f + j * QV::N);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * j], q_s, qrcp),
+                                                div_by_scale(f[4 * j + 1], q_s, qrcp), 0, false);
+        c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * j + 2], q_s, qrcp),
+                                            div_by_scale(f[4 * j + 3], q_s, qrcp), c, true);
+        qf[dc][j] = c;
+      }
+    }
+  } else {
+    const int qi = qi_ld;
     const uint8_t* qp = p.q8 + b * p.qsb + h * p.qsh + (int64_t)qi * p.qst;
 #pragma unroll
     for (int dc = 0; dc < NDC; ++dc) {
@@ -401,8 +433,15 @@ static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s
 static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, const int64_t* kst,
                    const uint8_t* vt, const float* qs, const float* ks, const float* vs, int gran,
                    void* out, int out_dtype, const int64_t* ost, int64_t B, int64_t H, int64_t T,
-                   int64_t D, int64_t window, hipStream_t stream, Timer tm) {
+                   int64_t D, int64_t window, hipStream_t stream, Timer tm, const void* qx = nullptr,
+                   const int64_t* xst = nullptr, const float* qr = nullptr) {
   FLW_REQUIRE(q8 && k8 && vt && qs && ks && vs && out && qst && kst && ost, FLW_E_INVALID, "null pointer argument");
+  if (qx != nullptr) {
+    const int64_t vec = out_dtype == FLW_F32 ? 4 : 8;
+    FLW_REQUIRE(xst != nullptr && qr != nullptr, FLW_E_INVALID, "null Q strides / reciprocals");
+    FLW_REQUIRE(xst[0] % vec == 0 && xst[1] % vec == 0 && xst[2] % vec == 0 && ((uintptr_t)qx & 15) == 0,
+                FLW_E_INVALID, "Q must have 16-byte aligned rows (strides multiples of %lld elements)", (long long)vec);
+  }
   FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
   FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
   FLW_REQUIRE(out_dtype == FLW_F32 || out_dtype == FLW_BF16, FLW_E_UNSUPPORTED, "output dtype %d", out_dtype);
@@ -431,6 +470,9 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.out = out; p.osb = ost[0]; p.osh = ost[1]; p.ost = ost[2];
   p.H = (int)H; p.T = (int)T; p.W = (int)W; p.nM = (int)nM;
   p.nwg = (int)(B * H * nM);
+  p.qx = qx;
+  p.qr = qr;
+  if (qx != nullptr) { p.xsb = xst[0]; p.xsh = xst[1]; p.xst = xst[2]; }
   p.ramp = W > 0 ? (int)std::min<int64_t>(nM, (W - 1) / kBM + 1) : 0;
   p.group_slices = ((B * H) % 8 == 0 && (p.nwg & 7) == 0) ? (int)(B * H / 8) : (int)(B * H);
   dim3 grid((unsigned)p.nwg);
@@ -443,7 +485,7 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct SwaWorkspace {
-  size_t q8, k8, vt, scales, partials, total;
+  size_t q8, k8, vt, scales, qrcp, partials, total;
 };
 
 static SwaWorkspace swa_ws_layout(int64_t B, int64_t H, int64_t T, int64_t D) {
@@ -453,7 +495,8 @@ static SwaWorkspace swa_ws_layout(int64_t B, int64_t H, int64_t T, int64_t D) {
   w.k8 = align256(n);
   w.vt = w.k8 + align256(n);
   w.scales = w.vt + align256(flw_vtile_bytes(B, H, T, D));
-  w.partials = w.scales + align256(3 * sizeof(float) * (size_t)(B * H));
+  w.qrcp = w.scales + align256(3 * sizeof(float) * (size_t)(B * H));
+  w.partials = w.qrcp + align256(sizeof(float) * (size_t)(B * H));
   w.total = w.partials + align256(3 * flw_quant_workspace_bytes(B, H, T, D));
   return w;
 }
@@ -471,6 +514,19 @@ extern "C" int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, cons
   return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, granularity,
                  out, out_dtype, out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream),
                  take_timer());
+}
+
+extern "C" int flw_fp8_swa_fwd_qx(const void* q, const int64_t* q_strides, const uint8_t* q8_nonfinite,
+                                  const float* q_rcp, const uint8_t* k8, const int64_t* k_strides,
+                                  const uint8_t* v_tiles, const float* q_scale, const float* k_scale,
+                                  const float* v_scale, int granularity, void* out, int dtype,
+                                  const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                                  int64_t window, void* stream) {
+  FLW_REQUIRE(q != nullptr, FLW_E_INVALID, "null q");
+  const int64_t s8[3] = {H * T * D, T * D, D};
+  return swa_fwd(q8_nonfinite, s8, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, granularity, out, dtype,
+                 out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream), take_timer(), q, q_strides,
+                 q_rcp);
 }
 
 extern "C" size_t flw_fp8_swa_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
@@ -500,12 +556,16 @@ static int attention_forward(const void* q, const void* k, const void* v, int dt
   // An armed timer brackets the whole operator: start with the first quantiser launch, stop with
   // the attention kernel.
   const Timer tm = take_timer();
+  // Without a producer amax, Q is quantised on load by the attention kernel: the quantise pass
+  // writes only Q's scale and its reciprocal (and Q's codes for groups whose amax is not finite)
+  // and spends its bandwidth on K and V. With a given amax the quantiser writes all three codes.
+  float* qrcp = amax == nullptr ? reinterpret_cast<float*>(ws + w.qrcp) : nullptr;
   int rc = quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, scs,
-                        ws + w.partials, w.total - w.partials, s, Timer{tm.start, nullptr}, amax);
+                        ws + w.partials, w.total - w.partials, s, Timer{tm.start, nullptr}, amax, nullptr, qrcp);
   if (rc) return rc;
   const int64_t s8[3] = {H * T * D, T * D, D};
   return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, granularity, out, dtype, strides + 9,
-                 B, H, T, D, window, s, Timer{nullptr, tm.stop});
+                 B, H, T, D, window, s, Timer{nullptr, tm.stop}, qrcp ? q : nullptr, strides, qrcp);
 }
 
 extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, int dtype,

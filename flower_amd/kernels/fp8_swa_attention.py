@@ -230,3 +230,92 @@ def reference_swa_attention(
     keep = (idx[:, None] >= idx[None, :]) & ((idx[:, None] - idx[None, :]) < window)
     scores = scores.masked_fill(~keep, float("-inf"))
     return (torch.softmax(scores, dim=-1) @ vf).to(q.dtype)
+
+
+def qk_norm_rope_quant_e4m3(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, qk_norm: bool,
+                            eps: float = 1e-6, rope_cos: torch.Tensor | None = None,
+                            rope_sin: torch.Tensor | None = None, granularity: str = "head",
+                            return_transformed: bool = False):
+    """The FP8 attention's quantisation point of ``CausalSelfAttention.qkv_heads``
+    (flower/models/base.py:618-639) in one HIP pass pair: HeadRMSNorm (``qk_norm``, base.py:341-357)
+    and RoPE (``rope_cos`` / ``rope_sin``: [T, D] tables, base.py:436-483) applied to q and k, then
+    the three ``_per_tensor_fp8`` quantisations (fp8_swa_attention.py:242-244) of q', k', v -- the
+    transformed q', k' never round-trip through HBM.
+
+    q / k / v: (B, H, T, D) bf16 or fp32 on the GPU, any strides with D contiguous (e.g. the head
+    views of the qkv projection's output). Returns ``(q8, k8, v_tiles, scales)``: e4m3 codes of q'
+    and k' (uint8 (B, H, T, D)), v's codes in the attention kernel's tile layout, and the float32
+    scales [3 * groups] in the order q, k, v; with ``return_transformed`` also (q', k') in the
+    input dtype (for checks; it costs their extra write).
+    """
+    lib = _lib.load()
+    _lib.require_gpu(q, k, v)
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"expected three (B, H, T, D) tensors of one shape, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    if granularity not in _lib.GRANULARITY:
+        raise ValueError(f"granularity must be one of {sorted(_lib.GRANULARITY)}, got {granularity!r}")
+    B, H, T, D = q.shape
+    if D not in (32, 64, 128):
+        raise ValueError(f"head_dim must be 32/64/128 for the MFMA tiling, got {D}")
+    if (rope_cos is None) != (rope_sin is None):
+        raise ValueError("pass both RoPE tables or neither")
+    if rope_cos is not None:
+        if rope_cos.shape != (T, D) or rope_sin.shape != (T, D):
+            raise ValueError(f"RoPE tables must be [T, D] = [{T}, {D}]")
+        rope_cos = rope_cos.to(device=q.device, dtype=q.dtype).contiguous()
+        rope_sin = rope_sin.to(device=q.device, dtype=q.dtype).contiguous()
+    q, sq = _prepare(q)
+    k, sk = _prepare(k)
+    v, sv = _prepare(v)
+    G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+    dev = q.device
+    q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device=dev)
+    k8 = torch.empty_like(q8)
+    vt = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device=dev)
+    scales = torch.empty(3 * G, dtype=torch.float32, device=dev)
+    qt = kt = None
+    if return_transformed:
+        qt = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+        kt = torch.empty_like(qt)
+    ws = _lib.workspace(3 * lib.flw_quant_workspace_bytes(B, H, T, D), dev)
+    rc = lib.flw_qk_norm_rope_quant_e4m3(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.dtype_code(q.dtype), B, H, T, D,
+        _lib.i64s(*sq, *sk, *sv), int(bool(qk_norm)), float(eps), _lib.ptr(rope_cos), _lib.ptr(rope_sin),
+        _lib.GRANULARITY[granularity], q8.data_ptr(), k8.data_ptr(), vt.data_ptr(), scales.data_ptr(),
+        _lib.ptr(qt), _lib.ptr(kt), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+    _lib.check(rc, "qk_norm_rope_quant_e4m3")
+    if return_transformed:
+        return q8, k8, vt, scales, qt, kt
+    return q8, k8, vt, scales
+
+
+def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: torch.Tensor,
+                                 scales: torch.Tensor, window: int, *, granularity: str = "head",
+                                 out_dtype: torch.dtype = torch.bfloat16,
+                                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """The attention kernel alone on pre-quantised operands (the ``_fp8_swa_fwd_kernel`` launch,
+    fp8_swa_attention.py:249-258): q8 / k8 uint8 (B, H, T, D) e4m3 codes, v_tiles in the
+    kernel's V layout, scales [3 * groups] (q, k, v), as ``qk_norm_rope_quant_e4m3`` returns them.
+    ``out``: optional (B, H, T, D) destination of ``out_dtype`` with D contiguous."""
+    lib = _lib.load()
+    _lib.require_gpu(q8, k8, v_tiles, scales)
+    B, H, T, D = q8.shape
+    G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
+    if scales.numel() != 3 * G or scales.dtype != torch.float32 or not scales.is_contiguous():
+        raise ValueError(f"scales must be a contiguous float32 tensor of {3 * G} elements")
+    if out is None:
+        out = torch.empty((B, H, T, D), dtype=out_dtype, device=q8.device)
+    elif out.shape != (B, H, T, D) or out.stride(-1) != 1:
+        raise ValueError("out must be a (B, H, T, D) tensor with D contiguous")
+    s8 = _lib.i64s(*q8.stride()[:3])
+    sk = _lib.i64s(*k8.stride()[:3])
+    base = scales.data_ptr()
+    rc = lib.flw_fp8_swa_fwd(q8.data_ptr(), s8, k8.data_ptr(), sk, v_tiles.data_ptr(), base, base + 4 * G,
+                             base + 8 * G, _lib.GRANULARITY[granularity], out.data_ptr(),
+                             _lib.dtype_code(out.dtype), _lib.i64s(*out.stride()[:3]), B, H, T, D, int(window),
+                             _lib.stream_of(q8))
+    _lib.check(rc, "fp8_swa_attention_from_codes")
+    return out

@@ -106,6 +106,37 @@ int flw_quant_qkv_e4m3(const void* q, const void* k, const void* v, int dtype, i
                        uint8_t* q8, uint8_t* k8, uint8_t* v_tiles, float* scales_out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* flw_quant_qkv_e4m3 with Q's codes deferred to the attention kernel (flw_fp8_swa_fwd_qx): the
+ * amax pass covers q, k, v; the quantise pass writes k8, v_tiles and all scales, plus q_rcp_out
+ * (1 | H | B*H floats, RN(1 / q scale)), and q8 codes only for Q's scale groups whose amax is not
+ * finite (left to the quantiser's exact path). Half the `_per_tensor_fp8` calls of
+ * flower/kernels/fp8_swa_attention.py:242-244 in full, the Q one split with the attention kernel. */
+int flw_quant_qkv_e4m3_deferq(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                              int64_t H, int64_t T, int64_t D, const int64_t* strides, int granularity,
+                              uint8_t* q8, uint8_t* k8, uint8_t* v_tiles, float* scales_out,
+                              float* q_rcp_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The FP8 attention's quantisation point in `CausalSelfAttention.qkv_heads`
+ * (flower/models/base.py:618-639: qkv -> heads -> HeadRMSNorm -> RoPE, "quantize AFTER QK-norm
+ * and RoPE", :634-637) fused with the three `_per_tensor_fp8` calls it feeds
+ * (flower/kernels/fp8_swa_attention.py:242-244): flw_quant_qkv_e4m3 on q', k', v where
+ *   q' = rope(norm(q)), k' = rope(norm(k)), every step rounded to the input dtype as torch rounds:
+ *   norm (qk_norm != 0; HeadRMSNorm, base.py:341-357): x' = dtype(x * (1 / sqrt(mean(x^2) + eps)))
+ *     over each (b, h, t) row of D, fp32 maths (IEEE sqrt and division);
+ *   rope (rope_cos / rope_sin: [T, D] contiguous tables in the input dtype, i.e. the module's
+ *     cached cos / sin cast to it as base.py:478-483 casts them; both NULL: no RoPE):
+ *     out[2i] = dtype(dtype(x'[2i] c[2i]) + dtype(-x'[2i+1] s[2i])),
+ *     out[2i+1] = dtype(dtype(x'[2i+1] c[2i+1]) + dtype(x'[2i] s[2i+1]))  (rotate_half, :465-469).
+ * The amax pass and the quantise pass both apply the transform, so q' and k' never go through
+ * HBM; q_out / k_out (contiguous (B, H, T, D), input dtype, may be NULL) receive them if given.
+ * Other arguments, layouts and the workspace as flw_quant_qkv_e4m3. */
+int flw_qk_norm_rope_quant_e4m3(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                                int64_t H, int64_t T, int64_t D, const int64_t* strides, int qk_norm,
+                                float eps, const void* rope_cos, const void* rope_sin, int granularity,
+                                uint8_t* q8, uint8_t* k8, uint8_t* v_tiles, float* scales_out,
+                                void* q_out, void* k_out, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
 /* flw_quant_qkv_e4m3 without a workspace: no counterpart in the reference. For callers that
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): the amax partials live in a library-owned device array of
@@ -166,6 +197,20 @@ int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* 
                     const float* k_scale, const float* v_scale, int granularity, void* out,
                     int out_dtype, const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
                     int64_t D, int64_t window, void* stream);
+
+/* flw_fp8_swa_fwd with Q in its input dtype, quantised on load by the attention kernel (the
+ * `_per_tensor_fp8(q)` of flower/kernels/fp8_swa_attention.py:242 moved into the kernel's
+ * prologue; every Q row is read by exactly one workgroup): q (B, H, T, D) bf16 or fp32 (= dtype,
+ * also the output dtype) with element strides q_strides[3]; q_rcp: RN(1 / q_scale) per scale
+ * group, and q8_nonfinite: contiguous (B, H, T, D) codes read only for groups whose scale is not
+ * finite -- both as flw_quant_qkv_e4m3_deferq writes them. The codes, hence the output, are
+ * those of flw_quant_qkv_e4m3 + flw_fp8_swa_fwd. */
+int flw_fp8_swa_fwd_qx(const void* q, const int64_t* q_strides, const uint8_t* q8_nonfinite,
+                       const float* q_rcp, const uint8_t* k8, const int64_t* k_strides,
+                       const uint8_t* v_tiles, const float* q_scale, const float* k_scale,
+                       const float* v_scale, int granularity, void* out, int dtype,
+                       const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                       int64_t window, void* stream);
 
 /* Workspace of flw_fp8_swa_attention_forward (e4m3 Q, K, tiled V, scales, amax partials). */
 size_t flw_fp8_swa_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D);

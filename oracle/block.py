@@ -8,6 +8,12 @@
              bf16( (0.5 x) * (1 + erf(x / sqrt 2)) ), evaluated in fp32 in that order with a
              correctly rounded erf.
 
+``head_rmsnorm``  flower/models/base.py:341-357 (HeadRMSNorm, the QK-norm), per row of D:
+             h = dtype( x * (1 / sqrt(mean(x^2) + eps)) ), fp32 maths.
+``rope``     base.py:478-483 with rotate_half (:465-469), tables given ([T, D], already in the
+             activations' dtype): out = dtype( dtype(x * cos) + dtype(rotate_half(x) * sin) ),
+             rotate_half(x)[2i] = -x[2i+1], rotate_half(x)[2i+1] = x[2i].
+
 Pinned by tests/test_oracle_block.py against torch's CPU operators on the same bf16 inputs (a
 library routine): identical except for rare last-place differences from summation order and
 the erf implementation.
@@ -44,3 +50,31 @@ def gelu(x: np.ndarray) -> np.ndarray:
     a = (xf * F32(1.0 / math.sqrt(2.0))).astype(F32)
     e = _erf(a.astype(np.float64)).astype(F32)
     return round_bf16(((F32(0.5) * xf).astype(F32) * (F32(1.0) + e).astype(F32)).astype(F32))
+
+
+def _round_dtype(x: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return round_bf16(np.asarray(x, dtype=F32))
+    if dtype == "f32":
+        return np.asarray(x, dtype=F32)
+    raise ValueError(dtype)
+
+
+def head_rmsnorm(x: np.ndarray, eps: float = 1e-6, dtype: str = "bf16") -> np.ndarray:
+    """x [..., D] (values of ``dtype`` as fp32) -> HeadRMSNorm(x) as fp32 values of ``dtype``."""
+    xf = np.asarray(x, dtype=F32)
+    ms = np.mean(xf * xf, axis=-1, keepdims=True, dtype=F32)
+    r = (F32(1.0) / np.sqrt(ms + F32(eps), dtype=F32)).astype(F32)
+    return _round_dtype((xf * r).astype(F32), dtype)
+
+
+def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """x [..., T, D], cos / sin [T, D] (values of ``dtype``) -> x * cos + rotate_half(x) * sin with
+    every product and the sum rounded to ``dtype``."""
+    xf = np.asarray(x, dtype=F32)
+    rot = np.empty_like(xf)
+    rot[..., 0::2] = -xf[..., 1::2]
+    rot[..., 1::2] = xf[..., 0::2]
+    a = _round_dtype(xf * np.asarray(cos, F32), dtype)
+    b = _round_dtype(rot * np.asarray(sin, F32), dtype)
+    return _round_dtype(a + b, dtype)

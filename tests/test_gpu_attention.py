@@ -197,3 +197,64 @@ def test_attention_with_producer_amax_is_identical():
     assert torch.equal(plain, given_f)
     with pytest.raises(ValueError, match="amax"):
         fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax[:5])
+
+
+def _two_pass(q, k, v, W, gran):
+    """The operator as two explicit passes: flw_quant_qkv_e4m3 (Q, K, V codes) then
+    flw_fp8_swa_fwd on those codes -- the path before Q was quantised on load."""
+    from flower_amd import _lib as L
+    lib = L.load()
+    B, H, T, D = q.shape
+    G = {"tensor": 1, "head": H, "bh": B * H}[gran]
+    q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device="cuda")
+    k8 = torch.empty_like(q8)
+    vt = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(3 * G, dtype=torch.float32, device="cuda")
+    ws = L.workspace(3 * lib.flw_quant_workspace_bytes(B, H, T, D), q.device)
+    L.check(lib.flw_quant_qkv_e4m3(q.data_ptr(), k.data_ptr(), v.data_ptr(), L.dtype_code(q.dtype), B, H, T, D,
+                                   L.i64s(*q.stride()[:3], *k.stride()[:3], *v.stride()[:3]), L.GRANULARITY[gran],
+                                   q8.data_ptr(), k8.data_ptr(), vt.data_ptr(), sc.data_ptr(), ws.data_ptr(),
+                                   ws.numel(), L.stream_of(q)), "quant")
+    out = torch.empty((B, H, T, D), dtype=q.dtype, device="cuda")
+    s8 = L.i64s(H * T * D, T * D, D)
+    base = sc.data_ptr()
+    L.check(lib.flw_fp8_swa_fwd(q8.data_ptr(), s8, k8.data_ptr(), s8, vt.data_ptr(), base, base + 4 * G,
+                                base + 8 * G, L.GRANULARITY[gran], out.data_ptr(), L.dtype_code(q.dtype),
+                                L.i64s(*out.stride()[:3]), B, H, T, D, W, L.stream_of(q)), "swa")
+    return out
+
+
+@pytest.mark.parametrize("gran", ["tensor", "head", "bh"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_q_quantised_on_load_is_bit_identical_to_the_two_pass_path(D, dtype, gran):
+    """fp8_swa_attention_forward quantises Q inside the attention kernel (flw_quant_qkv_e4m3_deferq +
+    flw_fp8_swa_fwd_qx); with near-tie Q values (quotients within ulps of an e4m3 rounding midpoint)
+    and strided Q, its output equals the two-pass path's bit for bit."""
+    from test_oracle_quant import near_tie_input
+    from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
+    B, H, T, W = 2, 3, 333, 100
+    # heads scaled by powers of two: a head's quotients x / s are unchanged, so they stay near ties
+    qn = near_tie_input((B, T, H, D), 81) * (2.0 ** np.arange(H, dtype=np.float32))[None, None, :, None]
+    q = torch.from_numpy(qn).to(dtype).cuda().transpose(1, 2)          # (B, H, T, D) view, strided
+    k, v = (seeded((B, H, T, D), s, dtype) for s in (82, 83))
+    got = fp8_swa_attention_forward(q, k, v, W, granularity=gran)
+    want = _two_pass(q, k, v, W, gran)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_q_on_load_leaves_non_finite_groups_to_the_quantiser():
+    """A NaN in one head of Q (per-head scales): that group's codes come from the quantiser's exact
+    path, the other heads' from the attention kernel's quantise-on-load; the output equals the
+    two-pass path bit for bit (NaN rows in that head included) and an inf head too."""
+    from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
+    B, H, T, D, W = 1, 4, 256, 64, 64
+    q, k, v = (seeded((B, H, T, D), s, torch.bfloat16) for s in (84, 85, 86))
+    q[0, 1, 17, 5] = float("nan")
+    q[0, 2, 100, 0] = float("inf")
+    got = fp8_swa_attention_forward(q, k, v, W, granularity="head")
+    want = _two_pass(q, k, v, W, "head")
+    torch.cuda.synchronize()
+    assert torch.isnan(got[0, 1]).all()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
