@@ -31,6 +31,8 @@ SIGNATURES = {
     "flw_time_next_launch": (c_int, [c_void_p, c_void_p]),
     "flw_quant_workspace_bytes": (c_size_t, [c_int64] * 4),
     "flw_vtile_bytes": (c_size_t, [c_int64] * 4),
+    "flw_vtile_from_bhtd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                    c_void_p, c_void_p]),
     "flw_quant_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                                c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "flw_amax_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,

@@ -1159,6 +1159,71 @@ extern "C" int flw_diag_quotient(const float* x, int64_t n, const float* scales,
   return check_launch("flw_diag_quotient");
 }
 
+namespace flw {
+
+// ---------------------------------------------------------------- BHTD codes -> V tile layout
+//
+// For callers that hold V's e4m3 codes in plain (B, H, T, D) layout (e.g. _per_tensor_fp8's
+// output): one workgroup per (b, h) slice and 64-key tile stages the tile's rows in LDS with
+// 16-byte loads (keys past T read as zero), then every thread assembles whole 16-byte runs of the
+// tile layout (16 keys of one dim each) from LDS bytes and stores them with 16-byte stores.
+__global__ __launch_bounds__(256) void bhtd_to_vtile_kernel(const uint8_t* __restrict__ src, int64_t sb,
+                                                            int64_t sh, int64_t st, int64_t H, int64_t T,
+                                                            int D, uint8_t* __restrict__ dst) {
+  __shared__ __align__(16) uint8_t tile[64 * 128];
+  const int64_t ntiles = (T + 63) >> 6;
+  const int64_t slice = blockIdx.y, tt = blockIdx.x;
+  const int64_t b = slice / H, h = slice % H;
+  const uint8_t* base = src + b * sb + h * sh;
+  const int cpr = D / 16;                               // 16-byte chunks per key row
+  for (int i = threadIdx.x; i < 64 * cpr; i += 256) {
+    const int kk = i / cpr, c = i % cpr;
+    const int64_t key = tt * 64 + kk;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (key < T) v = *reinterpret_cast<const uint4*>(base + key * st + 16 * c);
+    *reinterpret_cast<uint4*>(tile + kk * D + 16 * c) = v;
+  }
+  __syncthreads();
+  uint8_t* out = dst + (slice * ntiles + tt) * 64 * D;
+  for (int j = threadIdx.x; j < 4 * D; j += 256) {      // 16-byte runs of the tile
+    const int dblk = j >> 7, kblk = (j >> 6) & 1, hh = (j >> 5) & 1, dd = j & 31;
+    const int d = 32 * dblk + dd;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int bi = 4 * q + e;                       // byte index inside the run
+        const int r = 8 * (bi >> 2) + 4 * hh + (bi & 3);
+        x |= (uint32_t)tile[(32 * kblk + r) * D + d] << (8 * e);
+      }
+      w[q] = x;
+    }
+    *reinterpret_cast<uint4*>(out + 16 * j) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+}  // namespace flw
+
+extern "C" int flw_vtile_from_bhtd(const uint8_t* codes, int64_t B, int64_t H, int64_t T, int64_t D,
+                                   int64_t stride_b, int64_t stride_h, int64_t stride_t, uint8_t* v_tiles,
+                                   void* stream) {
+  using namespace flw;
+  FLW_REQUIRE(codes != nullptr && v_tiles != nullptr, FLW_E_INVALID, "null pointer argument");
+  FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
+  FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
+  FLW_REQUIRE(stride_b % 16 == 0 && stride_h % 16 == 0 && stride_t % 16 == 0 && ((uintptr_t)codes & 15) == 0 &&
+              ((uintptr_t)v_tiles & 15) == 0, FLW_E_INVALID, "codes rows and v_tiles must be 16-byte aligned");
+  FLW_REQUIRE(B * H <= 65535 && (T + 63) / 64 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "B*H must be <= 65535");
+  const dim3 grid((unsigned)((T + 63) / 64), (unsigned)(B * H));
+  const Timer tm = take_timer();
+  (void)launch_args(reinterpret_cast<const void*>(&bhtd_to_vtile_kernel), grid, dim3(256), 0,
+                    static_cast<hipStream_t>(stream), tm.start, tm.stop, codes, stride_b, stride_h, stride_t, H, T,
+                    (int)D, v_tiles);
+  return check_launch("flw_vtile_from_bhtd");
+}
+
 // ---------------------------------------------------------------- allocation-free QKV quantiser
 //
 // flw_quant_qkv_e4m3 without a workspace argument, for callers that cannot allocate (code under

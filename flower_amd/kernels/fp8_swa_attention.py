@@ -297,12 +297,24 @@ def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: to
                                  out_dtype: torch.dtype = torch.bfloat16,
                                  out: torch.Tensor | None = None) -> torch.Tensor:
     """The attention kernel alone on pre-quantised operands (the ``_fp8_swa_fwd_kernel`` launch,
-    fp8_swa_attention.py:249-258): q8 / k8 uint8 (B, H, T, D) e4m3 codes, v_tiles in the
-    kernel's V layout, scales [3 * groups] (q, k, v), as ``qk_norm_rope_quant_e4m3`` returns them.
+    fp8_swa_attention.py:249-258): q8 / k8 (B, H, T, D) e4m3 codes (uint8 or float8_e4m3fn, as
+    ``_per_tensor_fp8`` returns them), V either in the kernel's tile layout (1-D, as
+    ``qk_norm_rope_quant_e4m3`` returns it) or as (B, H, T, D) codes (permuted into the tile layout
+    first, one pass), scales [3 * groups] (q, k, v) float32 on the device.
     ``out``: optional (B, H, T, D) destination of ``out_dtype`` with D contiguous."""
     lib = _lib.load()
     _lib.require_gpu(q8, k8, v_tiles, scales)
+    q8, k8, v_tiles = (t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t for t in (q8, k8, v_tiles))
     B, H, T, D = q8.shape
+    if v_tiles.dim() == 4:
+        if v_tiles.shape != q8.shape:
+            raise ValueError(f"V codes {tuple(v_tiles.shape)} do not match Q's {tuple(q8.shape)}")
+        v4 = v_tiles if v_tiles.stride(-1) == 1 and all(s % 16 == 0 for s in v_tiles.stride()[:3]) \
+            else v_tiles.contiguous()
+        v_tiles = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device=q8.device)
+        rc = lib.flw_vtile_from_bhtd(v4.data_ptr(), B, H, T, D, *v4.stride()[:3], v_tiles.data_ptr(),
+                                     _lib.stream_of(q8))
+        _lib.check(rc, "fp8_swa_attention_from_codes (V layout)")
     G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
     if scales.numel() != 3 * G or scales.dtype != torch.float32 or not scales.is_contiguous():
         raise ValueError(f"scales must be a contiguous float32 tensor of {3 * G} elements")

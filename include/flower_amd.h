@@ -87,6 +87,15 @@ int flw_quant_e4m3_amax(const void* x, int dtype, int64_t B, int64_t H, int64_t 
 /* Bytes of a FLW_LAYOUT_VTILE buffer for a (B, H, T, D) tensor: B*H*ceil(T/64)*64*D. */
 size_t flw_vtile_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
 
+/* The attention kernel reads V only in FLW_LAYOUT_VTILE (V^T operand order, written by the
+ * quantisers). For V codes held in plain (B, H, T, D) layout -- e.g. the e4m3 tensor
+ * `_per_tensor_fp8(v)` returns (flower/kernels/fp8_swa_attention.py:195-205, :244) -- this
+ * permutes them into v_tiles (flw_vtile_bytes bytes; keys past T zero), one pass over the codes.
+ * codes: element (= byte) strides, 16-byte aligned rows; D in {32, 64, 128}. */
+int flw_vtile_from_bhtd(const uint8_t* codes, int64_t B, int64_t H, int64_t T, int64_t D,
+                        int64_t stride_b, int64_t stride_h, int64_t stride_t, uint8_t* v_tiles,
+                        void* stream);
+
 /* e4m3 quantisation with amax scales, replacing `_per_tensor_fp8`
  * (flower/kernels/fp8_swa_attention.py:195-205) and extending it to per-head / per-(b,h):
  *   scale = max(amax, 1e-12) / 448  (fp32),  code = e4m3_rne(clamp(x / scale, -448, 448)).
@@ -188,7 +197,8 @@ int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, in
 /* FP8 causal sliding-window attention forward on pre-quantised operands, replacing the launch
  * of `_fp8_swa_fwd_kernel` (flower/kernels/fp8_swa_attention.py:249-258):
  *   q8, k8: (B, H, T, D) e4m3 with element strides q_strides[3] / k_strides[3] = {b, h, t};
- *   v_tiles: FLW_LAYOUT_VTILE e4m3 V;  scales: 1, H or B*H floats each (granularity);
+ *   v_tiles: FLW_LAYOUT_VTILE e4m3 V (BHTD V codes: permute them with flw_vtile_from_bhtd);
+ *   scales: 1, H or B*H floats each (granularity);
  *   out: (B, H, T, D) fp32 or bf16 with strides out_strides[3].
  * Query i attends to keys j with j <= i and i - j < window; window <= 0 gives zeros.
  * D in {32, 64, 128}. */

@@ -258,3 +258,43 @@ def test_q_on_load_leaves_non_finite_groups_to_the_quantiser():
     torch.cuda.synchronize()
     assert torch.isnan(got[0, 1]).all()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("D,T", [(64, 300), (32, 64), (128, 130)])
+def test_attention_from_bhtd_codes(D, T):
+    """V codes in plain (B, H, T, D) layout (what _per_tensor_fp8 returns) reach the kernel through
+    flw_vtile_from_bhtd: the permuted bytes equal the layout's definition (gpu_util.vtile_permute,
+    keys past T zero), and attention on _per_tensor_fp8's own codes equals the fused operator."""
+    from flower_amd import _lib as L
+    from flower_amd.kernels.fp8_swa_attention import (_per_tensor_fp8, fp8_swa_attention_forward,
+                                                      fp8_swa_attention_from_codes)
+    from gpu_util import vtile_permute
+    lib = L.load()
+    B, H, W = 2, 3, 77
+    q, k, v = (seeded((B, H, T, D), s, torch.bfloat16) for s in (87, 88, 89))
+    codes = [_per_tensor_fp8(t, "head") for t in (q, k, v)]
+    v8 = codes[2][0].view(torch.uint8)
+    vt = torch.full((lib.flw_vtile_bytes(B, H, T, D),), 0x5A, dtype=torch.uint8, device="cuda")
+    L.check(lib.flw_vtile_from_bhtd(v8.data_ptr(), B, H, T, D, *v8.stride()[:3], vt.data_ptr(),
+                                    L.stream_of(v8)), "permute")
+    scales = torch.cat([c[1] for c in codes])
+    got = fp8_swa_attention_from_codes(codes[0][0], codes[1][0], codes[2][0], scales, W, granularity="head")
+    want = fp8_swa_attention_forward(q, k, v, W, granularity="head")
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(vt), vtile_permute(to_np(v8)))
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_small_and_large_grid_kernels_agree_bit_for_bit(dtype):
+    """A slice's output does not depend on the grid it runs in (dispatch order, XCD grouping, the
+    ramp-last tile order): the same (b, h) slices run in a small grid (2 heads) and inside a large
+    one (the heads repeated 200 times, per-head scales so every copy gets the same scale) give
+    identical outputs."""
+    from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
+    q, k, v = (seeded((1, 2, 1024, 64), s, dtype) for s in (90, 91, 92))
+    small = fp8_swa_attention_forward(q, k, v, 300, granularity="head")
+    big = fp8_swa_attention_forward(*(t.repeat(1, 200, 1, 1) for t in (q, k, v)), 300, granularity="head")
+    torch.cuda.synchronize()
+    for r in (0, 57, 199):
+        assert torch.equal(big[:, 2 * r:2 * r + 2], small), r
