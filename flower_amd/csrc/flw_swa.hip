@@ -99,6 +99,13 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* lds, int off) {
   return r;
 }
 
+// A K fragment (32 keys x 64 bytes for this lane) from its swizzled region (offsets from the lane).
+__device__ __forceinline__ v8i load_kfrag(const uint8_t* lds, int region, int x0, int x1) {
+  const uint4 a = *reinterpret_cast<const uint4*>(lds + region + x0);
+  const uint4 b = *reinterpret_cast<const uint4*>(lds + region + x1);
+  return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
+}
+
 // x combined with its value in lane ^ 32 (the other half of the same query's keys).
 __device__ __forceinline__ float pair_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -219,7 +226,11 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
     const int d0 = 16 * g;
     const int blk = kk >> 5, krow = kk & 31, dc = d0 >> 6, h2 = (d0 >> 5) & 1, cc = (d0 >> 4) & 1;
     koff[j] = (uint32_t)(kk * p.kst + 16 * g);
-    ldsk[j] = (uint32_t)((((blk * NDC + dc) * 2 + cc) * 64 + krow + 32 * h2) * 16);
+    // Chunk (krow + 32 h2) of fragment region (blk, dc, cc), its index XORed with 4 (h2 + 2 cc):
+    // the 16 lanes of a ds_write_b128 phase (4 rows x 4 chunks) then fall in 16 distinct bank
+    // groups, and the fragment reads below (one region and one lane half per phase) stay a
+    // permutation of 16 consecutive chunks.
+    ldsk[j] = (uint32_t)((((blk * NDC + dc) * 2 + cc) * 64 + ((krow + 32 * h2) ^ (4 * (h2 + 2 * cc)))) * 16);
   }
   uint4 kreg[CPT], vreg[CPT];
 
@@ -270,6 +281,8 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   float m_run = -INFINITY, l_run = 0.0f;
   int pk[8] = {0, 0, 0, 0, 0, 0, 0, 0};     // e4m3 P of the current tile, packed 4 per word
 
+  // This lane's swizzled chunk offsets in the two halves (cc = 0, 1) of a K fragment region.
+  const int kx0 = (lane ^ (4 * hh)) * 16, kx1 = 1024 + (lane ^ (4 * hh + 8)) * 16;
   // S^T = K Q^T for the tile in LDS stage `buf`.
   auto qk = [&](Scores& s, int buf) __attribute__((always_inline)) {
     const uint8_t* lk = lds_k[buf];
@@ -277,8 +290,8 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
     s.s1 = v16f{};
 #pragma unroll
     for (int dc = 0; dc < NDC; ++dc) {
-      v8i k0 = load_frag(lk, ((0 * NDC + dc) * 2 * 64 + lane) * 16);
-      v8i k1 = load_frag(lk, ((1 * NDC + dc) * 2 * 64 + lane) * 16);
+      v8i k0 = load_kfrag(lk, (0 * NDC + dc) * 2 * 1024, kx0, kx1);
+      v8i k1 = load_kfrag(lk, (1 * NDC + dc) * 2 * 1024, kx0, kx1);
       if (D == 32 && hh) { k0 = v8i{0, 0, 0, 0, 0, 0, 0, 0}; k1 = k0; }
       s.s0 = mfma_32x32x64_f8(k0, qf[dc], s.s0);
       s.s1 = mfma_32x32x64_f8(k1, qf[dc], s.s1);
