@@ -46,25 +46,7 @@ struct GemmParams {
   int lds_epi;         // epilogue staged through LDS (N % 8 == 0, 16-byte aligned y / residual rows)
   uint32_t* gmax;      // optional: max |y| (fp32 bit patterns) per group of gcols output columns
   int gcols;           // power of two in [8, 256]
-  int xpm, xpn;        // XCD-block tile order (xcd_block_tile), 0 = the grouped order
 };
-
-// XCD-block tile order of the persistent GEMMs. Workgroup b runs on XCD b % 8 (dispatch is
-// round-robin over the XCDs); the tile grid is cut into xpm x xpn = 8 blocks of bm x bn tiles,
-// XCD x owns block (x % xpm, x / xpm), and its G / 8 workgroups take the block's tiles in turn
-// (m fastest). An XCD's L2 then fetches each operand row block of its rectangle once: at C2
-// (32 x 16 tiles) an 8 x 8 block, 2 MB of x and 2 MB of w per XCD, where the grouped order made
-// each XCD fetch two 4 x 8 blocks (6 MB). Returns false past the block's last tile.
-__device__ __forceinline__ bool xcd_block_tile(int xpm, int xpn, int tiles_m, int tiles_n, int item, int& tm,
-                                               int& tn) {
-  const int x = (int)(blockIdx.x & 7), per = (int)(gridDim.x >> 3);
-  const int bm = tiles_m / xpm, bn = tiles_n / xpn;
-  const int li = (int)(blockIdx.x >> 3) + item * per;
-  if (li >= bm * bn) return false;
-  tm = (x % xpm) * bm + li % bm;
-  tn = (x / xpm) * bn + li / bm;
-  return true;
-}
 
 // The epilogue value of one output: bf16(v), or bf16(residual + bf16(v)) -- x + linear(h) with
 // both terms in bf16, as the reference's residual adds compute it.
@@ -647,14 +629,6 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
 
   // Split-K: work item t = split * ntiles + tile; split s covers K stages [s nst / S, (s+1) nst / S).
   const int nst_all = p.K / kFBK;
-  if (p.xpm > 0) {                                // unsplit, 8 XCD blocks (chosen on the host)
-    int tm, tn;
-    for (int it = 0; xcd_block_tile(p.xpm, p.xpn, p.tiles_m, p.tiles_n, it, tm, tn); ++it) {
-      if constexpr (TM == 256) gemm_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, 0, nst_all, 0);
-      else gemm_tile_128(p, st0, st1, tm * TM, tn * kFBN, wave, lane, 0, nst_all, 0);
-    }
-    return;
-  }
   for (int t = L; t < ntiles * p.splits; t += G) {
     const int split = t / ntiles, tt = t % ntiles;
     const int group = tt / (kGroupM * p.tiles_n);
@@ -732,7 +706,6 @@ struct W8A16Params {
   int64_t ys;
   int M, N, K;
   int tiles_n, tiles_m;
-  int xpm, xpn;        // XCD-block tile order (xcd_block_tile), 0 = the grouped order
   int lds_epi;         // epilogue staged through LDS (N % 8 == 0, 16-byte aligned y rows)
 };
 
@@ -880,12 +853,6 @@ __global__ __launch_bounds__(kFThreads, 1) void w8a16_gemm_kernel(W8A16Params p)
   const int G = gridDim.x;
   const int L = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   const int ntiles = p.tiles_n * p.tiles_m;
-  if (p.xpm > 0) {
-    int tm, tn;
-    for (int it = 0; xcd_block_tile(p.xpm, p.xpn, p.tiles_m, p.tiles_n, it, tm, tn); ++it)
-      w8a16_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane);
-    return;
-  }
   for (int t = L; t < ntiles; t += G) {
     const int group = t / (kGroupM * p.tiles_n);
     const int first_m = group * kGroupM;
@@ -914,22 +881,6 @@ static int splitk_of(int64_t tiles, int64_t K) {
   sp = sp > 8 ? 8 : sp;
   while (sp > 1 && (K / kFBK) / sp < 4) --sp;
   return sp < 1 ? 1 : sp;
-}
-
-// The XCD-block partition (xcd_block_tile) of a tiles_m x tiles_n grid run by a grid of G
-// workgroups: the factorisation xpm x xpn = 8 whose blocks divide the grid and fetch the fewest
-// operand bytes per XCD (x_tile / w_tile: bytes of one m-tile of x / one n-tile of w), or
-// {0, 0} (the grouped order) when the grid does not split into 8 whole blocks.
-static void xcd_blocks(int tiles_m, int tiles_n, int64_t G, double x_tile, double w_tile, int& xpm, int& xpn) {
-  xpm = xpn = 0;
-  if (G % 8 != 0 || G < 8) return;
-  double best = 0;
-  for (int pm = 1; pm <= 8; pm *= 2) {
-    const int pn = 8 / pm;
-    if (tiles_m % pm || tiles_n % pn) continue;
-    const double cost = (tiles_m / pm) * x_tile + (tiles_n / pn) * w_tile;
-    if (xpm == 0 || cost < best) { best = cost; xpm = pm; xpn = pn; }
-  }
 }
 
 static size_t splitk_bytes(int64_t M, int64_t N, int64_t K) {
@@ -988,7 +939,6 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
     // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per work item.
     const int64_t items = (int64_t)p.tiles_n * p.tiles_m * p.splits;
     const int64_t grid = items < compute_units() ? items : compute_units();
-    if (p.splits == 1) xcd_blocks(p.tiles_m, p.tiles_n, grid, (double)(narrow ? 128 : 256) * K, 256.0 * K, p.xpm, p.xpn);
     if (gmax) {
       FLW_REQUIRE(p.splits == 1 && p.lds_epi, FLW_E_UNSUPPORTED,
                   "the group amax needs an unsplit GEMM with N %% 8 == 0 and 16-byte aligned rows");
@@ -1043,7 +993,6 @@ static int w8a16_mm(const uint16_t* x, int64_t M, int64_t K, int64_t xs, const u
   const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
   FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
   const int64_t grid = tiles < compute_units() ? tiles : compute_units();
-  xcd_blocks(p.tiles_m, p.tiles_n, grid, 256.0 * 2 * K, 256.0 * K, p.xpm, p.xpn);
   (void)launch_timed(reinterpret_cast<const void*>(&w8a16_gemm_kernel), dim3((unsigned)grid), dim3(kFThreads), s, p);
   return check_launch("flw_fp8_linear (W8A16)");
 }
