@@ -84,12 +84,14 @@ DATA = {
     "swa_bf16": "synthetic (seeded; bf16 q, k, v, dO ~ N(0,1))",
 }
 
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on each workload
-# (summaries under profiles/). FETCH_SIZE is scaled by 2.0: a plain 256 MiB device copy reads back
-# 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0).
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on each workload, as
+# recorded in profiles/ (swa_fwd_c3.md, swa_fwd_c4.md, fp8_gemm_c2.md, w8a16_gemm_c2.md,
+# swa_bf16_450m.md). FETCH_SIZE is scaled by 2.0: a plain 256 MiB device copy reads back
+# 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0). The attention kernel
+# reads Q in bf16 (quantised on load); "quant" is the deferred-Q quantise pair.
 TRAFFIC = {
-    "c3": {"swa_fwd": 167_986_176, "quant": 504_024_064},
-    "c4": {"swa_fwd": 167_974_912, "quant": 503_960_576},
+    "c3": {"swa_fwd": 209_484_186, "quant": 403_369_677},
+    "c4": {"swa_fwd": 209_952_154, "quant": 403_344_998},
     "c2": {"gemm": 117_834_752, "w8a16": 134_490_112},
     "swa_bf16_450m": {"bwd": 554_757_120, "fwd": 169_459_712},
 }
