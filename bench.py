@@ -35,6 +35,10 @@ its 450M model shape B2 H20 T8192 D64 W2048; roofline = the backward entry point
 --workload c2_train measures the C2 linear as an FP8 training step (forward, dgrad and wgrad GEMMs
 with their quantisers), beside torch's bf16 matmuls of the same three products.
 Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
+--issue-probe runs no workload: it measures, on one SIMD at four waves, the issue cost of each
+instruction class of the attention loop (v_fma, v_exp, v_max3, v_cvt_pk_fp8, v_mul,
+v_permlane32_swap, the FP8 MFMA) and how much of the MFMA hides under each VALU class, the
+figures the attention kernel's time is accounted with.
 """
 
 from __future__ import annotations
@@ -422,6 +426,56 @@ def cpu_baseline_gemm(x, w, budget_s=15.0, weight_only=False):
                       "; weight quantised once outside the timing, as the weight cache does"}
 
 
+# Instruction classes of flw_diag_issue_probe (bit mask) and the attention loop's count of each per
+# 64-key tile and wave (steady state, from the kernel's assembly).
+ISSUE_CLASSES = {1: "v_fma_f32", 2: "v_exp_f32", 4: "v_max3_f32", 8: "v_cvt_pk_fp8_f32", 16: "v_mul_f32",
+                 32: "v_permlane32_swap_b32", 64: "v_mfma_scale_f32_32x32x64_f8f6f4"}
+ISSUE_PROBES = [1, 2, 4, 8, 16, 32, 64, 65, 66, 68, 72, 80, 3, 67]
+
+
+def issue_probe():
+    """Per-SIMD issue cost of single instruction classes and of MFMA + VALU mixes (four waves per
+    SIMD, the attention kernel's occupancy). A probe kernel runs `iters` iterations per wave of 32
+    independent VALU instructions per class in its mask and / or 2 independent MFMAs; the cost of
+    one iteration on one SIMD is the kernel time divided by the iterations all waves of a SIMD run.
+    For a mix, `overlap` is the fraction of the smaller component hidden under the larger."""
+    from flower_amd import _lib
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = 4 * cus                              # 4 workgroups of 4 waves per CU = 4 waves per SIMD
+    iters = lib.flw_diag_issue_probe_iters()
+    out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    waves_per_simd = blocks * 4 / (4 * cus)
+    per_iter = {}
+    for mask in ISSUE_PROBES:
+        call = lambda: _lib.check(lib.flw_diag_issue_probe(mask, out.data_ptr(), out.numel(), blocks, stream), "probe")
+        call()
+        torch.cuda.synchronize()
+        ev = _events(5)
+        for a, b in ev:
+            a.record()
+            call()
+            b.record()
+        torch.cuda.synchronize()
+        ms = float(np.median([a.elapsed_time(b) for a, b in ev]))
+        ns = ms * 1e6 / (iters * waves_per_simd)
+        per_iter[mask] = ns
+        parts = [m for m in ISSUE_CLASSES if mask & m]
+        rec = {"probe": "+".join(ISSUE_CLASSES[m] for m in parts), "mask": mask, "ns_per_iter_per_simd": round(ns, 3)}
+        if len(parts) == 1:
+            n = 2 if mask == 64 else 32
+            rec["ns_per_instruction"] = round(ns / n, 4)
+            rec["cycles_at_2.4GHz"] = round(ns / n * 2.4, 2)
+        else:
+            comp = [per_iter[m] for m in parts if m in per_iter]
+            if len(comp) == len(parts):
+                rec["sum_of_parts_ns"] = round(sum(comp), 3)
+                rec["overlap"] = round((sum(comp) - ns) / min(comp), 3)
+        rec.update(iters=iters, waves_per_simd=waves_per_simd, device=torch.cuda.get_device_name(0))
+        print(json.dumps(rec), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -432,6 +486,10 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run one plain 256 MiB device copy, the reference point that scales "
                          "the HBM byte counters of a rocprofv3 --pmc run")
+    ap.add_argument("--issue-probe", action="store_true",
+                    help="instead of a workload, measure the per-SIMD issue cost of the attention "
+                         "loop's instruction classes and their overlap with the FP8 MFMA "
+                         "(flw_diag_issue_probe); prints one JSON line per probe")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU (every box here has one); it measures "
@@ -441,6 +499,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.issue_probe:
+        issue_probe()
+        return
     cfg = WORKLOADS[args.workload]
     if args.copy_probe:
         src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda").fill_(1)

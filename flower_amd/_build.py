@@ -19,7 +19,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJDIR = os.path.join(ROOT, "_build")
 LIB = os.path.join(HERE, "libflower_amd.so")
-SOURCES = ["flw_error.hip", "flw_quant.hip", "flw_swa.hip", "flw_swa_bf16.hip", "flw_gemm.hip", "flw_selftest.hip"]
+SOURCES = ["flw_error.hip", "flw_quant.hip", "flw_swa.hip", "flw_swa_bf16.hip", "flw_gemm.hip", "flw_selftest.hip",
+           "flw_diag_issue.hip"]
 ARCH = os.environ.get("FLW_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [

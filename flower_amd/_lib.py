@@ -98,6 +98,8 @@ SIGNATURES = {
                                            c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "flw_diag_cvt_e4m3": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "flw_diag_quotient": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p]),
+    "flw_diag_issue_probe": (c_int, [c_int, c_void_p, c_int64, c_int, c_void_p]),
+    "flw_diag_issue_probe_iters": (c_int, []),
 }
 
 _lib = None

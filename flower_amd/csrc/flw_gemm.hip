@@ -678,7 +678,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p) {
 // value) and the product runs on v_mfma_f32_32x32x16_bf16 (bf16 dense peak 2.5 PFLOP/s). Same
 // persistent 256 x 256 tiles, wave grid, XCD / group-M tile order and direct-to-LDS staging as
 // the FP8 kernel; a stage is 64 deep in K: a 256 x 128-byte X tile (bf16) and a 256 x 64-byte W
-// tile (e4m3), 48 KB, two stages.
+// tile (e4m3), 48 KB, in a ring of three (144 KB of LDS): the loads of stage s + 2 are issued
+// while stage s computes, so two stages of MFMA work cover the load latency, and one barrier per
+// stage both publishes stage s and retires every wave's reads of stage s - 1, whose buffer the
+// loads issued right after it refill.
 //
 // K order inside a stage. An MFMA only needs A and B to agree on which K each lane holds, so
 // k-step ks (16 deep) gives lane half h the K values 32 h + 8 ks .. +7: a lane then reads its W
@@ -692,7 +695,7 @@ constexpr int kWK = 64;                           // K per stage
 constexpr int kWXBytes = 256 * 128;               // X tile per stage (32 KB)
 constexpr int kWWBytes = 256 * 64;                // W tile per stage (16 KB)
 constexpr int kWStageBytes = kWXBytes + kWWBytes;
-constexpr int kWStageAlloc = 65536;               // >= kWStageBytes, and half of a staged bf16 tile
+constexpr int kWStages = 3;                       // LDS ring; the staged epilogue reuses its first 128 KB
 
 typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
 
@@ -724,8 +727,8 @@ __device__ __forceinline__ v8bf_t widen8(uint32_t lo, uint32_t hi) {
   return v8bf_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
-__device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, uint8_t* st1, int m0,
-                                           int n0, int wave, int lane) {
+__device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* lds, int m0, int n0, int wave,
+                                           int lane) {
   const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
   // Direct-to-LDS loads: wave w fills X rows 32 w .. 32 w + 31 (four instructions of 8 rows x
   // 128 bytes) and W rows 32 w .. 32 w + 31 (two instructions of 16 rows x 64 bytes).
@@ -744,7 +747,8 @@ __device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, u
     const int grow = min(n0 + r, p.N - 1);
     woff[t] = (uint32_t)grow * (uint32_t)p.K + 16u * (uint32_t)c;
   }
-  auto issue = [&](uint8_t* stage, int s) __attribute__((always_inline)) {
+  auto issue = [&](int buf, int s) __attribute__((always_inline)) {
+    uint8_t* stage = lds + buf * kWStageBytes;
     const uint32_t kx = (uint32_t)s * kWK * 2, kw = (uint32_t)s * kWK;
     const uint32_t lx = (uint32_t)(uintptr_t)(lds_u8_t*)(stage + 32 * wave * 128);
     const uint32_t lw = (uint32_t)(uintptr_t)(lds_u8_t*)(stage + kWXBytes + 32 * wave * 64);
@@ -766,15 +770,16 @@ __device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, u
 
   const int nst = p.K / kWK;
   const int h = lane >> 5;
-  issue(st0, 0);
-  auto step = [&](int s, const uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
-    if (s + 1 < nst) {
-      issue(nxt, s + 1);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(6));   // this wave's loads of stage s landed
-    } else {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    }
-    lds_barrier();                                // ... and every wave's
+  issue(0, 0);
+  if (nst > 1) issue(1, 1);
+  auto step = [&](int s, auto bufc) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(bufc)::value;
+    // This wave's loads of stage s landed (only stage s + 1's six are issued after them) ...
+    if (s + 1 < nst) __builtin_amdgcn_s_waitcnt(vmcnt_imm(6));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    lds_barrier();                                // ... and every wave's; stage s - 1 is retired
+    if (s + 2 < nst) issue((BUF + 2) % kWStages, s + 2);
+    const uint8_t* cur = lds + BUF * kWStageBytes;
     // X fragments for both m blocks and all four k-steps: chunk 4 h + ks of row 32 (2 wm + j) + lane % 32.
     v8bf_t b[2][4];
 #pragma unroll
@@ -797,17 +802,21 @@ __device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, u
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], b[j][ks], acc[i][j], 0, 0, 0);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): reads of `cur` done
-    lds_barrier();
+    __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): this wave's reads of `cur` done
   };
-  for (int s = 0; s < nst; s += 2) {
-    step(s, st0, st1);
-    if (s + 1 < nst) step(s + 1, st1, st0);
+  for (int s = 0; s < nst; s += kWStages) {
+    step(s, std::integral_constant<int, 0>{});
+    if (s + 1 < nst) step(s + 1, std::integral_constant<int, 1>{});
+    if (s + 2 < nst) step(s + 2, std::integral_constant<int, 2>{});
   }
+  // The epilogue (and the next tile's first loads) overwrite the ring: every wave's reads of the
+  // last stage are done.
+  lds_barrier();
 
   if (p.lds_epi) {
     const float one[2] = {1.0f, 1.0f};
-    staged_epilogue(acc, one, p.sw, p.sw_step, p.y, p.ys, nullptr, 0, p.M, p.N, st0, st1, m0, n0, wave, lane);
+    staged_epilogue(acc, one, p.sw, p.sw_step, p.y, p.ys, nullptr, 0, p.M, p.N, lds, lds + 65536, m0, n0, wave,
+                    lane);
     return;
   }
   // Epilogue: lane owns m = m0 + 64 wm + 32 j + lane % 32, n = n0 + 128 wn + 32 i + 8 g + 4 h + 0..3
@@ -845,9 +854,9 @@ __device__ __forceinline__ void w8a16_tile(const W8A16Params& p, uint8_t* st0, u
 }
 
 __global__ __launch_bounds__(kFThreads, 1) void w8a16_gemm_kernel(W8A16Params p) {
-  // 64 KB each (a stage uses 48 KB): the staged epilogue needs 2 x 64 KB.
-  __shared__ __align__(16) uint8_t st0[kWStageAlloc];
-  __shared__ __align__(16) uint8_t st1[kWStageAlloc];
+  // Three 48 KB stages; the staged epilogue uses the first 2 x 64 KB.
+  __shared__ __align__(16) uint8_t lds[kWStages * kWStageBytes];
+  static_assert(kWStages * kWStageBytes >= 2 * 65536, "the staged epilogue needs 128 KB");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x;
@@ -859,7 +868,7 @@ __global__ __launch_bounds__(kFThreads, 1) void w8a16_gemm_kernel(W8A16Params p)
     const int gm = min(p.tiles_m - first_m, kGroupM);
     const int tm = first_m + (t % (kGroupM * p.tiles_n)) % gm;
     const int tn = (t % (kGroupM * p.tiles_n)) / gm;
-    w8a16_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane);
+    w8a16_tile(p, lds, tm * kFBM, tn * kFBN, wave, lane);
   }
 }
 

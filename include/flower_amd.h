@@ -353,6 +353,16 @@ int flw_diag_cvt_e4m3(const float* x, uint8_t* out, int64_t n, int hardware, voi
 int flw_diag_quotient(const float* x, int64_t n, const float* scales, int64_t n_scales,
                       uint32_t* out, int mode, void* stream);
 
+/* No counterpart in the reference. Issue-cost probe of the attention loop's instruction classes:
+ * one kernel of `blocks` 256-thread workgroups in which every wave runs
+ * flw_diag_issue_probe_iters() iterations of 32 independent instructions of each VALU class in
+ * `mask` (1 v_fma_f32, 2 v_exp_f32, 4 v_max3_f32, 8 v_cvt_pk_fp8_f32, 16 v_mul_f32,
+ * 32 v_permlane32_swap_b32) and / or 2 independent v_mfma_scale_f32_32x32x64_f8f6f4 (64).
+ * Supported masks: 1, 2, 4, 8, 16, 32, 64, 65, 66, 68, 72, 80, 3, 67. out: blocks * 256 floats
+ * (a checksum per thread). Armable with flw_time_next_launch. */
+int flw_diag_issue_probe(int mask, float* out, int64_t out_count, int blocks, void* stream);
+int flw_diag_issue_probe_iters(void);
+
 #ifdef __cplusplus
 }
 #endif
