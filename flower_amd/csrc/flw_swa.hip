@@ -10,12 +10,14 @@
 // e4m3 in registers (v_cvt_pk_fp8_f32) straight into the B operand of O^T += V^T P^T (D/32 more
 // MFMAs, accumulators kept in VGPRs so the rescale is one multiply per element).
 //
-// The softmax is VALU-bound (per score: one FMA, one v_exp_f32 at half rate, half a max3, half a
-// convert, one add; per tile D/64 rescale multiplies per score) while the MFMA work per tile is
-// about a third of that. The MFMA work of one wave runs under the VALU work of the other waves
-// of its SIMD (four workgroups per CU at D <= 64: 118 VGPRs, 24 KB of LDS each); issuing
-// the next tile's QK^T before the current softmax was measured slower (its extra accumulators
-// cost a wave per SIMD).
+// The softmax is VALU-bound. Per score: one FMA, one v_exp_f32 and half a v_cvt_pk_fp8_f32
+// (each of those two costs about three full-rate issue slots on gfx950), half a max3, one add,
+// and D/64 rescale multiplies per tile; the MFMA work of a tile is about a third of its VALU
+// time. Inside a wave every step depends on the previous one, so the MFMA time hides only under
+// the other waves of the SIMD (four workgroups per CU at D <= 64: 120 VGPRs, 24 KB of LDS each);
+// a wave raises its priority for its softmax and drops it to issue its MFMAs, which keeps the
+// VALU fed. Software-pipelining the tiles inside a wave (the next tile's QK^T and the previous
+// tile's PV issued between the current tile's exponentials) was measured slower.
 //
 // K tiles are staged in LDS in MFMA-fragment order (a permutation of 16-byte chunks of the
 // row-major tile); V arrives already in that order from the quantiser (FLW_LAYOUT_VTILE), so every
@@ -123,8 +125,8 @@ struct Scores {
   v16f s0, s1;
 };
 
-// At D <= 64 the kernel takes 118 VGPRs, so four workgroups (16 waves) share a CU; the launch bound
-// only asks for three. D = 128 asks for two (its O^T needs 64 VGPRs more).
+// At D <= 64 the kernel takes 120 VGPRs (D = 32: 110), so four workgroups (16 waves) share a CU;
+// the launch bound only asks for three. D = 128 asks for two (its O^T needs 64 VGPRs more).
 template <int D, typename OutT>
 __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParams p) {
   constexpr int NDC = D >= 64 ? D / 64 : 1;   // 64-deep K chunks of the QK^T product
@@ -337,6 +339,9 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   // p = exp(S - m_new), alpha = exp(m - m_new), l = l alpha + sum p, O = O alpha + e4m3(448 p) V),
   // in base 2 with the scale folded in, then O^T += V^T P^T.
   auto softmax_pv = [&](Scores& s, int n0, int buf) __attribute__((always_inline)) {
+    // A wave in its softmax issues ahead of the waves about to issue MFMAs (s_setprio 1 until
+    // its PV), so the VALU stays fed and the matrix core works through the others' MFMAs.
+    __builtin_amdgcn_s_setprio(1);
     // Keys past T only meet queries past T, whose rows are not stored.
     mask_block(s.s0, 0, n0);
     mask_block(s.s1, 1, n0);
@@ -379,6 +384,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
     l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
     const v8i pf = v8i{pk[0], pk[1], pk[2], pk[3], pk[4], pk[5], pk[6], pk[7]};
     const uint8_t* lv = lds_v[buf];
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const v8i vf = load_frag(lv, (db * 2 * 64 + lane) * 16);
