@@ -35,6 +35,8 @@ its 450M model shape B2 H20 T8192 D64 W2048; roofline = the backward entry point
 --workload c2_train measures the C2 linear as an FP8 training step (forward, dgrad and wgrad GEMMs
 with their quantisers), beside torch's bf16 matmuls of the same three products.
 Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
+--library-gemm-reference runs no workload: it times hipBLASLt (through torch) at the GEMM shapes,
+the reference point for the library's own GEMMs.
 --issue-probe runs no workload: it measures, on one SIMD at four waves, the issue cost of each
 instruction class of the attention loop (v_fma, v_exp, v_max3, v_cvt_pk_fp8, v_mul,
 v_permlane32_swap, the FP8 MFMA) and how much of the MFMA hides under each VALU class, the
@@ -433,6 +435,46 @@ ISSUE_CLASSES = {1: "v_fma_f32", 2: "v_exp_f32", 4: "v_max3_f32", 8: "v_cvt_pk_f
 ISSUE_PROBES = [1, 2, 4, 8, 16, 32, 64, 65, 66, 68, 72, 80, 3, 67]
 
 
+LIBRARY_GEMM_SHAPES = {"c2": (8192, 4096, 1024), "c5_qkv": (32768, 3072, 1024), "c5_ff1": (32768, 4096, 1024),
+                       "c5_ff2": (32768, 1024, 4096), "c5_o": (32768, 1024, 1024)}
+
+
+def library_gemm_reference(steps=50):
+    """The vendor GEMM at this build's GEMM shapes (M, N, K): torch's bf16 matmul and FP8
+    torch._scaled_mm (e4m3 operands, bf16 out) with per-row x per-column scales (the A8W8 recipe's
+    scaling) and with per-tensor scales, all on hipBLASLt. Timed with events over `steps` calls
+    after 5 warm-up calls. A reference point only: no epilogue (residual, amax) is included."""
+    for name, (M, N, K) in LIBRARY_GEMM_SHAPES.items():
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16, generator=g)
+        b = torch.randn(N, K, device="cuda", dtype=torch.bfloat16, generator=g)
+        a8, b8 = a.to(torch.float8_e4m3fn), b.to(torch.float8_e4m3fn)
+        sa, sb = torch.ones(M, 1, device="cuda"), torch.ones(1, N, device="cuda")
+        one = torch.ones((), device="cuda")
+        calls = {"bf16_matmul": lambda: a @ b.t(),
+                 "fp8_scaled_mm_rowwise": lambda: torch._scaled_mm(a8, b8.t(), scale_a=sa, scale_b=sb,
+                                                                   out_dtype=torch.bfloat16),
+                 "fp8_scaled_mm_tensorwise": lambda: torch._scaled_mm(a8, b8.t(), scale_a=one, scale_b=one,
+                                                                      out_dtype=torch.bfloat16)}
+        rec = {"shape": name, "M": M, "N": N, "K": K}
+        for key, fn in calls.items():
+            try:
+                for _ in range(5):
+                    fn()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(steps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) / steps * 1e3
+                rec[key] = {"us": round(us, 2), "tflops": round(2 * M * N * K / us / 1e6, 1)}
+            except RuntimeError as e:                 # a recipe this torch build lacks
+                rec[key] = {"error": str(e)[:120]}
+        print(json.dumps(rec), flush=True)
+
+
 def issue_probe():
     """Per-SIMD issue cost of single instruction classes and of MFMA + VALU mixes (four waves per
     SIMD, the attention kernel's occupancy). A probe kernel runs `iters` iterations per wave of 32
@@ -486,6 +528,11 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run one plain 256 MiB device copy, the reference point that scales "
                          "the HBM byte counters of a rocprofv3 --pmc run")
+    ap.add_argument("--library-gemm-reference", action="store_true",
+                    help="instead of a workload, time the vendor GEMM (hipBLASLt through torch: bf16 "
+                         "matmul, FP8 _scaled_mm with per-row x per-column and per-tensor scales) at "
+                         "the C2 shape and C5's four linear shapes, the reference point for the "
+                         "library's own GEMMs; prints one JSON line per shape")
     ap.add_argument("--issue-probe", action="store_true",
                     help="instead of a workload, measure the per-SIMD issue cost of the attention "
                          "loop's instruction classes and their overlap with the FP8 MFMA "
@@ -501,6 +548,9 @@ def main():
         sys.exit(1)
     if args.issue_probe:
         issue_probe()
+        return
+    if args.library_gemm_reference:
+        library_gemm_reference()
         return
     cfg = WORKLOADS[args.workload]
     if args.copy_probe:
