@@ -145,7 +145,10 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
   const int nwg = p.nwg;
   int L = (int)__builtin_amdgcn_workgroup_id_x();
-  if ((nwg & 7) == 0) L = (L & 7) * (nwg >> 3) + (L >> 3);   // contiguous work per XCD
+  // Contiguous work per XCD when the slices split evenly over the 8 XCDs (each XCD then takes
+  // whole slices); otherwise the workgroups stay dealt round-robin over the XCDs, so every XCD
+  // gets an even share of the long and the short work items of the order below.
+  if (p.group_slices * 8 * p.nM == nwg) L = (L & 7) * (nwg >> 3) + (L >> 3);
   // Inside a group of slices (one XCD's share), the full-band query tiles come first, slice by
   // slice (consecutive tiles share K / V tiles in that XCD's L2), then the causal-ramp tiles in
   // decreasing length, so the short work items fill the end of the grid as the long ones drain.

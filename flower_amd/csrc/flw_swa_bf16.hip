@@ -57,6 +57,8 @@ struct SwaB16Params {
   float* lse;             // [B, H, T]
   float* delta;           // [B, H, T]
   int H, T, W, nblk, nwg; // nblk: 128-row blocks per (b, h)
+  int ramp;               // blocks per slice whose band is cut short by the sequence's start / end
+  int group_slices;       // slices per dispatch group (one XCD's share when it is whole slices)
   float sm_scale;
   int64_t rows;           // B * H * T (delta kernel)
 };
@@ -177,10 +179,31 @@ __device__ __forceinline__ void wait_all_loads() {
 }
 
 // XCD-contiguous work numbering (as in the FP8 kernel).
-__device__ __forceinline__ int xcd_id(int nwg) {
+// Contiguous work per XCD when the slices split evenly over the 8 XCDs; otherwise round-robin
+// over the XCDs, so each XCD gets an even share of the long and short work items.
+__device__ __forceinline__ int xcd_id(const SwaB16Params& p) {
   int L = (int)blockIdx.x;
-  if ((nwg & 7) == 0) L = (L & 7) * (nwg >> 3) + (L >> 3);
+  if (p.group_slices * 8 * p.nblk == p.nwg) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
   return L;
+}
+
+// (slice, 128-row block) of this workgroup. Inside one XCD's group of slices the blocks with a
+// full-length band come first, slice by slice (consecutive blocks share K / V or Q / dO tiles in
+// that XCD's L2), then the `ramp` short-band blocks in decreasing band length, so the short work
+// items fill the grid's drain. Query-block kernels: the short blocks are a slice's first ones (their
+// band starts at key 0); the key-block kernel: its last ones (their band ends at query T - 1).
+__device__ __forceinline__ void band_order(const SwaB16Params& p, bool ramp_at_end, int& bh, int& blk) {
+  const int L = xcd_id(p);
+  const int gs = p.group_slices, R = p.ramp, nfull = p.nblk - R;
+  const int gi = L / (gs * p.nblk), i = L % (gs * p.nblk);
+  if (i < gs * nfull) {
+    bh = gi * gs + i / nfull;
+    blk = (ramp_at_end ? 0 : R) + i % nfull;
+  } else {
+    const int j = i - gs * nfull, r = j / gs;     // r-th longest short-band block
+    bh = gi * gs + j % gs;
+    blk = ramp_at_end ? nfull + r : R - 1 - r;
+  }
 }
 
 // ---------------------------------------------------------------- forward
@@ -193,8 +216,8 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
   __shared__ __align__(16) uint8_t lk[2][NAT];
   __shared__ __align__(16) uint8_t lv[2][NAT];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, qc = lane & 31;
-  const int L = xcd_id(p.nwg);
-  const int bh = L / p.nblk, mt = L % p.nblk;
+  int bh, mt;
+  band_order(p, false, bh, mt);
   const int T = p.T, W = p.W;
   const int m0 = mt * 128, q0 = m0 + 32 * wave;
   const int64_t slice = (int64_t)bh * T * D;
@@ -348,8 +371,8 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
   __shared__ __align__(16) uint8_t ldo[2][NAT];    // dO tile: A operand of dP, read transposed for dV
   __shared__ __align__(16) float lstat[2][2][64];  // -L log2(e) and Delta of the tile's queries
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, kc = lane & 31;
-  const int L = xcd_id(p.nwg);
-  const int bh = L / p.nblk, nt0 = L % p.nblk;
+  int bh, nt0;
+  band_order(p, true, bh, nt0);
   const int T = p.T, W = p.W;
   const int k0w = nt0 * 128, k0 = k0w + 32 * wave;     // this wave's 32 keys
   const int64_t slice = (int64_t)bh * T * D;
@@ -492,8 +515,8 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 3) void swa_bf16_dq_kernel(SwaB
   __shared__ __align__(16) uint8_t lk[2][NAT];     // K tile: A operand of S^T, read transposed for dQ^T
   __shared__ __align__(16) uint8_t lv[2][NAT];     // V tile, natural (A operand of dP^T)
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, qc = lane & 31;
-  const int L = xcd_id(p.nwg);
-  const int bh = L / p.nblk, mt = L % p.nblk;
+  int bh, mt;
+  band_order(p, false, bh, mt);
   const int T = p.T, W = p.W;
   const int m0 = mt * 128, q0 = m0 + 32 * wave;
   const int64_t slice = (int64_t)bh * T * D;
@@ -608,6 +631,20 @@ static int check_b16(const void* a, const void* b, const void* c, int64_t B, int
   return FLW_OK;
 }
 
+// Query blocks whose band starts at key 0 (shorter than W + 127 keys): the first ceil(W / 128).
+static int query_ramp(const SwaB16Params& p) {
+  return p.W > 0 ? std::min(p.nblk, (p.W - 1) / 128 + 1) : 0;
+}
+// Key blocks whose band of queries ends at T - 1 before its full W + 127: the last ones.
+static int key_ramp(const SwaB16Params& p) {
+  const int64_t span = (int64_t)p.T - p.W - 127;
+  const int nfull = span < 0 ? 0 : std::min<int64_t>(p.nblk, span / 128 + 1);
+  return p.nblk - nfull;
+}
+static int group_slices(int64_t slices, int nwg) {
+  return (slices % 8 == 0 && (nwg & 7) == 0) ? (int)(slices / 8) : (int)slices;
+}
+
 }  // namespace flw
 
 using namespace flw;
@@ -623,6 +660,8 @@ extern "C" int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int
   p.out = static_cast<uint16_t*>(out); p.lse = lse;
   p.H = (int)H; p.T = (int)T; p.W = (int)(window < T ? window : T);
   p.nblk = (int)((T + 127) / 128); p.nwg = (int)(B * H * p.nblk);
+  p.ramp = query_ramp(p);
+  p.group_slices = group_slices(B * H, p.nwg);
   p.sm_scale = 1.0f / sqrtf((float)D);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)p.nwg);
@@ -661,10 +700,13 @@ extern "C" int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, con
   const int64_t threads = p.rows * (D / 8);
   const dim3 dgrid((unsigned)((threads + 255) / 256));
   const dim3 grid((unsigned)p.nwg);
+  p.group_slices = group_slices(B * H, p.nwg);
   SwaB16Params pk = p;
   pk.out2 = static_cast<uint16_t*>(dk); pk.out3 = static_cast<uint16_t*>(dv);
+  pk.ramp = key_ramp(p);
   SwaB16Params pq = p;
   pq.out = static_cast<uint16_t*>(dq);
+  pq.ramp = query_ramp(p);
   const void* kd = D == 32 ? reinterpret_cast<const void*>(&swa_bf16_delta_kernel<32>)
                  : D == 64 ? reinterpret_cast<const void*>(&swa_bf16_delta_kernel<64>)
                            : reinterpret_cast<const void*>(&swa_bf16_delta_kernel<128>);
