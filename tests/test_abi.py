@@ -136,3 +136,18 @@ def test_limits_and_empty_shapes_are_refused_on_the_host():
     # (M * K = 2^32 here) are refused instead of returning an unwritten amax
     rc = lib.flw_fp8_scaled_mm_group_amax(P, 1 << 22, 1024, P, 256, P, 1 << 22, P, 256, P, 256, 64, P, None)
     assert rc == 2 and b"group amax" in lib.flw_last_error()
+
+
+@fake_pointers
+def test_issue_probe_refuses_bad_arguments_on_the_host():
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = _lib.load()
+    assert lib.flw_diag_issue_probe_iters() > 0
+    fake = 1 << 20
+    assert lib.flw_diag_issue_probe(1, None, 256, 1, None) == 1           # null out
+    assert lib.flw_diag_issue_probe(1, fake, 255, 1, None) == 1           # out too small
+    assert lib.flw_diag_issue_probe(1, fake, 256, 0, None) == 1           # no workgroups
+    assert lib.flw_diag_issue_probe(5, fake, 256, 1, None) == 1           # no such probe
+    assert b"no issue probe" in lib.flw_last_error()
