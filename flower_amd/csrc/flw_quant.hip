@@ -26,8 +26,10 @@
 namespace flw {
 
 constexpr int kThreads = 256;
-constexpr int64_t kRowsPerChunk = 256;   // multiple of 64: VTILE chunks hold whole key tiles
-constexpr int kUnroll = 2;               // 16-byte loads in flight per thread (swept: 2..16)
+// Chunk height and loads in flight per thread, swept together (64-1024 rows x 1-16 loads): 128 x 1
+// ties 256 x 2 on the large shapes and is faster on small ones (more workgroups to spread).
+constexpr int64_t kRowsPerChunk = 128;   // multiple of 64: VTILE chunks hold whole key tiles
+constexpr int kUnroll = 1;               // 16-byte loads in flight per thread per iteration
 
 struct QTensor {
   const void* x;
@@ -1280,7 +1282,7 @@ extern "C" int flw_quant_qkv_e4m3_noalloc(const void* q, const void* k, const vo
   FLW_REQUIRE(B * H <= 65535 && T < ((int64_t)1 << 40), FLW_E_UNSUPPORTED, "B*H must be <= 65535");
   const size_t need = 3 * partial_bytes(B, H, T);
   FLW_REQUIRE(need <= kNoAllocScratchBytes, FLW_E_UNSUPPORTED,
-              "allocation-free quantiser: 3 * B * H * ceil(T / 256) amax partials must fit its %zu-byte "
+              "allocation-free quantiser: 3 * B * H * ceil(T / 128) amax partials must fit its %zu-byte "
               "scratch (this shape needs %zu bytes); use flw_quant_qkv_e4m3 with a workspace",
               kNoAllocScratchBytes, need);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -150,7 +150,7 @@ int flw_qk_norm_rope_quant_e4m3(const void* q, const void* k, const void* v, int
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): the amax partials live in a library-owned device array of
  * flw_noalloc_scratch_bytes() bytes (1 MiB) per GPU, held until the process ends; the call itself
- * allocates nothing. Limit: 3 * B * H * ceil(T / 256) * 4 bytes of partials must fit the array
+ * allocates nothing. Limit: 3 * B * H * ceil(T / 128) * 4 bytes of partials must fit the array
  * (FLW_E_UNSUPPORTED otherwise). Outputs and their contract are those of flw_quant_qkv_e4m3. Calls
  * that overlap on one GPU (e.g. on two streams) share the array and race; serialise them. */
 size_t flw_noalloc_scratch_bytes(void);

@@ -54,7 +54,7 @@ def test_host_only_calls_work_without_a_gpu():
     lib = _lib.load()
     assert lib.flw_abi_version() == 1
     assert lib.flw_vtile_bytes(2, 3, 100, 64) == 2 * 3 * 128 * 64
-    assert lib.flw_quant_workspace_bytes(1, 1, 1000, 64) == 4 * 4          # 4 chunks of 256 rows
+    assert lib.flw_quant_workspace_bytes(1, 1, 1000, 64) == 8 * 4          # 8 chunks of 128 rows
     assert lib.flw_fp8_swa_workspace_bytes(4, 16, 8192, 64) >= 3 * 4 * 16 * 8192 * 64
     # argument validation happens on the host, before any device work
     rc = lib.flw_fp8_swa_fwd(None, None, None, None, None, None, None, None, 0, None, 0, None,

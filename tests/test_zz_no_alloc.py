@@ -47,7 +47,7 @@ def _run(noalloc, q, k, v, gran):
 
 @pytest.mark.parametrize("gran", ["tensor", "head", "bh"])
 def test_noalloc_quantiser_equals_the_workspace_entry_point(gran):
-    # First a large call (B2 H8 T4096: 384 partials), then a smaller one (B1 H3 T300: 18 partials)
+    # First a large call (B2 H8 T4096: 1,536 partials), then a smaller one (B1 H3 T300: 27 partials)
     # whose partials occupy the start of the same scratch array.
     for shape, seed in (((2, 8, 4096, 64), 1), ((1, 3, 300, 64), 2)):
         q, k, v = _inputs(*shape, seed)
@@ -65,7 +65,7 @@ def test_noalloc_quantiser_refuses_shapes_beyond_its_scratch():
     lib = L.load()
     cap = lib.flw_noalloc_scratch_bytes()
     assert cap == 1 << 20
-    # 3 tensors x B*H*ceil(T/256) partials x 4 bytes: B1 H64 T1,048,576 needs 3 MiB. Refused on the
+    # 3 tensors x B*H*ceil(T/128) partials x 4 bytes: B1 H64 T1,048,576 needs 6 MiB. Refused on the
     # host before any launch; the real (small) buffers are never touched.
     x = torch.zeros(16, dtype=torch.bfloat16, device="cuda")
     o = torch.zeros(16, dtype=torch.uint8, device="cuda")
