@@ -842,8 +842,8 @@ int quant_bhtd_n(int n, const void* const* xs, int dtype, int64_t B, int64_t H, 
     }
   }
   if (q_rcp_deferred != nullptr) {
-    FLW_REQUIRE(amax_given == nullptr && xf == nullptr && layouts[0] == FLW_LAYOUT_BHTD, FLW_E_INVALID,
-                "deferred Q codes need the amax pass, no transform and BHTD codes");
+    FLW_REQUIRE(xf == nullptr && layouts[0] == FLW_LAYOUT_BHTD, FLW_E_INVALID,
+                "deferred Q codes need no transform and BHTD codes");
     p.t[0].defer = 1;
     p.t[0].rcp_out = q_rcp_deferred;
   }

@@ -72,6 +72,10 @@ struct SwaParams {
   const void* qx;
   int64_t xsb, xsh, xst;
   const float* qr;
+  // Optional with qx: the caller-given |q| maximum of each scale group (fp32 bit patterns) that
+  // the scale was derived from. A lane holding a larger |q| (a stale or wrong maximum) takes the
+  // exact path for its values: IEEE division, clamp to +-448, then the cast.
+  const uint32_t* qamax;
 };
 
 template <typename OutT> struct Store4;
@@ -106,6 +110,14 @@ __device__ __forceinline__ v8i load_kfrag(const uint8_t* lds, int region, int x0
   const uint4 a = *reinterpret_cast<const uint4*>(lds + region + x0);
   const uint4 b = *reinterpret_cast<const uint4*>(lds + region + x1);
   return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
+}
+
+// clamp(y, -448, 448) on the bit pattern (this file is built without NaN semantics, so a float
+// comparison could not be trusted to keep a NaN): |y| above 448, inf included, becomes +-448;
+// NaN is kept.
+__device__ __forceinline__ float clamp448_bits(float y) {
+  const uint32_t u = __float_as_uint(y), a = u & 0x7FFFFFFFu;
+  return a > 0x43E00000u && a <= 0x7F800000u ? __uint_as_float((u & 0x80000000u) | 0x43E00000u) : y;
 }
 
 // x combined with its value in lane ^ 32 (the other half of the same query's keys).
@@ -196,13 +208,33 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
       float f[32];
 #pragma unroll
       for (int j = 0; j < 32 / QV::N; ++j) QV::load(qx + 64 * dc + 32 * hh + j * QV::N, f + j * QV::N);
+      bool exact = false;
+      if (p.qamax != nullptr) {                     // values beyond the given maximum?
+        const uint32_t g = p.qamax[si];
+        const uint32_t lim = (int32_t)g > 0 ? g : 0u;   // a given maximum <= 0 admits only zeros
+        uint32_t m = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        int c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * j], q_s, qrcp),
-                                                div_by_scale(f[4 * j + 1], q_s, qrcp), 0, false);
-        c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * j + 2], q_s, qrcp),
-                                            div_by_scale(f[4 * j + 3], q_s, qrcp), c, true);
-        qf[dc][j] = c;
+        for (int j = 0; j < 32; ++j) { const uint32_t a = abs_bits(f[j]); m = m > a ? m : a; }
+        exact = m > lim;
+      }
+      if (!exact) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          int c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * j], q_s, qrcp),
+                                                  div_by_scale(f[4 * j + 1], q_s, qrcp), 0, false);
+          c = __builtin_amdgcn_cvt_pk_fp8_f32(div_by_scale(f[4 * j + 2], q_s, qrcp),
+                                              div_by_scale(f[4 * j + 3], q_s, qrcp), c, true);
+          qf[dc][j] = c;
+        }
+      } else {                                      // rare: the reference's clamp, then the cast
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          uint32_t c = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            c |= (f32_to_e4m3(clamp448_bits(f[4 * j + e] / q_s)) & 0xFFu) << (8 * e);   // IEEE division
+          qf[dc][j] = (int)c;
+        }
       }
     }
   } else {
@@ -456,7 +488,7 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
                    const uint8_t* vt, const float* qs, const float* ks, const float* vs, int gran,
                    void* out, int out_dtype, const int64_t* ost, int64_t B, int64_t H, int64_t T,
                    int64_t D, int64_t window, hipStream_t stream, Timer tm, const void* qx = nullptr,
-                   const int64_t* xst = nullptr, const float* qr = nullptr) {
+                   const int64_t* xst = nullptr, const float* qr = nullptr, const uint32_t* qamax = nullptr) {
   FLW_REQUIRE(q8 && k8 && vt && qs && ks && vs && out && qst && kst && ost, FLW_E_INVALID, "null pointer argument");
   if (qx != nullptr) {
     const int64_t vec = out_dtype == FLW_F32 ? 4 : 8;
@@ -494,6 +526,7 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.nwg = (int)(B * H * nM);
   p.qx = qx;
   p.qr = qr;
+  p.qamax = qx != nullptr ? qamax : nullptr;
   if (qx != nullptr) { p.xsb = xst[0]; p.xsh = xst[1]; p.xst = xst[2]; }
   p.ramp = W > 0 ? (int)std::min<int64_t>(nM, (W - 1) / kBM + 1) : 0;
   p.group_slices = ((B * H) % 8 == 0 && (p.nwg & 7) == 0) ? (int)(B * H / 8) : (int)(B * H);
@@ -578,16 +611,17 @@ static int attention_forward(const void* q, const void* k, const void* v, int dt
   // An armed timer brackets the whole operator: start with the first quantiser launch, stop with
   // the attention kernel.
   const Timer tm = take_timer();
-  // Without a producer amax, Q is quantised on load by the attention kernel: the quantise pass
-  // writes only Q's scale and its reciprocal (and Q's codes for groups whose amax is not finite)
-  // and spends its bandwidth on K and V. With a given amax the quantiser writes all three codes.
-  float* qrcp = amax == nullptr ? reinterpret_cast<float*>(ws + w.qrcp) : nullptr;
+  // Q is quantised on load by the attention kernel: the quantise pass writes only Q's scale and its
+  // reciprocal (and Q's codes for groups whose amax is not finite) and spends its bandwidth on K
+  // and V. With a given amax the kernel also checks Q against it (the check the quantise pass
+  // makes for K and V), so a stale maximum still gives the reference's clamp-then-cast codes.
+  float* qrcp = reinterpret_cast<float*>(ws + w.qrcp);
   int rc = quant_bhtd_n(3, xs, dtype, B, H, T, D, strides, granularity, layouts, outs, scs,
                         ws + w.partials, w.total - w.partials, s, Timer{tm.start, nullptr}, amax, nullptr, qrcp);
   if (rc) return rc;
   const int64_t s8[3] = {H * T * D, T * D, D};
   return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, granularity, out, dtype, strides + 9,
-                 B, H, T, D, window, s, Timer{nullptr, tm.stop}, qrcp ? q : nullptr, strides, qrcp);
+                 B, H, T, D, window, s, Timer{nullptr, tm.stop}, q, strides, qrcp, amax);
 }
 
 extern "C" int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, int dtype,

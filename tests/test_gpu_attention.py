@@ -199,6 +199,58 @@ def test_attention_with_producer_amax_is_identical():
         fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax[:5])
 
 
+def _given_amax_two_pass(q, k, v, W, amax_bits):
+    """The operator under a given amax as explicit passes: each tensor through flw_quant_e4m3_amax
+    (its codes checked against the given maximum, pinned against the oracle in
+    tests/test_gpu_quant.py), V into the tile layout, then flw_fp8_swa_fwd on those codes."""
+    from flower_amd import _lib as L
+    lib = L.load()
+    B, H, T, D = q.shape
+    G = H
+    codes, scales = [], torch.empty(3 * G, dtype=torch.float32, device="cuda")
+    for i, (t, layout) in enumerate(((q, L.LAYOUT_BHTD), (k, L.LAYOUT_BHTD), (v, L.LAYOUT_VTILE))):
+        n = lib.flw_vtile_bytes(B, H, T, D) if layout == L.LAYOUT_VTILE else B * H * T * D
+        c = torch.empty(n, dtype=torch.uint8, device="cuda")
+        L.check(lib.flw_quant_e4m3_amax(t.data_ptr(), L.dtype_code(t.dtype), B, H, T, D, *t.stride()[:3],
+                                        L.SCALE_HEAD, layout, amax_bits[i * G:].data_ptr(), c.data_ptr(),
+                                        scales[i * G:].data_ptr(), L.stream_of(t)), "quant")
+        codes.append(c)
+    out = torch.empty((B, H, T, D), dtype=q.dtype, device="cuda")
+    s8 = L.i64s(H * T * D, T * D, D)
+    base = scales.data_ptr()
+    L.check(lib.flw_fp8_swa_fwd(codes[0].data_ptr(), s8, codes[1].data_ptr(), s8, codes[2].data_ptr(), base,
+                                base + 4 * G, base + 8 * G, L.SCALE_HEAD, out.data_ptr(), L.dtype_code(q.dtype),
+                                L.i64s(*out.stride()[:3]), B, H, T, D, W, L.stream_of(q)), "swa")
+    return out
+
+
+@pytest.mark.parametrize("factor", [0.5, 1.0, -1.0])
+def test_q_on_load_under_a_given_amax_checks_it_like_the_quantiser(factor):
+    """With a producer amax, fp8_swa_attention_forward quantises Q inside the attention kernel and
+    checks every lane's values against the given maximum: with the maximum at 0.5x, 1x or -1x the
+    data's own and inf / -inf / NaN / 1e30 planted in Q, the lanes beyond it take the exact path
+    (IEEE division, clamp to +-448, the cast), so the output equals the attention over the
+    given-amax quantiser's codes bit for bit."""
+    from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
+    g = torch.Generator().manual_seed(31)
+    B, H, T, D, W = 2, 4, 300, 64, 96
+    q, k, v = (torch.randn(B, H, T, D, generator=g).mul(torch.rand(1, H, 1, 1, generator=g) * 4 + 0.5)
+               .to(torch.bfloat16) for _ in range(3))
+    amax = torch.cat([t.float().abs().amax(dim=(0, 2, 3)) for t in (q, k, v)]) * factor
+    q[0, 1, 5, :4] = torch.tensor([float("inf"), float("-inf"), float("nan"), 1e30]).to(torch.bfloat16)
+    q[1, 2, 7, 9] = 1e30
+    q, k, v = q.cuda(), k.cuda(), v.cuda()
+    bits = amax.cuda().contiguous().view(torch.int32)
+    print(f"[amax-q-on-load] factor {factor}", flush=True)
+    got = fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=bits)
+    want = _given_amax_two_pass(q, k, v, W, bits)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    if factor == 1.0:
+        # rows that saw no planted value are finite; the planted rows carry the NaN / saturation
+        assert bool(torch.isfinite(got[1, 0]).all())
+
+
 def _two_pass(q, k, v, W, gran):
     """The operator as two explicit passes: flw_quant_qkv_e4m3 (Q, K, V codes) then
     flw_fp8_swa_fwd on those codes -- the path before Q was quantised on load."""
