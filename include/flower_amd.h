@@ -238,7 +238,9 @@ int flw_fp8_swa_attention_forward(const void* q, const void* k, const void* v, i
 /* flw_fp8_swa_attention_forward with the amax of Q, K and V supplied by their producer (u32
  * [3 * (1 | H | B*H)], |x| max fp32 bit patterns in the order q, k, v, e.g. from
  * flw_fp8_scaled_mm_group_amax): the quantiser's amax pass is skipped; scales, codes and the
- * output are those of flw_fp8_swa_attention_forward on the same inputs. */
+ * output are those of flw_fp8_swa_attention_forward on the same inputs. A given maximum below the
+ * data's own gives the reference's clamp(x / s, -448, 448)-then-cast codes for that maximum (Q is
+ * checked against it inside the attention kernel, K and V in the quantiser). */
 int flw_fp8_swa_attention_forward_amax(const void* q, const void* k, const void* v, int dtype,
                                        const int64_t* strides, int64_t B, int64_t H, int64_t T, int64_t D,
                                        int64_t window, int granularity, const uint32_t* amax, void* out,
