@@ -61,7 +61,7 @@ struct SwaParams {
   const float* qs;
   const float* ks;
   const float* vs;
-  int gran;
+  int64_t ssb, ssh;           // element strides of b and h in the scale arrays (0/0 tensor, 0/1 head, H/1 (b, h))
   void* out;
   int64_t osb, osh, ost;      // element strides of out
   int H, T, W, nM, nwg;
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   const int q0 = m0 + 32 * wave;
   const int qcol = lane & 31, hh = lane >> 5;
 
-  const int si = p.gran == FLW_SCALE_TENSOR ? 0 : (p.gran == FLW_SCALE_HEAD ? h : bh);
+  const int64_t si = b * p.ssb + h * p.ssh;
   const float q_s = p.qs[si], k_s = p.ks[si], v_s = p.vs[si];
   const float rsd = D == 32 ? 0.17677669529663687f : (D == 64 ? 0.125f : 0.08838834764831845f);
   const float c = q_s * k_s * rsd * kLog2e;
@@ -485,7 +485,7 @@ static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s
 }
 
 static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, const int64_t* kst,
-                   const uint8_t* vt, const float* qs, const float* ks, const float* vs, int gran,
+                   const uint8_t* vt, const float* qs, const float* ks, const float* vs, int64_t ssb, int64_t ssh,
                    void* out, int out_dtype, const int64_t* ost, int64_t B, int64_t H, int64_t T,
                    int64_t D, int64_t window, hipStream_t stream, Timer tm, const void* qx = nullptr,
                    const int64_t* xst = nullptr, const float* qr = nullptr, const uint32_t* qamax = nullptr) {
@@ -499,7 +499,7 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
   FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
   FLW_REQUIRE(out_dtype == FLW_F32 || out_dtype == FLW_BF16, FLW_E_UNSUPPORTED, "output dtype %d", out_dtype);
-  FLW_REQUIRE(gran >= FLW_SCALE_TENSOR && gran <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", gran);
+  FLW_REQUIRE(ssb >= 0 && ssh >= 0, FLW_E_INVALID, "scale strides must be non-negative");
   FLW_REQUIRE(T <= (int64_t)0x7FFFFF00, FLW_E_UNSUPPORTED, "T too large");
   for (int i = 0; i < 3; ++i) {
     FLW_REQUIRE(qst[i] % 16 == 0 && kst[i] % 16 == 0, FLW_E_INVALID, "q8/k8 strides must be multiples of 16 bytes");
@@ -520,7 +520,7 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.qsb = qst[0]; p.qsh = qst[1]; p.qst = qst[2];
   p.ksb = kst[0]; p.ksh = kst[1]; p.kst = kst[2];
   p.vt_slice = ((T + 63) / 64) * 64 * D;
-  p.qs = qs; p.ks = ks; p.vs = vs; p.gran = gran;
+  p.qs = qs; p.ks = ks; p.vs = vs; p.ssb = ssb; p.ssh = ssh;
   p.out = out; p.osb = ost[0]; p.osh = ost[1]; p.ost = ost[2];
   p.H = (int)H; p.T = (int)T; p.W = (int)W; p.nM = (int)nM;
   p.nwg = (int)(B * H * nM);
@@ -556,9 +556,28 @@ static SwaWorkspace swa_ws_layout(int64_t B, int64_t H, int64_t T, int64_t D) {
   return w;
 }
 
+// Scale-array strides of a granularity: per tensor 0/0, per head 0/1, per (b, h) H/1.
+static int scale_strides(int gran, int64_t H, int64_t* ssb, int64_t* ssh) {
+  FLW_REQUIRE(gran >= FLW_SCALE_TENSOR && gran <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d", gran);
+  *ssb = gran == FLW_SCALE_BH ? H : 0;
+  *ssh = gran == FLW_SCALE_TENSOR ? 0 : 1;
+  return FLW_OK;
+}
+
 }  // namespace flw
 
 using namespace flw;
+
+extern "C" int flw_fp8_swa_fwd_scale_strides(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                                             const int64_t* k_strides, const uint8_t* v_tiles,
+                                             const float* q_scale, const float* k_scale, const float* v_scale,
+                                             int64_t scale_stride_b, int64_t scale_stride_h, void* out,
+                                             int out_dtype, const int64_t* out_strides, int64_t B, int64_t H,
+                                             int64_t T, int64_t D, int64_t window, void* stream) {
+  return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, scale_stride_b,
+                 scale_stride_h, out, out_dtype, out_strides, B, H, T, D, window,
+                 static_cast<hipStream_t>(stream), take_timer());
+}
 
 extern "C" int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
                                const int64_t* k_strides, const uint8_t* v_tiles,
@@ -566,7 +585,10 @@ extern "C" int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, cons
                                int granularity, void* out, int out_dtype,
                                const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
                                int64_t D, int64_t window, void* stream) {
-  return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, granularity,
+  int64_t ssb, ssh;
+  const int rc = scale_strides(granularity, H, &ssb, &ssh);
+  if (rc) return rc;
+  return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, ssb, ssh,
                  out, out_dtype, out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream),
                  take_timer());
 }
@@ -578,8 +600,11 @@ extern "C" int flw_fp8_swa_fwd_qx(const void* q, const int64_t* q_strides, const
                                   const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
                                   int64_t window, void* stream) {
   FLW_REQUIRE(q != nullptr, FLW_E_INVALID, "null q");
+  int64_t ssb, ssh;
+  const int rc = scale_strides(granularity, H, &ssb, &ssh);
+  if (rc) return rc;
   const int64_t s8[3] = {H * T * D, T * D, D};
-  return swa_fwd(q8_nonfinite, s8, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, granularity, out, dtype,
+  return swa_fwd(q8_nonfinite, s8, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, ssb, ssh, out, dtype,
                  out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream), take_timer(), q, q_strides,
                  q_rcp);
 }
@@ -620,7 +645,10 @@ static int attention_forward(const void* q, const void* k, const void* v, int dt
                         ws + w.partials, w.total - w.partials, s, Timer{tm.start, nullptr}, amax, nullptr, qrcp);
   if (rc) return rc;
   const int64_t s8[3] = {H * T * D, T * D, D};
-  return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, granularity, out, dtype, strides + 9,
+  int64_t ssb, ssh;
+  rc = scale_strides(granularity, H, &ssb, &ssh);
+  if (rc) return rc;
+  return swa_fwd(q8, s8, k8, s8, vt, sc, sc + G, sc + 2 * G, ssb, ssh, out, dtype, strides + 9,
                  B, H, T, D, window, s, Timer{nullptr, tm.stop}, q, strides, qrcp, amax);
 }
 

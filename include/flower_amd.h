@@ -208,6 +208,17 @@ int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* 
                     int out_dtype, const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
                     int64_t D, int64_t window, void* stream);
 
+/* flw_fp8_swa_fwd with the scales indexed by element strides instead of a granularity, as the
+ * boundary of flower/kernels/fp8_swa_attention.py:249-258 passes them: the scale of slice (b, h)
+ * is q_scale[b * scale_stride_b + h * scale_stride_h] (likewise k, v); 0/0 is per tensor, 0/1 per
+ * head, H/1 per (b, h), any other non-negative pair another layout of per-(b, h) scales. */
+int flw_fp8_swa_fwd_scale_strides(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                                  const int64_t* k_strides, const uint8_t* v_tiles, const float* q_scale,
+                                  const float* k_scale, const float* v_scale, int64_t scale_stride_b,
+                                  int64_t scale_stride_h, void* out, int out_dtype,
+                                  const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                                  int64_t window, void* stream);
+
 /* flw_fp8_swa_fwd with Q in its input dtype, quantised on load by the attention kernel (the
  * `_per_tensor_fp8(q)` of flower/kernels/fp8_swa_attention.py:242 moved into the kernel's
  * prologue; every Q row is read by exactly one workgroup): q (B, H, T, D) bf16 or fp32 (= dtype,

@@ -151,3 +151,17 @@ def test_issue_probe_refuses_bad_arguments_on_the_host():
     assert lib.flw_diag_issue_probe(1, fake, 256, 0, None) == 1           # no workgroups
     assert lib.flw_diag_issue_probe(5, fake, 256, 1, None) == 1           # no such probe
     assert b"no issue probe" in lib.flw_last_error()
+
+
+@fake_pointers
+def test_scale_strides_are_validated_on_the_host():
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = _lib.load()
+    P = 1 << 20                                  # a fake aligned "device" address
+    s64 = _lib.i64s(64 * 64, 64, 64)
+    rc = lib.flw_fp8_swa_fwd_scale_strides(P, s64, P, s64, P, P, P, P, -1, 1, P, 1, s64, 1, 1, 64, 64, 16, None)
+    assert rc == 1 and b"scale strides" in lib.flw_last_error()
+    rc = lib.flw_fp8_swa_fwd(P, s64, P, s64, P, P, P, P, 7, P, 1, s64, 1, 1, 64, 64, 16, None)
+    assert rc == 1 and b"granularity" in lib.flw_last_error()

@@ -199,6 +199,53 @@ def test_attention_with_producer_amax_is_identical():
         fp8_swa_attention_forward(q, k, v, W, granularity="head", amax=amax[:5])
 
 
+@pytest.mark.parametrize("gran", ["tensor", "head", "bh"])
+def test_scale_strides_entry_matches_the_granularity_entry(gran):
+    """flw_fp8_swa_fwd_scale_strides (scales indexed by b * stride_b + h * stride_h, the boundary's
+    form): 0/0, 0/1 and H/1 give the granularity entry point's output bit for bit, and per-(b, h)
+    scales stored head-major (strides 1/B) give the same output as stored batch-major."""
+    from flower_amd import _lib as L
+    lib = L.load()
+    B, H, T, D, W = 2, 3, 200, 64, 64
+    q, k, v = (seeded((B, H, T, D), s, torch.bfloat16) for s in (91, 92, 93))
+    G = {"tensor": 1, "head": H, "bh": B * H}[gran]
+    q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device="cuda")
+    k8 = torch.empty_like(q8)
+    vt = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device="cuda")
+    sc = torch.empty(3 * G, dtype=torch.float32, device="cuda")
+    ws = L.workspace(3 * lib.flw_quant_workspace_bytes(B, H, T, D), q.device)
+    L.check(lib.flw_quant_qkv_e4m3(q.data_ptr(), k.data_ptr(), v.data_ptr(), L.BF16, B, H, T, D,
+                                   L.i64s(*q.stride()[:3], *k.stride()[:3], *v.stride()[:3]), L.GRANULARITY[gran],
+                                   q8.data_ptr(), k8.data_ptr(), vt.data_ptr(), sc.data_ptr(), ws.data_ptr(),
+                                   ws.numel(), L.stream_of(q)), "quant")
+    s8 = L.i64s(H * T * D, T * D, D)
+    st = L.stream_of(q)
+
+    def run(scales, ssb, ssh):
+        out = torch.empty((B, H, T, D), dtype=torch.bfloat16, device="cuda")
+        base = scales.data_ptr()
+        n = scales.numel() // 3
+        L.check(lib.flw_fp8_swa_fwd_scale_strides(q8.data_ptr(), s8, k8.data_ptr(), s8, vt.data_ptr(), base,
+                                                  base + 4 * n, base + 8 * n, ssb, ssh, out.data_ptr(), L.BF16,
+                                                  L.i64s(*out.stride()[:3]), B, H, T, D, W, st), "swa")
+        return out
+
+    want = torch.empty((B, H, T, D), dtype=torch.bfloat16, device="cuda")
+    base = sc.data_ptr()
+    L.check(lib.flw_fp8_swa_fwd(q8.data_ptr(), s8, k8.data_ptr(), s8, vt.data_ptr(), base, base + 4 * G,
+                                base + 8 * G, L.GRANULARITY[gran], want.data_ptr(), L.BF16,
+                                L.i64s(*want.stride()[:3]), B, H, T, D, W, st), "swa")
+    ssb, ssh = {"tensor": (0, 0), "head": (0, 1), "bh": (H, 1)}[gran]
+    got = run(sc, ssb, ssh)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    if gran == "bh":
+        hm = sc.view(3, B, H).transpose(1, 2).contiguous().view(-1)      # [tensor][h][b]
+        got_hm = run(hm, 1, B)
+        torch.cuda.synchronize()
+        assert torch.equal(got_hm.view(torch.int16), want.view(torch.int16))
+
+
 def _given_amax_two_pass(q, k, v, W, amax_bits):
     """The operator under a given amax as explicit passes: each tensor through flw_quant_e4m3_amax
     (its codes checked against the given maximum, pinned against the oracle in
