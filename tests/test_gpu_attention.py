@@ -128,6 +128,23 @@ def test_full_size_config3_rows_match_oracle_on_sampled_slices():
         mx, mean = rel_errors(out[b:b + 1, h:h + 1], ref)
         assert mx <= MAX_REL and mean <= MEAN_REL, (b, h, mx, mean)
     assert np.isfinite(out).all()
+    _all_slices_checks(q, k, v, W, out)
+
+
+def _all_slices_checks(q, k, v, W, out):
+    """Every (b, h) slice at full size, without the CPU oracle: the operator equals the explicit
+    two-pass path (Q, K, V codes from flw_quant_qkv_e4m3, then flw_fp8_swa_fwd) bit for bit, and
+    reversing the heads of q, k, v reverses the heads of the output bit for bit (per-head scales:
+    no slice's result depends on another slice or on where its workgroups ran)."""
+    got = run(q, k, v, W, "head")
+    assert np.array_equal(to_np(got), out)                 # the operator is deterministic
+    want = _two_pass(q, k, v, W, "head")
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    flip = lambda t: t.flip(1).contiguous()  # noqa: E731
+    rev = run(flip(q), flip(k), flip(v), W, "head")
+    torch.cuda.synchronize()
+    assert torch.equal(rev.flip(1).view(torch.int16), want.view(torch.int16))
 
 
 def test_full_size_config4_rows_match_oracle_on_sampled_slices():
@@ -153,6 +170,7 @@ def test_full_size_config4_rows_match_oracle_on_sampled_slices():
         mx, mean = rel_errors(out[:, h:h + 1], ref)
         assert mx <= MAX_REL and mean <= MEAN_REL, (h, mx, mean)
     assert np.isfinite(out).all()
+    _all_slices_checks(q, k, v, W, out)
 
 
 def test_refuses_grad_tensors():                      # test_swa_kernel.py:68-78
