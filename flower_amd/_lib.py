@@ -103,6 +103,7 @@ SIGNATURES = {
     "flw_diag_quotient": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p]),
     "flw_diag_issue_probe": (c_int, [c_int, c_void_p, c_int64, c_int, c_void_p]),
     "flw_diag_issue_probe_iters": (c_int, []),
+    "flw_diag_mfma_e4m3_dot": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
 }
 
 _lib = None

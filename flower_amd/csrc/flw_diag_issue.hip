@@ -7,6 +7,10 @@
 // independent chains of v_mfma_scale_f32_32x32x64_f8f6f4 (the attention kernel's MFMA). Launched
 // with 256-thread workgroups, four per CU (four waves per SIMD, the attention kernel's
 // occupancy). The host divides the kernel time by the instructions issued per SIMD.
+//
+// Also here: the attention kernel's score product (the same MFMA on e4m3 operands in fragment
+// order) on caller-given operands, so a test can measure its fp32 accumulation against the exact
+// dot product.
 #include "flw_common.h"
 
 namespace flw {
@@ -62,9 +66,46 @@ __global__ __launch_bounds__(256) void issue_probe_kernel(float* out, float seed
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+// The attention kernel's score product on given operands: problem p computes the 32 x 32 block
+// A_p B_p (+ A2_p B2_p when chain != 0, the two-chunk accumulation of head_dim 128) with
+// v_mfma_scale_f32_32x32x64_f8f6f4 on e4m3 codes. Operands arrive in fragment order, 32 bytes per
+// lane (A: row lane % 32, k = 32 (lane / 32) + 0..31; B: column lane % 32, the same k), and the
+// lane's 16 results are written as d[p][64 v + lane] (column lane % 32, row 8 (v / 4) +
+// 4 (lane / 32) + v % 4). Every access is inside problem p's 2 KB / 4 KB.
+__global__ __launch_bounds__(64) void mfma_e4m3_dot_kernel(const uint8_t* __restrict__ a,
+                                                           const uint8_t* __restrict__ b,
+                                                           const uint8_t* __restrict__ a2,
+                                                           const uint8_t* __restrict__ b2, float* __restrict__ d,
+                                                           int chain) {
+  const int64_t p = blockIdx.x;
+  const int lane = threadIdx.x;
+  auto frag = [&](const uint8_t* src) __attribute__((always_inline)) {
+    const uint4* q = reinterpret_cast<const uint4*>(src + p * 2048 + 32 * lane);
+    const uint4 x = q[0], y = q[1];
+    return dv8i{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+  };
+  dv16f acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(frag(a), frag(b), dv16f{}, 0, 0, 0, 0, 0, 0);
+  if (chain) acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(frag(a2), frag(b2), acc, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) d[p * 1024 + 64 * v + lane] = acc[v];
+}
+
 }  // namespace flw
 
 using namespace flw;
+
+extern "C" int flw_diag_mfma_e4m3_dot(const uint8_t* a, const uint8_t* b, const uint8_t* a2, const uint8_t* b2,
+                                      float* d, int64_t nprobe, int chain, void* stream) {
+  FLW_REQUIRE(a != nullptr && b != nullptr && d != nullptr && (!chain || (a2 != nullptr && b2 != nullptr)),
+              FLW_E_INVALID, "null operand");
+  FLW_REQUIRE(nprobe > 0 && nprobe <= 0x7FFFFFFF, FLW_E_INVALID, "nprobe out of range");
+  FLW_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0 && ((uintptr_t)d & 3) == 0 &&
+              (!chain || (((uintptr_t)a2 & 15) == 0 && ((uintptr_t)b2 & 15) == 0)),
+              FLW_E_INVALID, "operands must be 16-byte aligned");
+  hipLaunchKernelGGL(mfma_e4m3_dot_kernel, dim3((unsigned)nprobe), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     a, b, a2, b2, d, chain);
+  return check_launch("flw_diag_mfma_e4m3_dot");
+}
 
 // Instruction-class mask combinations the host may ask for (each is its own kernel).
 #define FLW_ISSUE_PROBES(X)                                                                         \

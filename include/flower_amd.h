@@ -376,6 +376,16 @@ int flw_diag_quotient(const float* x, int64_t n, const float* scales, int64_t n_
 int flw_diag_issue_probe(int mask, float* out, int64_t out_count, int blocks, void* stream);
 int flw_diag_issue_probe_iters(void);
 
+/* No counterpart in the reference. The attention kernel's score product on given e4m3 operands,
+ * so a test can measure how far the FP8 MFMA's fp32 accumulation is from the exact dot product:
+ * nprobe independent 32 x 32 x 64 products d[p] = a[p] b[p] (+ a2[p] b2[p] when chain != 0, as
+ * the two 64-deep chunks of head_dim 128 accumulate). a, b, a2, b2: nprobe x 2048 bytes in
+ * fragment order (lane-major, 32 bytes per lane: A row lane % 32 / B column lane % 32, k =
+ * 32 (lane / 32) + 0..31); d: nprobe x 1024 floats, d[p][64 v + lane] = row 8 (v / 4) +
+ * 4 (lane / 32) + v % 4, column lane % 32. 16-byte aligned operands. */
+int flw_diag_mfma_e4m3_dot(const uint8_t* a, const uint8_t* b, const uint8_t* a2, const uint8_t* b2,
+                           float* d, int64_t nprobe, int chain, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
