@@ -131,6 +131,29 @@ def test_full_size_config3_rows_match_oracle_on_sampled_slices():
     _all_slices_checks(q, k, v, W, out)
 
 
+def test_full_size_config3_fp32_inputs():
+    """C3's shape with fp32 Q, K, V (the quantisers' and the Q-on-load fp32 paths at full size):
+    one slice against the simulator, every slice bit-identical to the two-pass path."""
+    B, H, T, D, W = 4, 16, 8192, 64, 1024
+    g = torch.Generator().manual_seed(4032)
+    mk = lambda: (torch.randn(B, H, T, D, generator=g) * torch.randn(1, H, 1, 1, generator=g).exp()).cuda()  # noqa: E731
+    q, k, v = mk(), mk(), mk()
+    got = run(q, k, v, W, "head")
+    out = to_np(got)
+    q8, qs = per_tensor_fp8(to_np(q), "head")
+    k8, ks = per_tensor_fp8(to_np(k), "head")
+    v8, vs = per_tensor_fp8(to_np(v), "head")
+    b, h = 2, 9
+    ref = fp8_swa_simulate(q8[b:b + 1, h:h + 1], k8[b:b + 1, h:h + 1], v8[b:b + 1, h:h + 1],
+                           qs[:, h:h + 1], ks[:, h:h + 1], vs[:, h:h + 1], W, chunk=1024)
+    mx, mean = rel_errors(out[b:b + 1, h:h + 1], ref)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    assert np.isfinite(out).all()
+    want = _two_pass(q, k, v, W, "head")
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
 def _all_slices_checks(q, k, v, W, out, gran="head"):
     """Every (b, h) slice at full size, without the CPU oracle: the operator equals the explicit
     two-pass path (Q, K, V codes from flw_quant_qkv_e4m3, then flw_fp8_swa_fwd) bit for bit, and
