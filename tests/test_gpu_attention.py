@@ -154,6 +154,27 @@ def test_full_size_config3_fp32_inputs():
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
 
 
+def test_long_ragged_sequence():
+    """T = 30001 (not a multiple of the 64-key tile or the 128-query workgroup), W = 4096, eight
+    heads (slices split evenly over the XCDs): one slice against the simulator, every slice
+    against the two-pass path and under a head reversal."""
+    B, H, T, D, W = 1, 8, 30001, 64, 4096
+    g = torch.Generator().manual_seed(30001)
+    mk = lambda: (torch.randn(B, H, T, D, generator=g) * torch.randn(1, H, 1, 1, generator=g).exp()).to(torch.bfloat16)  # noqa: E731
+    q, k, v = mk().cuda(), mk().cuda(), mk().cuda()
+    out = to_np(run(q, k, v, W, "head"))
+    q8, qs = per_tensor_fp8(to_np(q), "head")
+    k8, ks = per_tensor_fp8(to_np(k), "head")
+    v8, vs = per_tensor_fp8(to_np(v), "head")
+    h = 5
+    ref = fp8_swa_simulate(q8[:, h:h + 1], k8[:, h:h + 1], v8[:, h:h + 1], qs[:, h:h + 1], ks[:, h:h + 1],
+                           vs[:, h:h + 1], W, chunk=1024)
+    mx, mean = rel_errors(out[:, h:h + 1], ref)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    assert np.isfinite(out).all()
+    _all_slices_checks(q, k, v, W, out)
+
+
 def _all_slices_checks(q, k, v, W, out, gran="head"):
     """Every (b, h) slice at full size, without the CPU oracle: the operator equals the explicit
     two-pass path (Q, K, V codes from flw_quant_qkv_e4m3, then flw_fp8_swa_fwd) bit for bit, and
