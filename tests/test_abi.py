@@ -154,6 +154,23 @@ def test_issue_probe_refuses_bad_arguments_on_the_host():
 
 
 @fake_pointers
+def test_mfma_dot_probe_refuses_bad_arguments_on_the_host():
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = _lib.load()
+    f = 1 << 20
+    assert lib.flw_diag_mfma_e4m3_dot(None, f, None, None, f, 1, 0, None) == 1        # null A
+    assert b"null operand" in lib.flw_last_error()
+    assert lib.flw_diag_mfma_e4m3_dot(f, f, None, f, f, 1, 1, None) == 1            # chain without A2
+    assert lib.flw_diag_mfma_e4m3_dot(f, f, None, None, f, 0, 0, None) == 1         # no problems
+    assert lib.flw_diag_mfma_e4m3_dot(f, f, None, None, f, 1 << 31, 0, None) == 1   # too many
+    assert b"nprobe" in lib.flw_last_error()
+    assert lib.flw_diag_mfma_e4m3_dot(f + 8, f, None, None, f, 1, 0, None) == 1     # misaligned A
+    assert b"aligned" in lib.flw_last_error()
+
+
+@fake_pointers
 def test_scale_strides_are_validated_on_the_host():
     from flower_amd import _lib
     if not os.path.exists(_lib.LIB_PATH):
