@@ -482,7 +482,7 @@ def issue_probe():
     one iteration on one SIMD is the kernel time divided by the iterations all waves of a SIMD run.
     For a mix, `overlap` is the fraction of the smaller component hidden under the larger."""
     from flower_amd import _lib
-    lib = _lib.load()
+    lib = _lib.load_diag()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     blocks = 4 * cus                              # 4 workgroups of 4 waves per CU = 4 waves per SIMD
     iters = lib.flw_diag_issue_probe_iters()
@@ -491,7 +491,7 @@ def issue_probe():
     waves_per_simd = blocks * 4 / (4 * cus)
     per_iter = {}
     for mask in ISSUE_PROBES:
-        call = lambda: _lib.check(lib.flw_diag_issue_probe(mask, out.data_ptr(), out.numel(), blocks, stream), "probe")
+        call = lambda: _lib.check(lib.flw_diag_issue_probe(mask, out.data_ptr(), out.numel(), blocks, stream), "probe", lib)
         call()
         torch.cuda.synchronize()
         ev = _events(5)
@@ -654,8 +654,9 @@ def run_gemm(cfg, args):
 
 
 def run_block(cfg, args):
-    """one FP8 decoder block forward (RMSNorm -> QKV -> per-head FP8 SWA -> O ->
-    residual -> RMSNorm -> GELU MLP -> residual), every Linear from the FP8 weight cache."""
+    """one FP8 decoder block forward (RMSNorm -> QKV -> HeadRMSNorm + RoPE of q, k
+    (the reference block's qkv_heads) -> per-head FP8 SWA -> O -> residual -> RMSNorm -> GELU MLP ->
+    residual), every Linear from the FP8 weight cache."""
     from flower_amd.block import Fp8DecoderBlock, block_flops, init_block_
     from flower_amd.precision import fp8_weight_cache
     B, T, d = cfg["B"], cfg["T"], cfg["d_model"]
@@ -688,6 +689,7 @@ def run_block(cfg, args):
         "data": DATA["c5"],
         "config": {"workload": "Fp8DecoderBlock forward, BASELINE C5", "B": B, "T": T, "d_model": d,
                    "num_heads": cfg["num_heads"], "ffn_dim": cfg["ffn_dim"], "window": cfg["W"],
+                   "qk_norm": blk.attn.qk_norm is not None, "rope_base": blk.attn.rope._base,
                    "scales": "per-head attention, per-row x per-channel linears"},
         "roofline": {"bound": "mfma", "achieved": round(flops / (ms * 1e-3) / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),

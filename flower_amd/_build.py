@@ -2,9 +2,11 @@
 
     python -m flower_amd._build          # compile all HIP sources into flower_amd/libflower_amd.so
 
-One shared object, C ABI only (include/flower_amd.h). Every HIP source is compiled with packed
-FP32 instructions disabled (``-target-feature -packed-fp32-ops``); sources compile in parallel
-into ``_build/`` and are linked with ``hipcc -shared``.
+The product: one shared object, C ABI only (include/flower_amd.h). Beside it, and never linked
+into it, the diagnostics library flower_amd/libflower_amd_diag.so (csrc/diag/flw_diag.h: device
+arithmetic checks and the issue-cost probe that tests and bench.py load). Every HIP source is
+compiled with packed FP32 instructions disabled (``-target-feature -packed-fp32-ops``); sources
+compile in parallel into ``_build/`` and are linked with ``hipcc -shared``.
 """
 
 from __future__ import annotations
@@ -19,14 +21,16 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJDIR = os.path.join(ROOT, "_build")
 LIB = os.path.join(HERE, "libflower_amd.so")
-SOURCES = ["flw_error.hip", "flw_quant.hip", "flw_swa.hip", "flw_swa_bf16.hip", "flw_gemm.hip", "flw_selftest.hip",
-           "flw_diag_issue.hip"]
+DIAG_LIB = os.path.join(HERE, "libflower_amd_diag.so")
+SOURCES = ["flw_error.hip", "flw_quant.hip", "flw_swa.hip", "flw_swa_bf16.hip", "flw_gemm.hip"]
+# The diagnostics library: its own source plus its own copy of the error / timing state.
+DIAG_SOURCES = ["diag/flw_diag.hip"]
 ARCH = os.environ.get("FLW_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wno-unused-result", "-I", os.path.join(ROOT, "include"),
+    "-Wno-unused-result", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
 ]
 # Attention: MFMA accumulators in ordinary VGPRs (the online-softmax rescale works on them in
 # place instead of copying through AGPRs), and no IEEE mode, since in IEEE mode every fmax operand
@@ -61,19 +65,23 @@ def _run_all(cmds, verbose):
         raise RuntimeError("\n".join(errors))
 
 
+def _obj(source: str) -> str:
+    return os.path.join(OBJDIR, os.path.basename(source).replace(".hip", ".o"))
+
+
 def build(verbose: bool = False) -> str:
+    """Compile every source and link both libraries; returns the product library's path."""
     os.makedirs(OBJDIR, exist_ok=True)
     cc = hipcc()
-    objs, cmds = [], []
-    for s in SOURCES:
-        src = os.path.join(CSRC, s)
-        obj = os.path.join(OBJDIR, s.replace(".hip", ".o"))
-        objs.append(obj)
-        cmds.append([cc, *COMMON, *PER_SOURCE.get(s, []), "-c", src, "-o", obj])
+    cmds = [[cc, *COMMON, *PER_SOURCE.get(s, []), "-c", os.path.join(CSRC, s), "-o", _obj(s)]
+            for s in SOURCES + DIAG_SOURCES]
     _run_all(cmds, verbose)
-    tmp = LIB + ".tmp"
-    _run_all([[cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]], verbose)
-    os.replace(tmp, LIB)
+    links = []
+    for lib, srcs in ((LIB, SOURCES), (DIAG_LIB, DIAG_SOURCES + ["flw_error.hip"])):
+        links.append([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(_obj, srcs), "-o", lib + ".tmp"])
+    _run_all(links, verbose)
+    for lib in (LIB, DIAG_LIB):
+        os.replace(lib + ".tmp", lib)
     return LIB
 
 

@@ -99,6 +99,14 @@ SIGNATURES = {
                                   c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "flw_fp8_scaled_mm_residual": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                            c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
+}
+
+# The diagnostics library (flower_amd/csrc/diag/flw_diag.h): instruments for tests and bench.py.
+DIAG_LIB_PATH = os.path.join(_HERE, "libflower_amd_diag.so")
+DIAG_SIGNATURES = {
+    "flw_last_error": (c_char_p, []),
+    "flw_abi_version": (c_int, []),
+    "flw_time_next_launch": (c_int, [c_void_p, c_void_p]),
     "flw_diag_cvt_e4m3": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "flw_diag_quotient": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p]),
     "flw_diag_issue_probe": (c_int, [c_int, c_void_p, c_int64, c_int, c_void_p]),
@@ -107,6 +115,7 @@ SIGNATURES = {
 }
 
 _lib = None
+_diag = None
 
 
 def load() -> ctypes.CDLL:
@@ -128,13 +137,31 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+def load_diag() -> ctypes.CDLL:
+    """Load (once) the diagnostics library. Raises RuntimeError if it is not built."""
+    global _diag
+    if _diag is not None:
+        return _diag
+    if not os.path.exists(DIAG_LIB_PATH):
+        raise RuntimeError(
+            f"libflower_amd_diag.so is not built ({DIAG_LIB_PATH}); run `python -m flower_amd._build`")
+    lib = ctypes.CDLL(DIAG_LIB_PATH)
+    for name, (res, args) in DIAG_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _diag = lib
+    return lib
+
+
 class FlowerError(RuntimeError):
     pass
 
 
-def check(rc: int, what: str) -> None:
+def check(rc: int, what: str, lib: ctypes.CDLL | None = None) -> None:
+    """Raise for a non-zero status; ``lib`` is the library that returned it (default: the product)."""
     if rc != 0:
-        msg = load().flw_last_error().decode(errors="replace")
+        msg = (lib or load()).flw_last_error().decode(errors="replace")
         if rc in (1, 2):          # FLW_E_INVALID / FLW_E_UNSUPPORTED: caller error
             raise ValueError(f"{what}: {msg}")
         raise FlowerError(f"{what} failed ({rc}): {msg}")
@@ -172,5 +199,5 @@ def workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-__all__ = ["load", "check", "require_gpu", "dtype_code", "stream_of", "ptr", "i64s", "workspace",
-           "GRANULARITY", "SIGNATURES", "LIB_PATH"]
+__all__ = ["load", "load_diag", "check", "require_gpu", "dtype_code", "stream_of", "ptr", "i64s", "workspace",
+           "GRANULARITY", "SIGNATURES", "LIB_PATH", "DIAG_SIGNATURES", "DIAG_LIB_PATH"]

@@ -3,17 +3,23 @@ the attention on the fused FP8 sliding-window kernel.
 
 Layout and parameter names follow flower/models/base.py:
   ``RMSNorm``                 base.py:324-338 (fp32 mean-square, rsqrt, then the gain)
-  ``Fp8CausalSelfAttention``  base.py:553-665: ``qkv`` Linear(d, 3d) -> chunk -> heads as strided
-                              (B, H, T, D) views (base.py:607-614, read in place by the
-                              quantiser) -> FP8 SWA -> (B, T, d) -> ``out`` Linear(d, d);
+  ``Fp8CausalSelfAttention``  base.py:553-665: the module's ``attn_precision: "fp8"`` route
+                              (flower_amd.attention.CausalSelfAttention) with both projections as
+                              Fp8Linear: ``qkv`` Linear(d, 3d) -> heads as strided (B, H, T, D)
+                              views (base.py:607-614) -> HeadRMSNorm of q, k when ``qk_norm``
+                              (base.py:632-633; on by default, as the 450M FP8 configs set it,
+                              configs/sweep13_450m_longctx_fp8.yaml:109) -> RoPE of q, k
+                              (base.py:634, always, base ``rope_base``) -> e4m3 (the quantisation
+                              point, base.py:636-637) -> FP8 SWA -> ``out`` Linear(d, d);
                               forward-only like the FP8 kernel (fp8_swa_attention.py:71-76)
   ``Fp8FeedForward``          base.py:514-525 GELU layout (``net.0`` Linear(d, ffn), GELU,
                               ``net.3`` Linear(ffn, d); dropout is identity in eval)
   ``Fp8DecoderBlock``         base.py:698-722: x + attn(ln1(x)), then + ff(ln2(x))
 
 ``forward`` runs the fused path on bf16 GPU inputs (RMSNorm and GELU fused with the next
-linear's per-row e4m3 quantisation, residual adds in the GEMM epilogues, the attention writing its
-(B, T, H, D) output in place: 11 library kernels, no torch elementwise kernels);
+linear's per-row e4m3 quantisation, QK-norm + RoPE fused with the Q / K / V quantiser, residual
+adds in the GEMM epilogues, the attention writing its (B, T, H, D) output in place: library kernels
+only, no torch elementwise kernels);
 ``forward_unfused`` is the module-by-module composition (torch norms / GELU / adds around the
 library's linears and attention). Wrap calls in ``fp8_weight_cache(block)`` to quantise the
 weights once.
@@ -21,11 +27,14 @@ weights once.
 
 from __future__ import annotations
 
+from types import SimpleNamespace
+
 import torch
 import torch.nn as nn
 
 from . import _lib
-from .kernels.fp8_swa_attention import fp8_swa_attention_forward
+from .attention import CausalSelfAttention
+from .kernels.fp8_swa_attention import fp8_swa_attention_from_codes, qk_norm_rope_quant_e4m3
 from .precision import Fp8Linear
 
 
@@ -40,29 +49,20 @@ class RMSNorm(nn.Module):
         return (x.float() * rms).to(dtype=x.dtype) * self.weight
 
 
-class Fp8CausalSelfAttention(nn.Module):
+class Fp8CausalSelfAttention(CausalSelfAttention):
+    """The reference's attention module with ``attn_precision: "fp8"`` and FP8 projections."""
+
     def __init__(self, d_model: int, num_heads: int, local_window: int | None, *, bias: bool = False,
-                 recipe: str = "rowwise", granularity: str = "head") -> None:
-        super().__init__()
-        if d_model % num_heads:
-            raise ValueError("d_model must be divisible by num_heads")
-        self.num_heads = num_heads
-        self.head_dim = d_model // num_heads
-        self.local_window = local_window
+                 recipe: str = "rowwise", granularity: str = "head", qk_norm: bool = True,
+                 rope_base: float = 10000.0, max_seq_len: int = 8192) -> None:
+        cfg = SimpleNamespace(d_model=d_model, num_heads=num_heads, max_seq_len=max_seq_len, rope_base=rope_base,
+                              use_bias=bias, qk_norm=qk_norm, attn_precision="fp8",
+                              fp8_attention_granularity=granularity)
+        super().__init__(cfg, local_window)
         self.granularity = granularity
-        self.qkv = Fp8Linear(d_model, 3 * d_model, bias=bias, recipe=recipe)
-        self.out = Fp8Linear(d_model, d_model, bias=bias, recipe=recipe)
-
-    def _split(self, x: torch.Tensor) -> torch.Tensor:
-        bsz, seq_len, _ = x.shape
-        return x.view(bsz, seq_len, self.num_heads, self.head_dim).transpose(1, 2)
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        q, k, v = self.qkv(x).chunk(3, dim=-1)
-        q, k, v = self._split(q), self._split(k), self._split(v)
-        window = x.shape[1] if self.local_window is None else self.local_window
-        out = fp8_swa_attention_forward(q, k, v, window, granularity=self.granularity)
-        return self.out(out.transpose(1, 2).reshape(x.shape))
+        self.qkv = Fp8Linear.from_linear(self.qkv, recipe)
+        self.out = Fp8Linear.from_linear(self.out, recipe)
+        self.out._is_residual_out = True
 
 
 class Fp8FeedForward(nn.Module):
@@ -80,13 +80,19 @@ class Fp8FeedForward(nn.Module):
 
 
 class Fp8DecoderBlock(nn.Module):
+    """BASELINE config 5's block. ``recipe`` defaults to "rowwise" (per-output-channel weight
+    scales, the configuration's stated recipe); ``qk_norm`` / ``rope_base`` / ``max_seq_len`` as
+    the reference's ModelConfig fields (the RoPE tables grow on demand past ``max_seq_len``)."""
+
     def __init__(self, d_model: int = 1024, num_heads: int = 16, ffn_dim: int = 4096,
                  local_window: int | None = 4096, *, bias: bool = False, recipe: str = "rowwise",
-                 granularity: str = "head") -> None:
+                 granularity: str = "head", qk_norm: bool = True, rope_base: float = 10000.0,
+                 max_seq_len: int = 8192) -> None:
         super().__init__()
         self.ln1 = RMSNorm(d_model)
         self.attn = Fp8CausalSelfAttention(d_model, num_heads, local_window, bias=bias, recipe=recipe,
-                                           granularity=granularity)
+                                           granularity=granularity, qk_norm=qk_norm, rope_base=rope_base,
+                                           max_seq_len=max_seq_len)
         self.ln2 = RMSNorm(d_model)
         self.ff = Fp8FeedForward(d_model, ffn_dim, bias=bias, recipe=recipe)
 
@@ -98,8 +104,9 @@ class Fp8DecoderBlock(nn.Module):
 
     @torch.no_grad()
     def forward_unfused(self, x: torch.Tensor) -> torch.Tensor:
-        """The reference composition, one module after the other."""
-        x = x + self.attn(self.ln1(x))
+        """The reference composition, one module after the other (the attention through torch's
+        qkv_heads -- QK-norm and RoPE in torch ops -- and fp8_swa_attention_forward)."""
+        x = x + self.attn.forward_unfused(self.ln1(x))
         return x + self.ff(self.ln2(x))
 
     def _linears(self):
@@ -115,7 +122,8 @@ class Fp8DecoderBlock(nn.Module):
 
     def _forward_fused(self, x: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
         """The same block with the work around the FP8 GEMMs fused into the library's kernels:
-        RMSNorm -> per-row e4m3 in one pass (flw_rmsnorm_quant_rows_e4m3), the attention writing
+        RMSNorm -> per-row e4m3 in one pass (flw_rmsnorm_quant_rows_e4m3), QK-norm + RoPE + the
+        Q / K / V e4m3 in one pass pair (flw_qk_norm_rope_quant_e4m3), the attention writing
         its (B, T, H, D) output in place, the residual adds in the GEMM epilogues
         (flw_fp8_scaled_mm_residual), GELU -> per-row e4m3 in one pass (flw_gelu_quant_rows_e4m3).
         Every rounding step of the unfused composition is kept (bf16 norm / GELU outputs, bf16
@@ -124,8 +132,9 @@ class Fp8DecoderBlock(nn.Module):
         ``trace`` (a dict, for stage-by-stage checks): receives every intermediate of the call --
         the row codes / scales of each linear's input ("c1"/"s1", "ca"/"sa", "c2"/"s2",
         "cg"/"sg"), the normed / activated rows the fused quantisers also write out when tracing
-        ("h1", "h2", "hg"), the QKV output "qkv" with its epilogue maxima "amax", the attention
-        output "attn", "x1" and the FF1 output "f". The kernels and the result are the same."""
+        ("h1", "h2", "hg"), the QKV output "qkv", the QK-normed and rotated "q" / "k", the attention
+        operands "q8" / "k8" / "v_tiles" / "scales", the attention output "attn", "x1" and the FF1
+        output "f". The kernels and the result are the same."""
         lib = _lib.load()
         B, T, d = x.shape
         M = B * T
@@ -171,37 +180,28 @@ class Fp8DecoderBlock(nn.Module):
 
         att = self.attn
         c1, s1 = codes_of("rmsnorm", x2, d, self.ln1, "h1")
-        amax = None
-        if att.granularity == "head" and d % 128 == 0 and M * d < 2 ** 32 and 3 * d * d < 2 ** 32:
-            # QKV projection with the per-head |q|, |k|, |v| maxima from its epilogue: the
-            # attention's quantiser then needs no amax pass. Nothing may transform q / k between
-            # the GEMM and the quantiser (no QK-norm or RoPE in this block), or these maxima
-            # would not be those of the quantised tensors. The epilogue exists only in the
-            # 256 x 256 GEMM (K % 128 == 0, operands < 2^32 bytes); other shapes take the
-            # quantiser's own amax pass.
-            w8, ws = qkv_l.weight_codes()
-            N, K = w8.shape
-            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-            amax = torch.empty(N // att.head_dim, dtype=torch.int32, device=dev)
-            _lib.check(lib.flw_fp8_scaled_mm_group_amax(c1.data_ptr(), M, K, w8.data_ptr(), N, s1.data_ptr(), M,
-                                                        ws.data_ptr(), ws.numel(), y.data_ptr(), N, att.head_dim,
-                                                        amax.data_ptr(), stream), "qkv + amax")
-            qkv = y.view(B, T, 3 * d)
-        else:
-            qkv = linear(c1, s1, qkv_l).view(B, T, 3 * d)
+        qkv = linear(c1, s1, qkv_l).view(B, T, 3 * d)
+        # The quantisation point of qkv_heads (base.py:630-637): HeadRMSNorm and RoPE of q, k and the
+        # three e4m3 quantisations in one pass pair over the strided head views of the projection.
         q, k, v = (att._split(t) for t in qkv.chunk(3, dim=-1))
+        cos, sin = att.rope.tables(T, qkv.dtype, dev)
+        res = qk_norm_rope_quant_e4m3(q, k, v, qk_norm=att.qk_norm is not None,
+                                      eps=att.qk_norm.eps if att.qk_norm is not None else 0.0,
+                                      rope_cos=cos, rope_sin=sin, granularity=att.granularity,
+                                      return_transformed=trace is not None)
+        q8, k8, vt, scales = res[:4]
         a = torch.empty((B, T, d), dtype=torch.bfloat16, device=dev)
         window = T if att.local_window is None else att.local_window
-        fp8_swa_attention_forward(q, k, v, window, granularity=att.granularity,
-                                  out=a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2), amax=amax)
+        fp8_swa_attention_from_codes(q8, k8, vt, scales, window, granularity=att.granularity,
+                                     out=a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2))
         ca, sa = codes_of("plain", a.view(M, d), d)
         x1 = linear(ca, sa, out_l, residual=x2)
         c2, s2 = codes_of("rmsnorm", x1, d, self.ln2, "h2")
         f = linear(c2, s2, ff1_l)
         cg, sg = codes_of("gelu", f, f.shape[1], h_name="hg")
         if trace is not None:
-            trace.update(c1=c1, s1=s1, qkv=qkv, amax=amax, attn=a, ca=ca, sa=sa, x1=x1, c2=c2, s2=s2, f=f,
-                         cg=cg, sg=sg)
+            trace.update(c1=c1, s1=s1, qkv=qkv, q=res[4], k=res[5], q8=q8, k8=k8, v_tiles=vt, scales=scales,
+                         attn=a, ca=ca, sa=sa, x1=x1, c2=c2, s2=s2, f=f, cg=cg, sg=sg)
         return linear(cg, sg, ff2_l, residual=x1).view(B, T, d)
 
 

@@ -1,16 +1,23 @@
-// Diagnostic: issue cost on one SIMD of the instruction classes the FP8 attention loop is made of,
-// alone and in combination with the QK^T / PV MFMA, so the kernel's time can be accounted for
-// from measured per-instruction costs instead of nominal rates. Not part of the attention path.
+// Diagnostics library (libflower_amd_diag.so), built beside the product library and never linked
+// into it: instruments that check the device arithmetic the product kernels rely on, and price the
+// attention loop's instruction classes. Nothing on the attention / quantiser / GEMM path calls it.
 //
-// Every probe kernel runs kIters iterations per lane of eight independent chains of one
-// instruction (inline assembly, so the instruction is exactly the one named), and/or two
-// independent chains of v_mfma_scale_f32_32x32x64_f8f6f4 (the attention kernel's MFMA). Launched
-// with 256-thread workgroups, four per CU (four waves per SIMD, the attention kernel's
-// occupancy). The host divides the kernel time by the instructions issued per SIMD.
-//
-// Also here: the attention kernel's score product (the same MFMA on e4m3 operands in fragment
-// order) on caller-given operands, so a test can measure its fp32 accumulation against the exact
-// dot product.
+// flw_diag_cvt_e4m3      the hardware fp32 -> e4m3 converter (v_cvt_pk_fp8_f32, the attention
+//                        kernel's P conversion and the quantisers' fast path) against the exact
+//                        software rounding, on caller-given values.
+// flw_diag_quotient      x / s by IEEE division against the quantisers' reciprocal-and-correct
+//                        sequence (div_by_scale), on caller-given pairs.
+// flw_diag_issue_probe   issue cost on one SIMD of the instruction classes the FP8 attention loop is
+//                        made of, alone and with the QK^T / PV MFMA. Every probe kernel runs
+//                        kIters iterations per lane of eight independent chains of one instruction
+//                        (inline assembly, so the instruction is exactly the one named), and/or two
+//                        independent chains of v_mfma_scale_f32_32x32x64_f8f6f4. Launched with
+//                        256-thread workgroups, four per CU (four waves per SIMD, the attention
+//                        kernel's occupancy). The host divides the kernel time by the instructions
+//                        issued per SIMD.
+// flw_diag_mfma_e4m3_dot the attention kernel's score product (the same MFMA on e4m3 operands in
+//                        fragment order) on caller-given operands, so a test can measure its fp32
+//                        accumulation against the exact dot product.
 #include "flw_common.h"
 
 namespace flw {
@@ -19,6 +26,33 @@ typedef int dv8i __attribute__((ext_vector_type(8)));
 typedef float dv16f __attribute__((ext_vector_type(16)));
 
 constexpr int kIters = 1024;
+
+__global__ __launch_bounds__(256) void cvt_hw_kernel(const float* __restrict__ x, uint8_t* __restrict__ out,
+                                                     int64_t npairs) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= npairs) return;
+  const int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[2 * i], x[2 * i + 1], 0, false);
+  out[2 * i] = (uint8_t)(w & 0xFF);
+  out[2 * i + 1] = (uint8_t)((w >> 8) & 0xFF);
+}
+
+__global__ __launch_bounds__(256) void cvt_sw_kernel(const float* __restrict__ x, uint8_t* __restrict__ out,
+                                                     int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  out[i] = (uint8_t)(f32_to_e4m3(x[i]) & 0xFF);
+}
+
+// mode 0: IEEE x / s;  mode 1: the quantisers' reciprocal-and-correct quotient.
+__global__ __launch_bounds__(256) void quotient_kernel(const float* __restrict__ x, int64_t n,
+                                                       const float* __restrict__ s, int64_t ns,
+                                                       uint32_t* __restrict__ out, int mode) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n * ns) return;
+  const float xv = x[i % n], sv = s[i / n];
+  const float q = mode == 0 ? xv / sv : div_by_scale(xv, sv, 1.0f / sv);
+  out[i] = __float_as_uint(q);
+}
 
 enum : int {
   P_FMA = 1, P_EXP = 2, P_MAX3 = 4, P_CVT = 8, P_MUL = 16, P_PERM = 32, P_MFMA = 64,
@@ -128,3 +162,29 @@ extern "C" int flw_diag_issue_probe(int mask, float* out, int64_t out_count, int
 }
 
 extern "C" int flw_diag_issue_probe_iters(void) { return kIters; }
+
+extern "C" int flw_diag_cvt_e4m3(const float* x, uint8_t* out, int64_t n, int hardware, void* stream) {
+  FLW_REQUIRE(x != nullptr && out != nullptr && n > 0, FLW_E_INVALID, "bad arguments");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hardware) {
+    FLW_REQUIRE(n % 2 == 0, FLW_E_INVALID, "hardware conversion works on pairs: n must be even");
+    const int64_t np = n / 2;
+    FLW_REQUIRE((np + 255) / 256 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many values");
+    hipLaunchKernelGGL(cvt_hw_kernel, dim3((unsigned)((np + 255) / 256)), dim3(256), 0, s, x, out, np);
+  } else {
+    FLW_REQUIRE((n + 255) / 256 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many values");
+    hipLaunchKernelGGL(cvt_sw_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, out, n);
+  }
+  return check_launch("flw_diag_cvt_e4m3");
+}
+
+extern "C" int flw_diag_quotient(const float* x, int64_t n, const float* scales, int64_t n_scales,
+                                 uint32_t* out, int mode, void* stream) {
+  FLW_REQUIRE(x && scales && out && n > 0 && n_scales > 0, FLW_E_INVALID, "bad arguments");
+  FLW_REQUIRE(mode == 0 || mode == 1, FLW_E_INVALID, "mode must be 0 (IEEE) or 1 (reciprocal + correction)");
+  const int64_t total = n * n_scales;
+  FLW_REQUIRE((total + 255) / 256 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many quotients");
+  hipLaunchKernelGGL(quotient_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, n, scales, n_scales, out, mode);
+  return check_launch("flw_diag_quotient");
+}

@@ -193,6 +193,60 @@ template <> struct Vec16<uint16_t> {   // bf16
   }
 };
 
+// Rounding to the tensor's dtype (bf16: round to nearest even, NaN quietened; fp32: identity).
+template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (sizeof(T) == 2) return round_bf16(x);
+  return x;
+}
+
+// The pre-attention transform of CausalSelfAttention.qkv_heads (flower/models/base.py:630-637) on
+// one lane's Vec16<T>::N consecutive values f of a head row of d values, every step rounded to the
+// tensor's dtype as the reference's torch ops round it:
+//   HeadRMSNorm (base.py:355-357, when `norm`): h = dtype(x * (1 / sqrt(mean(x^2) + eps))), fp32
+//     maths; the row's sum of squares is an fma chain over the lane's values, then a butterfly
+//     over the `lanes` lanes (an aligned power-of-two group, lane order = column order) that hold
+//     the row -- the same order wherever this is called, so every caller gets the same bits;
+//   RoPE (base.py:478-483, rotate_half :465-469; when cos_row is not null):
+//     out[2i]   = dtype(dtype(h[2i] c) + dtype(-h[2i+1] s)),
+//     out[2i+1] = dtype(dtype(h[2i+1] c) + dtype(h[2i] s)),
+//     c / s the lane's N entries of the [T, D] tables' row for this position.
+// Every lane of a group must call this together (it shuffles). An invalid lane (padding, zeros)
+// reads no table and keeps its zeros: with eps == 0 its r would be inf, and 0 * inf = NaN would
+// reach a caller's amax.
+template <typename T>
+__device__ __forceinline__ void head_norm_rope(float* f, bool norm, float eps, int d, int lanes, bool valid,
+                                               const T* cos_row, const T* sin_row) {
+  // Separate products and sums, as the reference's separate torch ops round them: no FMA
+  // contraction in this function (hipcc contracts a * b + c by default, which would change the
+  // fp32 results).
+#pragma clang fp contract(off)
+  constexpr int N = Vec16<T>::N;
+  if (norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ss = fmaf(f[i], f[i], ss);
+    for (int o = 1; o < lanes; o <<= 1) ss = ss + __shfl_xor(ss, o, 64);
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)d + eps);   // IEEE sqrt and division
+#pragma unroll
+    for (int i = 0; i < N; ++i) f[i] = valid ? round_to<T>(f[i] * r) : 0.0f;
+  }
+  if (cos_row != nullptr && valid) {
+    float c[N], sn[N];
+    Vec16<T>::load(cos_row, c);
+    Vec16<T>::load(sin_row, sn);
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      const float a0 = round_to<T>(f[i] * c[i]);
+      const float b0 = round_to<T>(-f[i + 1] * sn[i]);
+      const float a1 = round_to<T>(f[i + 1] * c[i + 1]);
+      const float b1 = round_to<T>(f[i] * sn[i + 1]);
+      f[i] = round_to<T>(a0 + b0);
+      f[i + 1] = round_to<T>(a1 + b1);
+    }
+  }
+}
+
 // LDS pointer type: the 32-bit LDS address of a __shared__ object is (uint32_t)(lds_u8_t*)p.
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 

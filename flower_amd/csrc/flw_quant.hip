@@ -16,7 +16,7 @@
 // (the reciprocal-then-correct sequence of Markstein, correctly rounded when r is the correctly
 // rounded reciprocal) and the hardware RNE converter v_cvt_pk_fp8_f32, two values per
 // instruction. Both are checked bit for bit on the device against the exact division and the
-// exact software rounding (flw_diag_* entry points and their tests). A group whose amax is NaN or
+// exact software rounding (the diagnostics library and its tests). A group whose amax is NaN or
 // infinite takes the exact path (IEEE division, clamp, software rounding) so that NaN and inf
 // propagate exactly as in the reference.
 #include <mutex>
@@ -82,54 +82,17 @@ __device__ __forceinline__ int64_t vec_offset(const QTensor& t, int64_t r0, int6
   return row * t.s2 + cv * n;
 }
 
-// Rounding to the tensor's dtype (bf16: round to nearest even, NaN quietened; fp32: identity).
-template <typename T>
-__device__ __forceinline__ float round_to(float x) {
-  if constexpr (sizeof(T) == 2) return round_bf16(x);
-  return x;
-}
-
-// The pre-attention transform of CausalSelfAttention.qkv_heads (flower/models/base.py:630-637) on
-// one 16-byte vector (column block cv of row `row` of a slice), every step rounded to the tensor's
-// dtype as the reference's torch ops round it:
-//   HeadRMSNorm (base.py:355-357): h = dtype(x * (1 / sqrt(mean(x^2) + eps))), fp32 maths; the
-//     row's sum of squares is reduced over the vpr lanes that hold the row (aligned groups);
-//   RoPE (base.py:478-483, rotate_half :465-469): out[2i]   = dtype(dtype(h[2i] c) + dtype(-h[2i+1] s)),
-//     out[2i+1] = dtype(dtype(h[2i+1] c) + dtype(h[2i] s)), c / s from the [T, D] tables.
-// Every lane of a vpr group must call this together (valid or not: invalid lanes carry
-// zeros and read no table).
+// The pre-attention transform of CausalSelfAttention.qkv_heads on one 16-byte vector (column
+// block cv of row `row` of a slice): head_norm_rope (flw_common.h) with the row's sum of squares
+// reduced over the vpr lanes that hold the row. Every lane of a vpr group must call this together
+// (valid or not: invalid lanes carry zeros and read no table).
 template <typename T>
 __device__ __forceinline__ void qk_transform(const QTensor& t, float* f, int64_t row, int64_t cv, int vpr,
                                              int64_t d3, bool valid) {
-  // Separate products and sums, as the reference's separate torch ops round them: no FMA
-  // contraction in this function (hipcc contracts a * b + c by default, which would change the
-  // fp32 results).
-#pragma clang fp contract(off)
-  constexpr int N = Vec16<T>::N;
-  if (t.norm) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < N; ++i) ss = fmaf(f[i], f[i], ss);
-    for (int o = 1; o < vpr; o <<= 1) ss = ss + __shfl_xor(ss, o, 64);
-    const float r = 1.0f / __builtin_sqrtf(ss / (float)d3 + t.eps);   // IEEE sqrt and division
-#pragma unroll
-    for (int i = 0; i < N; ++i) f[i] = round_to<T>(f[i] * r);
-  }
-  if (t.rcos != nullptr && valid) {
-    float c[N], sn[N];
-    const int64_t off = row * d3 + cv * N;
-    Vec16<T>::load(static_cast<const T*>(t.rcos) + off, c);
-    Vec16<T>::load(static_cast<const T*>(t.rsin) + off, sn);
-#pragma unroll
-    for (int i = 0; i < N; i += 2) {
-      const float a0 = round_to<T>(f[i] * c[i]);
-      const float b0 = round_to<T>(-f[i + 1] * sn[i]);
-      const float a1 = round_to<T>(f[i + 1] * c[i + 1]);
-      const float b1 = round_to<T>(f[i] * sn[i + 1]);
-      f[i] = round_to<T>(a0 + b0);
-      f[i + 1] = round_to<T>(a1 + b1);
-    }
-  }
+  const int64_t off = row * d3 + cv * Vec16<T>::N;
+  head_norm_rope<T>(f, t.norm, t.eps, (int)d3, vpr, valid,
+                    t.rcos ? static_cast<const T*>(t.rcos) + off : nullptr,
+                    t.rsin ? static_cast<const T*>(t.rsin) + off : nullptr);
 }
 
 template <typename T, bool XFORM = false>
@@ -896,19 +859,6 @@ int amax_bhtd(const void* x, int dtype, int64_t B, int64_t H, int64_t T, int64_t
   return check_launch("flw_amax_e4m3");
 }
 
-// ---------------------------------------------------------------- diagnostics
-
-// mode 0: IEEE x / s;  mode 1: the quantiser's reciprocal-and-correct quotient.
-__global__ __launch_bounds__(256) void quotient_kernel(const float* __restrict__ x, int64_t n,
-                                                       const float* __restrict__ s, int64_t ns,
-                                                       uint32_t* __restrict__ out, int mode) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n * ns) return;
-  const float xv = x[i % n], sv = s[i / n];
-  const float q = mode == 0 ? xv / sv : div_by_scale(xv, sv, 1.0f / sv);
-  out[i] = __float_as_uint(q);
-}
-
 }  // namespace flw
 
 using namespace flw;
@@ -1148,17 +1098,6 @@ extern "C" int flw_gelu_quant_rows_e4m3(const void* x, int64_t rows, int64_t col
                                         uint8_t* out, float* scale_out, void* h_out, void* stream) {
   return rows_act_quant<kActGelu>(x, rows, cols, row_stride, nullptr, 0.0f, out, scale_out, h_out,
                                   static_cast<hipStream_t>(stream), "flw_gelu_quant_rows_e4m3");
-}
-
-extern "C" int flw_diag_quotient(const float* x, int64_t n, const float* scales, int64_t n_scales,
-                                 uint32_t* out, int mode, void* stream) {
-  FLW_REQUIRE(x && scales && out && n > 0 && n_scales > 0, FLW_E_INVALID, "bad arguments");
-  FLW_REQUIRE(mode == 0 || mode == 1, FLW_E_INVALID, "mode must be 0 (IEEE) or 1 (reciprocal + correction)");
-  const int64_t total = n * n_scales;
-  FLW_REQUIRE((total + 255) / 256 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "too many quotients");
-  hipLaunchKernelGGL(quotient_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, n, scales, n_scales, out, mode);
-  return check_launch("flw_diag_quotient");
 }
 
 namespace flw {

@@ -292,6 +292,15 @@ def qk_norm_rope_quant_e4m3(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *
     return q8, k8, vt, scales
 
 
+_CODE_DTYPES = (torch.uint8, torch.float8_e4m3fn)
+
+
+def _group_count(granularity: str, B: int, H: int) -> int:
+    if granularity not in _lib.GRANULARITY:
+        raise ValueError(f"granularity must be one of {sorted(_lib.GRANULARITY)}, got {granularity!r}")
+    return {"tensor": 1, "head": H, "bh": B * H}[granularity]
+
+
 def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: torch.Tensor,
                                  scales: torch.Tensor, window: int, *, granularity: str = "head",
                                  out_dtype: torch.dtype = torch.bfloat16,
@@ -301,27 +310,51 @@ def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: to
     ``_per_tensor_fp8`` returns them), V either in the kernel's tile layout (1-D, as
     ``qk_norm_rope_quant_e4m3`` returns it) or as (B, H, T, D) codes (permuted into the tile layout
     first, one pass), scales [3 * groups] (q, k, v) float32 on the device.
-    ``out``: optional (B, H, T, D) destination of ``out_dtype`` with D contiguous."""
+    ``out``: optional (B, H, T, D) destination of ``out_dtype`` with D contiguous.
+
+    The kernel is given only B, H, T, D and strides, so every operand's shape, dtype and size is
+    checked here against q8's before anything is launched (ValueError otherwise)."""
     lib = _lib.load()
-    _lib.require_gpu(q8, k8, v_tiles, scales)
-    q8, k8, v_tiles = (t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t for t in (q8, k8, v_tiles))
+    if q8.dim() != 4:
+        raise ValueError(f"expected (B, H, T, D), got {tuple(q8.shape)}")
     B, H, T, D = q8.shape
+    if D not in (32, 64, 128):
+        raise ValueError(f"head_dim must be 32/64/128 for the MFMA tiling, got {D}")
+    for name, t in (("q8", q8), ("k8", k8), ("v_tiles", v_tiles)):
+        if t.dtype not in _CODE_DTYPES:
+            raise ValueError(f"{name} must hold e4m3 codes (uint8 or float8_e4m3fn), got {t.dtype}")
+    if k8.shape != q8.shape:
+        raise ValueError(f"k8 {tuple(k8.shape)} does not match q8 {tuple(q8.shape)}")
+    if q8.stride(-1) != 1 or k8.stride(-1) != 1:
+        raise ValueError("q8 and k8 must be contiguous in their last dimension")
     if v_tiles.dim() == 4:
         if v_tiles.shape != q8.shape:
             raise ValueError(f"V codes {tuple(v_tiles.shape)} do not match Q's {tuple(q8.shape)}")
+    elif v_tiles.dim() != 1 or v_tiles.numel() != lib.flw_vtile_bytes(B, H, T, D) or not v_tiles.is_contiguous():
+        raise ValueError(f"v_tiles must be (B, H, T, D) codes or a contiguous 1-D tile buffer of "
+                         f"flw_vtile_bytes(B, H, T, D) = {lib.flw_vtile_bytes(B, H, T, D)} bytes, "
+                         f"got {tuple(v_tiles.shape)}")
+    G = _group_count(granularity, B, H)
+    if scales.numel() != 3 * G or scales.dtype != torch.float32 or not scales.is_contiguous():
+        raise ValueError(f"scales must be a contiguous float32 tensor of {3 * G} elements")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"out_dtype must be bfloat16 or float32, got {out_dtype}")
+    if out is not None and (out.shape != (B, H, T, D) or out.stride(-1) != 1 or out.dtype != out_dtype):
+        raise ValueError(f"out must be a (B, H, T, D) tensor of {out_dtype} with D contiguous")
+    devices = {t.device for t in (q8, k8, v_tiles, scales) + ((out,) if out is not None else ())}
+    if len(devices) != 1:
+        raise ValueError(f"all operands must be on one device, got {sorted(map(str, devices))}")
+    _lib.require_gpu(q8, k8, v_tiles, scales)
+    q8, k8, v_tiles = (t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t for t in (q8, k8, v_tiles))
+    if v_tiles.dim() == 4:
         v4 = v_tiles if v_tiles.stride(-1) == 1 and all(s % 16 == 0 for s in v_tiles.stride()[:3]) \
             else v_tiles.contiguous()
         v_tiles = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device=q8.device)
         rc = lib.flw_vtile_from_bhtd(v4.data_ptr(), B, H, T, D, *v4.stride()[:3], v_tiles.data_ptr(),
                                      _lib.stream_of(q8))
         _lib.check(rc, "fp8_swa_attention_from_codes (V layout)")
-    G = {"tensor": 1, "head": H, "bh": B * H}[granularity]
-    if scales.numel() != 3 * G or scales.dtype != torch.float32 or not scales.is_contiguous():
-        raise ValueError(f"scales must be a contiguous float32 tensor of {3 * G} elements")
     if out is None:
         out = torch.empty((B, H, T, D), dtype=out_dtype, device=q8.device)
-    elif out.shape != (B, H, T, D) or out.stride(-1) != 1:
-        raise ValueError("out must be a (B, H, T, D) tensor with D contiguous")
     s8 = _lib.i64s(*q8.stride()[:3])
     sk = _lib.i64s(*k8.stride()[:3])
     base = scales.data_ptr()

@@ -1,4 +1,5 @@
-"""CPU: the C-ABI library loads and exports exactly what include/flower_amd.h declares."""
+"""CPU: the C-ABI library loads and exports exactly what include/flower_amd.h declares; the
+diagnostics library (flower_amd/csrc/diag/flw_diag.h) is separate and exports what it declares."""
 
 import ctypes
 import os
@@ -8,6 +9,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "flower_amd.h")
+DIAG_HEADER = os.path.join(ROOT, "flower_amd", "csrc", "diag", "flw_diag.h")
 
 
 def _gpu_visible() -> bool:
@@ -21,8 +23,8 @@ def _gpu_visible() -> bool:
 fake_pointers = pytest.mark.skipif(_gpu_visible(), reason="passes fake device pointers: CPU-only host check")
 
 
-def declared_functions():
-    text = open(HEADER).read()
+def declared_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(flw_\w+)\s*\(", text, flags=re.M)))
 
@@ -44,6 +46,22 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in include/flower_amd.h but not exported"
     # the Python binding types exactly the declared set
     assert set(_lib.SIGNATURES) == set(declared_functions())
+    # measurement instruments are not part of the product library
+    assert not any(n.startswith("flw_diag") for n in declared_functions())
+    for name in ("flw_diag_issue_probe", "flw_diag_cvt_e4m3", "flw_diag_quotient", "flw_diag_mfma_e4m3_dot"):
+        assert not hasattr(lib, name), f"{name} leaked into the product library"
+
+
+def test_diagnostics_library_exports_what_its_header_declares():
+    from flower_amd import _lib
+    if not os.path.exists(_lib.DIAG_LIB_PATH):
+        pytest.skip("libflower_amd_diag.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(_lib.DIAG_LIB_PATH)
+    names = declared_functions(DIAG_HEADER)
+    assert "flw_diag_issue_probe" in names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in flw_diag.h but not exported"
+    assert set(_lib.DIAG_SIGNATURES) == set(names)
 
 
 @fake_pointers
@@ -141,9 +159,9 @@ def test_limits_and_empty_shapes_are_refused_on_the_host():
 @fake_pointers
 def test_issue_probe_refuses_bad_arguments_on_the_host():
     from flower_amd import _lib
-    if not os.path.exists(_lib.LIB_PATH):
-        pytest.skip("libflower_amd.so not built")
-    lib = _lib.load()
+    if not os.path.exists(_lib.DIAG_LIB_PATH):
+        pytest.skip("libflower_amd_diag.so not built")
+    lib = _lib.load_diag()
     assert lib.flw_diag_issue_probe_iters() > 0
     fake = 1 << 20
     assert lib.flw_diag_issue_probe(1, None, 256, 1, None) == 1           # null out
@@ -156,9 +174,9 @@ def test_issue_probe_refuses_bad_arguments_on_the_host():
 @fake_pointers
 def test_mfma_dot_probe_refuses_bad_arguments_on_the_host():
     from flower_amd import _lib
-    if not os.path.exists(_lib.LIB_PATH):
-        pytest.skip("libflower_amd.so not built")
-    lib = _lib.load()
+    if not os.path.exists(_lib.DIAG_LIB_PATH):
+        pytest.skip("libflower_amd_diag.so not built")
+    lib = _lib.load_diag()
     f = 1 << 20
     assert lib.flw_diag_mfma_e4m3_dot(None, f, None, None, f, 1, 0, None) == 1        # null A
     assert b"null operand" in lib.flw_last_error()
@@ -182,3 +200,21 @@ def test_scale_strides_are_validated_on_the_host():
     assert rc == 1 and b"scale strides" in lib.flw_last_error()
     rc = lib.flw_fp8_swa_fwd(P, s64, P, s64, P, P, P, P, 7, P, 1, s64, 1, 1, 64, 64, 16, None)
     assert rc == 1 and b"granularity" in lib.flw_last_error()
+
+
+@fake_pointers
+def test_noalloc_quantiser_refuses_shapes_beyond_its_scratch():
+    """3 tensors x B*H*ceil(T/128) partials x 4 bytes: B1 H64 T1,048,576 needs 6 MiB against the
+    1 MiB scratch array, refused on the host before the scratch address is even looked up."""
+    from flower_amd import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = L.load()
+    assert lib.flw_noalloc_scratch_bytes() == 1 << 20
+    P = 1 << 20
+    strides = L.i64s(*([64 * 1048576 * 64, 1048576 * 64, 64] * 3))
+    rc = lib.flw_quant_qkv_e4m3_noalloc(P, P, P, L.BF16, 1, 64, 1048576, 64, strides, L.SCALE_HEAD,
+                                        P, P, P, P, None)
+    assert rc == 2 and b"scratch" in lib.flw_last_error()
+    rc = lib.flw_quant_qkv_e4m3_noalloc(P, P, P, L.BF16, 0, 64, 128, 64, strides, L.SCALE_HEAD, P, P, P, P, None)
+    assert rc == 1 and b"empty" in lib.flw_last_error()

@@ -73,3 +73,41 @@ def test_qkv_heads_is_the_reference_pipeline():
         n = norm(src)
         torch.testing.assert_close(got, n * cos + rot(n) * sin)
     torch.testing.assert_close(v, vs)
+
+
+def test_attention_from_codes_refuses_mismatched_operands_on_the_host():
+    """fp8_swa_attention_from_codes hands the kernel only q8's B, H, T, D and strides, so every
+    other operand is checked against q8 before any launch (CPU tensors: the refusals come before
+    the GPU check, nothing reaches the library's kernels)."""
+    import os
+    from flower_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_from_codes as f
+    B, H, T, D = 1, 2, 100, 64
+    lib = _lib.load()
+    q8 = torch.zeros(B, H, T, D, dtype=torch.uint8)
+    vt = torch.zeros(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8)
+    sc = torch.ones(3 * H)
+    with pytest.raises(ValueError, match="k8"):
+        f(q8, torch.zeros(B, H, T - 1, D, dtype=torch.uint8), vt, sc, 16)            # shorter K
+    with pytest.raises(ValueError, match="e4m3 codes"):
+        f(q8, q8.to(torch.int8), vt, sc, 16)                                          # wrong code dtype
+    with pytest.raises(ValueError, match="e4m3 codes"):
+        f(q8.float(), q8, vt, sc, 16)
+    with pytest.raises(ValueError, match="tile buffer"):
+        f(q8, q8, vt[:-64], sc, 16)                                                   # undersized V tiles
+    with pytest.raises(ValueError, match="V codes"):
+        f(q8, q8, torch.zeros(B, H, T + 1, D, dtype=torch.uint8), sc, 16)             # V of another T
+    with pytest.raises(ValueError, match="out must be"):
+        f(q8, q8, vt, sc, 16, out=torch.empty(B, H, T, D, dtype=torch.float32))       # out dtype != out_dtype
+    with pytest.raises(ValueError, match="granularity"):
+        f(q8, q8, vt, sc, 16, granularity="row")
+    with pytest.raises(ValueError, match="scales"):
+        f(q8, q8, vt, torch.ones(3), 16)                                              # per-tensor count for "head"
+    with pytest.raises(ValueError, match="head_dim"):
+        f(torch.zeros(B, H, T, 48, dtype=torch.uint8), q8, vt, sc, 16)
+    with pytest.raises(ValueError, match="out_dtype"):
+        f(q8, q8, vt, sc, 16, out_dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU"):                                    # consistent: only then the GPU check
+        f(q8, q8, vt, sc, 16)

@@ -1,6 +1,7 @@
 """GPU: the FP8 decoder block of BASELINE config 5 (flower_amd/block.py), composed from the
 C-ABI kernels, against the same block in plain fp32 torch (the reference's TransformerBlock maths,
-base.py:698-722) and, for the attention stage, against the CPU oracle.
+base.py:698-722, with the attention's HeadRMSNorm and RoPE of qkv_heads, base.py:618-639) and, for
+the attention stage, against the CPU oracle.
 
 Gates (written here; FP8 e4m3 is far coarser than the fp32 reference):
   - block update delta = out - x vs fp32: Frobenius relative error < 0.1 (each FP8 linear adds
@@ -14,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import rel_errors, to_np
+from gpu_util import rel_errors, to_np, vtile_permute
 from oracle.quant import per_tensor_fp8
 from oracle.swa import fp8_swa_simulate
 
@@ -31,7 +32,8 @@ def make_block(seed=0):
 
 
 def fp32_reference(blk, x):
-    """The same block in fp32 torch: RMSNorm, qkv, masked softmax attention, out, GELU MLP."""
+    """The same block in fp32 torch: RMSNorm, qkv, HeadRMSNorm of q and k, RoPE (fp32 tables),
+    masked softmax attention, out, GELU MLP."""
     def rms(mod, t):
         return t * t.pow(2).mean(-1, keepdim=True).add(mod.eps).rsqrt() * mod.weight.float()
     B, T, d = x.shape
@@ -40,6 +42,12 @@ def fp32_reference(blk, x):
     h = rms(blk.ln1, x)
     q, k, v = (h @ blk.attn.qkv.weight.float().t()).chunk(3, dim=-1)
     q, k, v = (t.reshape(B, T, H, D).transpose(1, 2).contiguous() for t in (q, k, v))
+    q, k = (t * t.pow(2).mean(-1, keepdim=True).add(blk.attn.qk_norm.eps).rsqrt() for t in (q, k))
+    cos, sin = (t.to(x.device) for t in blk.attn.rope._tables(T))
+
+    def rot(t):
+        return torch.stack((-t[..., 1::2], t[..., ::2]), dim=-1).flatten(-2)
+    q, k = q * cos + rot(q) * sin, k * cos + rot(k) * sin
     s = (q @ k.transpose(-1, -2).contiguous()) / D ** 0.5
     i = torch.arange(T, device=x.device)
     keep = (i[:, None] >= i[None, :]) & ((i[:, None] - i[None, :]) < W)
@@ -72,9 +80,8 @@ def test_block_attention_stage_matches_oracle():
     x = torch.randn(B, T, CFG["d_model"], generator=g).to("cuda", torch.bfloat16)
     from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
     with torch.no_grad():
-        q, k, v = blk.attn.qkv(blk.ln1(x)).chunk(3, dim=-1)
-        q, k, v = (blk.attn._split(t) for t in (q, k, v))
-        assert not q.is_contiguous()                     # read in place through its strides
+        q, k, v = blk.attn.qkv_heads(blk.ln1(x))      # QK-norm and RoPE in torch ops (base.py:618-639)
+        assert not v.is_contiguous()                     # read in place through its strides
         out = fp8_swa_attention_forward(q, k, v, CFG["local_window"], granularity="head")
     torch.cuda.synchronize()
     codes = [per_tensor_fp8(to_np(t.contiguous()), "head") for t in (q, k, v)]
@@ -132,18 +139,22 @@ def test_config5_full_shape_stage_by_stage():
     from the FP8 weight cache (base.py:698-722 block, base.py:514-525 GELU MLP), fused forward.
     Each stage is checked on the kernels' own inputs:
       (i)   attention, two heads, against the oracle's FP8 simulator on the oracle's per-head codes
-            of the block's own q / k / v (the QKV output);
+            of the block's own q', k', v (QK-normed and rotated as in (iv));
       (ii)  256 sampled rows of every linear (QKV, O + residual, FF1, FF2 + residual) against the
             float64 closed form on the kernel's codes and scales (rounded to bf16, then the
             residual added in bf16);
       (iii) the RMSNorm, attention-output and GELU row quantisers: codes and scales bit-exact
             against the per-row recipe on their own h, and h within 1 bf16 ulp of the oracle's
             RMSNorm / GELU on the sampled rows;
-      (iv)  the QKV epilogue's per-head maxima equal to max |q|, |k|, |v| of its own output.
+      (iv)  the attention's quantisation point (qkv_heads, base.py:618-639): the fused quantiser's
+            QK-normed and rotated q', k' against the oracle's HeadRMSNorm + RoPE of the QKV output
+            on the sampled rows (the per-value bounds of the fused-quantiser tests), and its e4m3
+            codes and per-head scales of q', k', v bit-exact against the per-head recipe on the
+            whole tensors (so the maxima are those of the transformed tensors).
     The traced call returns the same bits as the untraced one."""
     from flower_amd.block import Fp8DecoderBlock, init_block_
     from flower_amd.precision import fp8_weight_cache
-    from oracle.block import gelu, rmsnorm
+    from oracle.block import gelu, head_rmsnorm, rmsnorm, rope
     from oracle.e4m3 import round_bf16
     from oracle.gemm import scaled_mm
     from oracle.quant import rowwise_fp8
@@ -162,7 +173,6 @@ def test_config5_full_shape_stage_by_stage():
         wq = [lin.weight_codes() for lin in blk._linears()]
         torch.cuda.synchronize()
     assert torch.equal(out, plain)
-    assert tr["amax"] is not None                       # the producer-amax route is the one tested
 
     rows = np.sort(np.random.default_rng(57).choice(M, 256, replace=False))
     ridx = torch.from_numpy(rows).cuda()
@@ -170,10 +180,27 @@ def test_config5_full_shape_stage_by_stage():
     x2 = x.view(M, d)
     w8 = [(to_np(w.view(torch.uint8)), to_np(s)) for w, s in wq]
 
-    # (iv) per-head maxima of the QKV output, bit for bit (bf16 values as fp32 patterns)
+    # (iv) the quantisation point: q', k' on sampled rows against the oracle's transform of the QKV
+    # output; codes and per-head scales of q', k', v bit-exact on the whole tensors
     qkv = tr["qkv"].view(M, 3 * d)
-    want_amax = qkv.view(M, 3 * H, D).float().abs().amax(dim=(0, 2))
-    assert torch.equal(tr["amax"], want_amax.view(torch.int32))
+    cos, sin = (to_np(t) for t in blk.attn.rope.tables(T, torch.bfloat16, "cuda"))
+    raw = cpu(qkv).reshape(len(rows), 3, H, D)
+    pos = rows % T
+    for i, name in enumerate(("q", "k")):
+        want = rope(head_rmsnorm(raw[:, i], blk.attn.qk_norm.eps, "bf16"), cos[pos][:, None], sin[pos][:, None], "bf16")
+        got = to_np(tr[name].transpose(1, 2).reshape(M, H, D).index_select(0, ridx))
+        d_ = np.abs(got.astype(np.float64) - want)
+        assert (d_ > 0).mean() < 2e-3 and (d_ <= 2.0 ** -7 * (np.abs(want) + 1.0)).all(), (name, float(d_.max()))
+    vv = blk.attn._split(tr["qkv"].chunk(3, dim=-1)[2])
+    quant = []
+    for i, (vals, codes) in enumerate(((tr["q"], tr["q8"]), (tr["k"], tr["k8"]), (vv, None))):
+        c_, s_ = per_tensor_fp8(to_np(vals.contiguous()), "head")
+        quant.append((c_, s_))
+        if codes is not None:
+            assert np.array_equal(to_np(codes), c_), i
+        assert np.array_equal(to_np(tr["scales"][i * H:(i + 1) * H]).view(np.uint32),
+                              np.asarray(s_, np.float32).reshape(-1).view(np.uint32)), i
+    np.testing.assert_array_equal(to_np(tr["v_tiles"]), vtile_permute(quant[2][0]))
 
     # (iii) row quantisers: codes / scales on their own h; h against the oracle on sampled rows
     for c, s, h in (("c1", "s1", "h1"), ("c2", "s2", "h2"), ("cg", "sg", "hg")):
@@ -206,9 +233,7 @@ def test_config5_full_shape_stage_by_stage():
                + 1e-3 * np.sqrt(np.mean(prod.astype(np.float64) ** 2)))
         assert (np.abs(y - ref) <= tol).all(), (yname, float(np.abs(y - ref).max()))
 
-    # (i) attention on the block's own q / k / v, two heads, per-head codes of the whole tensor
-    q, k, v = (blk.attn._split(t) for t in tr["qkv"].chunk(3, dim=-1))
-    quant = [per_tensor_fp8(to_np(t.contiguous()), "head") for t in (q, k, v)]
+    # (i) attention on the block's own q' / k' / v codes (checked above), two heads
     attn = to_np(tr["attn"].view(B, T, H, D).transpose(1, 2))
     for h in (2, 11):
         sl = slice(h, h + 1)

@@ -18,11 +18,11 @@ MASKS = [1, 2, 4, 8, 16, 32, 64, 65, 66, 68, 72, 80, 3, 67]
 def _time(lib, mask, out, blocks):
     from flower_amd import _lib
     stream = torch.cuda.current_stream().cuda_stream
-    _lib.check(lib.flw_diag_issue_probe(mask, out.data_ptr(), out.numel(), blocks, stream), "probe")
+    _lib.check(lib.flw_diag_issue_probe(mask, out.data_ptr(), out.numel(), blocks, stream), "probe", lib)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    _lib.check(lib.flw_diag_issue_probe(mask, out.data_ptr(), out.numel(), blocks, stream), "probe")
+    _lib.check(lib.flw_diag_issue_probe(mask, out.data_ptr(), out.numel(), blocks, stream), "probe", lib)
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1)
@@ -30,7 +30,7 @@ def _time(lib, mask, out, blocks):
 
 def test_issue_probe_masks_and_orderings():
     from flower_amd import _lib
-    lib = _lib.load()
+    lib = _lib.load_diag()
     blocks = 4 * torch.cuda.get_device_properties(0).multi_processor_count
     out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
     ms = {m: _time(lib, m, out, blocks) for m in MASKS}
@@ -56,7 +56,7 @@ def _mfma_products(lib, A, B, A2=None, B2=None):
     ta2, tb2 = (frag(A2, True), frag(B2, False)) if chain else (ta, tb)
     d = torch.empty((n, 1024), dtype=torch.float32, device="cuda")
     _lib.check(lib.flw_diag_mfma_e4m3_dot(ta.data_ptr(), tb.data_ptr(), ta2.data_ptr(), tb2.data_ptr(), d.data_ptr(),
-                                          n, int(chain), torch.cuda.current_stream().cuda_stream), "mfma dot")
+                                          n, int(chain), torch.cuda.current_stream().cuda_stream), "mfma dot", lib)
     torch.cuda.synchronize()
     raw = d.cpu().numpy()
     D = np.empty((n, 32, 32), np.float32)
@@ -71,7 +71,7 @@ def test_mfma_e4m3_dot_layout_is_exact_on_small_integers():
     diagnostic's fragment layout and the MFMA give the exact products, single and chained."""
     from flower_amd import _lib
     from oracle.e4m3 import f32_to_e4m3
-    lib = _lib.load()
+    lib = _lib.load_diag()
     rng = np.random.default_rng(11)
     mk = lambda shape: f32_to_e4m3(rng.integers(-2, 3, size=shape).astype(np.float32))  # noqa: E731
     dec = lambda c: e4m3_to_f32(c).astype(np.float64)  # noqa: E731
@@ -90,7 +90,7 @@ def test_mfma_e4m3_accumulation_error_is_bounded(chain):
     product of each 64-deep (or chained 128-deep) dot."""
     from flower_amd import _lib
     from oracle.e4m3 import f32_to_e4m3
-    lib = _lib.load()
+    lib = _lib.load_diag()
     rng = np.random.default_rng(12)
     dec = lambda c: e4m3_to_f32(c).astype(np.float64)  # noqa: E731
 

@@ -270,7 +270,7 @@ def test_fp8_lm_head_matches_bf16_head(shift):
     reference's bounds (test_training_speedups.py:359-412: relative Frobenius < 0.05, norm ratio in
     (0.9, 1.1), next-token CE within 0.1; the -2.5 shift is its all-negative-rows regression),
     and sampled rows against the oracle's closed form on the same codes."""
-    from flower_amd.lm_head import compute_logits, fp8_head
+    from flower_amd.precision import compute_logits, fp8_head
     from oracle.quant import rowwise_fp8
     torch.manual_seed(0)
     vocab, d, B, T = 16384, 1024, 2, 64

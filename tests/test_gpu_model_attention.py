@@ -59,12 +59,16 @@ def _check_transform(got, want, dtype, normed):
         assert (d <= 1e-6 * (np.abs(want) + 1.0)).all(), float(d.max())
 
 
+@pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("gran", ["head", "tensor", "bh"])
 @pytest.mark.parametrize("qk_norm,use_rope", [(True, True), (False, True), (True, False)])
-def test_fused_quantiser_against_oracle(qk_norm, use_rope, gran, dtype):
+def test_fused_quantiser_against_oracle(qk_norm, use_rope, gran, dtype, D):
+    """Every head_dim the entry point accepts: the HeadRMSNorm row sum is reduced over D / N lanes
+    (4 / 8 / 16 lanes for bf16 at D = 32 / 64 / 128, 8 / 16 / 32 for fp32) and the RoPE tables are
+    indexed per D, so each width is its own case."""
     from flower_amd.kernels import qk_norm_rope_quant_e4m3
-    B, T, H, D = 2, 300, 4, 64
+    B, T, H = 2, 300, 4
     name = "bf16" if dtype == torch.bfloat16 else "f32"
     g = torch.Generator().manual_seed(71)
     scale = torch.randn(1, 1, 3 * H, 1, generator=g).exp()

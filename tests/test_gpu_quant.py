@@ -29,7 +29,7 @@ def test_hw_fp8_convert_is_exact_on_the_attention_P_range():
     """v_cvt_pk_fp8_f32 (used for P * 448 in the attention kernel) against the library's exact
     rounding, on EVERY fp32 value in [0, 448 * (1 + 2^-20)], compared on the device."""
     L = lib()
-    lb = L.load()
+    lb = L.load_diag()
     hi = int(np.array([448.0], np.float32).view(np.int32)[0]) + 16
     chunk = 1 << 26
     bad = 0
@@ -40,8 +40,8 @@ def test_hw_fp8_convert_is_exact_on_the_attention_P_range():
         hw = torch.empty(n, dtype=torch.uint8, device="cuda")
         sw = torch.empty(n, dtype=torch.uint8, device="cuda")
         s = L.stream_of(x)
-        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), hw.data_ptr(), n, 1, s), "hw")
-        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), sw.data_ptr(), n, 0, s), "sw")
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), hw.data_ptr(), n, 1, s), "hw", lb)
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), sw.data_ptr(), n, 0, s), "sw", lb)
         bad += int((hw != sw).sum())
     assert bad == 0, f"{bad} hardware conversions differ from exact RNE"
 
@@ -50,7 +50,7 @@ def test_hw_fp8_convert_is_exact_on_negative_quantiser_range():
     """The quantisers feed v_cvt_pk_fp8_f32 quotients in [-448 (1 + 2^-20), 448 (1 + 2^-20)]:
     the negative half, EVERY fp32 value, against the exact rounding."""
     L = lib()
-    lb = L.load()
+    lb = L.load_diag()
     hi = int(np.array([448.0], np.float32).view(np.int32)[0]) + 16
     chunk = 1 << 26
     bad = 0
@@ -62,20 +62,20 @@ def test_hw_fp8_convert_is_exact_on_negative_quantiser_range():
         hw = torch.empty(n, dtype=torch.uint8, device="cuda")
         sw = torch.empty(n, dtype=torch.uint8, device="cuda")
         s = L.stream_of(x)
-        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), hw.data_ptr(), n, 1, s), "hw")
-        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), sw.data_ptr(), n, 0, s), "sw")
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), hw.data_ptr(), n, 1, s), "hw", lb)
+        L.check(lb.flw_diag_cvt_e4m3(x.data_ptr(), sw.data_ptr(), n, 0, s), "sw", lb)
         bad += int((hw != sw).sum())
     assert bad == 0, f"{bad} hardware conversions differ from exact RNE"
 
 
 def _quotients(x, scales, mode):
     L = lib()
-    lb = L.load()
+    lb = L.load_diag()
     xt = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
     st = torch.from_numpy(np.ascontiguousarray(scales, np.float32)).cuda()
     out = torch.empty(x.size * scales.size, dtype=torch.int32, device="cuda")
     L.check(lb.flw_diag_quotient(xt.data_ptr(), x.size, st.data_ptr(), scales.size, out.data_ptr(),
-                                 mode, L.stream_of(xt)), "quotient")
+                                 mode, L.stream_of(xt)), "quotient", lb)
     return out
 
 
@@ -135,7 +135,7 @@ def test_device_exact_rounding_matches_oracle():
     """The device's software e4m3 rounding (used by the quantisers) vs the oracle, on random
     bit patterns, every e4m3 midpoint +-4 ulp, NaN and inf."""
     L = lib()
-    lb = L.load()
+    lb = L.load_diag()
     from test_oracle_e4m3 import _boundaries
     pts = _boundaries()
     u = pts.view(np.int32).astype(np.int64)
@@ -145,7 +145,7 @@ def test_device_exact_rounding_matches_oracle():
     x = np.concatenate([cand, rnd, np.array([np.nan, -np.nan, np.inf, -np.inf], np.float32)])
     xt = torch.from_numpy(x).cuda()
     out = torch.empty(x.size, dtype=torch.uint8, device="cuda")
-    L.check(lb.flw_diag_cvt_e4m3(xt.data_ptr(), out.data_ptr(), x.size, 0, L.stream_of(xt)), "sw")
+    L.check(lb.flw_diag_cvt_e4m3(xt.data_ptr(), out.data_ptr(), x.size, 0, L.stream_of(xt)), "sw", lb)
     np.testing.assert_array_equal(out.cpu().numpy(), f32_to_e4m3(x))
 
 

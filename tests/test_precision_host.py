@@ -97,6 +97,18 @@ def test_convert_swaps_only_eligible_layers_and_keeps_parameters():
     assert {id(p) for p in m.parameters()} == params_before
 
 
+def test_default_recipe_is_the_references_tensorwise():
+    """convert_model_to_fp8(model) with no recipe, maybe_convert_fp8 with a config that carries none,
+    and a bare Fp8Linear all take "tensorwise" (precision.py:137, config.py:593)."""
+    m, info = convert_model_to_fp8(_Tiny(), verbose=False)
+    assert info["fp8_recipe"] == "tensorwise"
+    assert m.blocks[1]["qkv"].recipe == "tensorwise" and m.blocks[2]["qkv"].recipe == "tensorwise"
+    assert Fp8Linear(32, 32).recipe == "tensorwise"
+    assert Fp8Linear.from_linear(nn.Linear(32, 32)).recipe == "tensorwise"
+    m2, info2 = convert_model_to_fp8(_Tiny(), recipe="rowwise", verbose=False)
+    assert info2["fp8_recipe"] == "rowwise" and m2.blocks[1]["qkv"].recipe == "rowwise"
+
+
 def test_convert_refuses_models_without_blocks_and_unknown_recipes():
     with pytest.raises(RuntimeError, match="no `blocks`"):
         convert_model_to_fp8(nn.Sequential(nn.Linear(16, 16)), verbose=False)
@@ -124,5 +136,5 @@ def test_weight_cache_is_a_no_op_without_fp8_layers():
     m = nn.Sequential(nn.Linear(8, 8))
     before = m[0].forward
     with fp8_weight_cache(m) as c:
-        assert c._layers == []
+        assert c.entries == []
     assert m[0].forward == before
