@@ -71,6 +71,11 @@ SIGNATURES = {
     "flw_fp8_swa_fwd_qx": (c_int, [c_void_p, _P64, c_void_p, c_void_p, c_void_p, _P64, c_void_p, c_void_p,
                                    c_void_p, c_void_p, c_int, c_void_p, c_int, _P64, c_int64, c_int64, c_int64,
                                    c_int64, c_int64, c_void_p]),
+    "flw_fp8_swa_fwd_lse": (c_int, [c_void_p, _P64, c_void_p, _P64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                    c_int, c_void_p, c_int, _P64, c_int64, c_int64, c_int64, c_int64,
+                                    c_int64, c_void_p, c_void_p]),
+    "flw_dequant_e4m3": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p,
+                                 c_int, c_void_p]),
     "flw_quant_qkv_e4m3_deferq": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                           c_int64, _P64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                           c_void_p, c_size_t, c_void_p]),
@@ -92,6 +97,10 @@ SIGNATURES = {
                                c_int64, c_int, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     "flw_fp8_scaled_mm_group_amax": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                              c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "flw_fp8_scaled_mm_qk_norm_rope_amax": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p,
+                                                    c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+                                                    c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
+                                                    c_void_p, c_void_p]),
     "flw_fp8_scaled_mm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "flw_fp8_scaled_mm_ws": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                      c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),

@@ -12,7 +12,9 @@
                            "fp8" routes the heads through the FP8 sliding-window kernel, with the
                            QK-norm, RoPE and the e4m3 quantisation of Q/K/V fused in one HIP pass
                            pair (the reference's quantisation point, "after QK-norm and RoPE",
-                           base.py:634-637); "bf16" through the HIP bf16 sliding-window kernel.
+                           base.py:634-637) -- and, in training, through the differentiable FP8
+                           attention (bf16 backward, straight-through quantisers); "bf16"
+                           through the HIP bf16 sliding-window kernel.
 ``fp8_attention``       -- the FP8 route on (B, H, T, D) Q/K/V that are already normed and rotated.
 """
 
@@ -22,8 +24,8 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .kernels.fp8_swa_attention import (fp8_swa_attention_forward, fp8_swa_attention_from_codes,
-                                        qk_norm_rope_quant_e4m3)
+from .kernels.fp8_swa_attention import (fp8_swa_attention, fp8_swa_attention_forward,
+                                        fp8_swa_attention_from_codes, qk_norm_rope_quant_e4m3)
 from .kernels.swa_attention import swa_attention
 
 
@@ -157,12 +159,15 @@ class CausalSelfAttention(nn.Module):
     ("bf16" | "fp8", config.py:373; validated as config.py:464-465), plus this build's
     ``fp8_attention_granularity`` ("head" by default: one e4m3 scale per head for each of Q, K, V).
 
-    attn_precision "fp8": forward-only, like the FP8 kernel (fp8_swa_attention.py:230-234: raises
-    RuntimeError if gradients would be needed). The qkv projection, then ONE HIP pass pair that
-    applies QK-norm and RoPE to q and k and quantises q', k', v to e4m3 (the reference's
+    attn_precision "fp8", inference (no gradient needed): the qkv projection, then ONE HIP pass pair
+    that applies QK-norm and RoPE to q and k and quantises q', k', v to e4m3 (the reference's
     quantisation point, base.py:634-637, "exactly the tensors a real FP8 attention kernel would
     consume"), then the FP8 sliding-window kernel writing the (B, T, H, D) output in place, then
     ``out``. ``forward_unfused`` is the same route with the heads built by ``qkv_heads`` in torch.
+    attn_precision "fp8", training (gradients needed): ``qkv_heads`` in torch (its QK-norm and RoPE
+    differentiate as usual), then the differentiable ``fp8_swa_attention`` -- the same FP8 forward,
+    and the bf16 sliding-window backward at the dequantised q', k', v (straight-through
+    quantisers, the estimator `_fake_quant_e4m3` trains with), then ``out``.
     attn_precision "bf16": ``qkv_heads`` then the differentiable HIP bf16 sliding-window kernel
     (a full causal window when ``local_window`` is None). The reference's flex / SDPA choice and
     its RBF distance bias (local_attn_kernel_bias "rbf") are not offered: rbf raises ValueError.
@@ -209,14 +214,19 @@ class CausalSelfAttention(nn.Module):
             q, k, v = _fake_quant_e4m3(q), _fake_quant_e4m3(k), _fake_quant_e4m3(v)
         return q, k, v
 
-    def _check_forward_only(self, x: torch.Tensor) -> None:
-        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            raise RuntimeError(
-                "attn_precision='fp8' is forward-only and has no backward (fp8_swa_attention_forward); "
-                "run it under torch.no_grad() / inference_mode or with frozen parameters.")
+    def _needs_grad(self, x: torch.Tensor) -> bool:
+        return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+
+    def _forward_fp8_train(self, x: torch.Tensor) -> torch.Tensor:
+        """The differentiable FP8 route: qkv_heads in torch, fp8_swa_attention, out."""
+        q, k, v = self.qkv_heads(x)
+        out = fp8_swa_attention(q, k, v, self._window(x.shape[1]), granularity=self.fp8_granularity)
+        return self.out(out.transpose(1, 2).reshape(x.shape))
 
     def forward(self, x: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
         if self.attn_precision == "fp8":
+            if self._needs_grad(x):
+                return self._forward_fp8_train(x)
             return self._forward_fp8(x, trace)
         q, k, v = self.qkv_heads(x)
         out = swa_attention(q, k, v, self._window(x.shape[1]))
@@ -226,7 +236,6 @@ class CausalSelfAttention(nn.Module):
         """qkv -> fused QK-norm + RoPE + e4m3 quantisation -> FP8 SWA -> out. ``trace`` (a dict,
         for checks) receives the projection "qkv", the transformed "q" / "k", the codes and scales,
         and the attention output "attn"."""
-        self._check_forward_only(x)
         B, T, d = x.shape
         y = self.qkv(x)
         q, k, v = (self._split(t) for t in y.chunk(3, dim=-1))
@@ -245,8 +254,10 @@ class CausalSelfAttention(nn.Module):
 
     def forward_unfused(self, x: torch.Tensor) -> torch.Tensor:
         """The FP8 route composed from the reference's pieces: ``qkv_heads`` in torch, then
-        ``fp8_swa_attention_forward`` (its own quantisation), then ``out``."""
-        self._check_forward_only(x)
+        ``fp8_swa_attention_forward`` (its own quantisation), then ``out``; with gradients needed,
+        the differentiable route."""
+        if self._needs_grad(x):
+            return self._forward_fp8_train(x)
         q, k, v = self.qkv_heads(x)
         out = fp8_swa_attention_forward(q, k, v, self._window(x.shape[1]), granularity=self.fp8_granularity)
         return self.out(out.transpose(1, 2).reshape(x.shape))

@@ -34,7 +34,8 @@ import torch.nn as nn
 
 from . import _lib
 from .attention import CausalSelfAttention
-from .kernels.fp8_swa_attention import fp8_swa_attention_from_codes, qk_norm_rope_quant_e4m3
+from .kernels.fp8_swa_attention import (fp8_swa_attention_forward, fp8_swa_attention_from_codes,
+                                        qk_norm_rope_quant_e4m3)
 from .precision import Fp8Linear
 
 
@@ -95,6 +96,9 @@ class Fp8DecoderBlock(nn.Module):
                                            max_seq_len=max_seq_len)
         self.ln2 = RMSNorm(d_model)
         self.ff = Fp8FeedForward(d_model, ffn_dim, bias=bias, recipe=recipe)
+        # Fused path: QK-norm, RoPE and the per-head maxima in the QKV GEMM's epilogue (True) or in
+        # the Q / K / V quantiser's pass pair (False); the two give the same q', k' bit for bit.
+        self.fuse_qk_epilogue = True
 
     @torch.no_grad()
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -123,7 +127,8 @@ class Fp8DecoderBlock(nn.Module):
     def _forward_fused(self, x: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
         """The same block with the work around the FP8 GEMMs fused into the library's kernels:
         RMSNorm -> per-row e4m3 in one pass (flw_rmsnorm_quant_rows_e4m3), QK-norm + RoPE + the
-        Q / K / V e4m3 in one pass pair (flw_qk_norm_rope_quant_e4m3), the attention writing
+        per-head maxima in the QKV GEMM's epilogue (flw_fp8_scaled_mm_qk_norm_rope_amax) and the
+        Q / K / V e4m3 from those maxima (Q on load in the attention kernel), the attention writing
         its (B, T, H, D) output in place, the residual adds in the GEMM epilogues
         (flw_fp8_scaled_mm_residual), GELU -> per-row e4m3 in one pass (flw_gelu_quant_rows_e4m3).
         Every rounding step of the unfused composition is kept (bf16 norm / GELU outputs, bf16
@@ -132,9 +137,11 @@ class Fp8DecoderBlock(nn.Module):
         ``trace`` (a dict, for stage-by-stage checks): receives every intermediate of the call --
         the row codes / scales of each linear's input ("c1"/"s1", "ca"/"sa", "c2"/"s2",
         "cg"/"sg"), the normed / activated rows the fused quantisers also write out when tracing
-        ("h1", "h2", "hg"), the QKV output "qkv", the QK-normed and rotated "q" / "k", the attention
-        operands "q8" / "k8" / "v_tiles" / "scales", the attention output "attn", "x1" and the FF1
-        output "f". The kernels and the result are the same."""
+        ("h1", "h2", "hg"), the QKV output "qkv" (with the epilogue: q' and k' already QK-normed
+        and rotated), the QK-normed and rotated "q" / "k" heads, with the epilogue the per-head
+        maxima "amax" of q', k', v, without it the attention operands "q8" / "k8" / "v_tiles" /
+        "scales"; the attention output "attn", "x1" and the FF1 output "f". The kernels and the
+        result are the same."""
         lib = _lib.load()
         B, T, d = x.shape
         M = B * T
@@ -180,28 +187,50 @@ class Fp8DecoderBlock(nn.Module):
 
         att = self.attn
         c1, s1 = codes_of("rmsnorm", x2, d, self.ln1, "h1")
-        qkv = linear(c1, s1, qkv_l).view(B, T, 3 * d)
-        # The quantisation point of qkv_heads (base.py:630-637): HeadRMSNorm and RoPE of q, k and the
-        # three e4m3 quantisations in one pass pair over the strided head views of the projection.
-        q, k, v = (att._split(t) for t in qkv.chunk(3, dim=-1))
-        cos, sin = att.rope.tables(T, qkv.dtype, dev)
-        res = qk_norm_rope_quant_e4m3(q, k, v, qk_norm=att.qk_norm is not None,
-                                      eps=att.qk_norm.eps if att.qk_norm is not None else 0.0,
-                                      rope_cos=cos, rope_sin=sin, granularity=att.granularity,
-                                      return_transformed=trace is not None)
-        q8, k8, vt, scales = res[:4]
+        cos, sin = att.rope.tables(T, torch.bfloat16, dev)
+        qk_norm = att.qk_norm is not None
+        eps = att.qk_norm.eps if qk_norm else 0.0
         a = torch.empty((B, T, d), dtype=torch.bfloat16, device=dev)
+        a_heads = a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2)
         window = T if att.local_window is None else att.local_window
-        fp8_swa_attention_from_codes(q8, k8, vt, scales, window, granularity=att.granularity,
-                                     out=a.view(B, T, att.num_heads, att.head_dim).transpose(1, 2))
+        if self.fuse_qk_epilogue and att.granularity == "head" and d % 128 == 0 and M * d < 2 ** 32 \
+                and 3 * d * d < 2 ** 32:
+            # The quantisation point of qkv_heads (base.py:630-637) in the QKV GEMM's epilogue: the q
+            # and k heads are QK-normed and rotated before they are stored, and the per-head maxima
+            # of q', k', v come with them, so the attention's quantiser runs only its quantise pass
+            # (K / V codes; Q is quantised on load by the attention kernel). The 256 x 256 GEMM
+            # (K % 128 == 0, operands < 2^32 bytes) carries this epilogue; other shapes take the
+            # quantiser pair below.
+            w8, ws = qkv_l.weight_codes()
+            N, K = w8.shape
+            qkv = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            amax = torch.empty(N // att.head_dim, dtype=torch.int32, device=dev)
+            _lib.check(lib.flw_fp8_scaled_mm_qk_norm_rope_amax(
+                c1.data_ptr(), M, K, w8.data_ptr(), N, s1.data_ptr(), M, ws.data_ptr(), ws.numel(), qkv.data_ptr(),
+                N, att.head_dim, 2 * d, int(qk_norm), float(eps), cos.data_ptr(), sin.data_ptr(), T, amax.data_ptr(),
+                stream), "qkv + qk-norm + rope + amax")
+            qkv = qkv.view(B, T, 3 * d)
+            q, k, v = (att._split(t) for t in qkv.chunk(3, dim=-1))
+            fp8_swa_attention_forward(q, k, v, window, granularity="head", out=a_heads, amax=amax)
+            if trace is not None:
+                trace.update(q=q, k=k, amax=amax)
+        else:
+            # HeadRMSNorm and RoPE of q, k and the three e4m3 quantisations in one pass pair over the
+            # strided head views of the projection.
+            qkv = linear(c1, s1, qkv_l).view(B, T, 3 * d)
+            q, k, v = (att._split(t) for t in qkv.chunk(3, dim=-1))
+            res = qk_norm_rope_quant_e4m3(q, k, v, qk_norm=qk_norm, eps=eps, rope_cos=cos, rope_sin=sin,
+                                          granularity=att.granularity, return_transformed=trace is not None)
+            fp8_swa_attention_from_codes(*res[:4], window, granularity=att.granularity, out=a_heads)
+            if trace is not None:
+                trace.update(q=res[4], k=res[5], q8=res[0], k8=res[1], v_tiles=res[2], scales=res[3])
         ca, sa = codes_of("plain", a.view(M, d), d)
         x1 = linear(ca, sa, out_l, residual=x2)
         c2, s2 = codes_of("rmsnorm", x1, d, self.ln2, "h2")
         f = linear(c2, s2, ff1_l)
         cg, sg = codes_of("gelu", f, f.shape[1], h_name="hg")
         if trace is not None:
-            trace.update(c1=c1, s1=s1, qkv=qkv, q=res[4], k=res[5], q8=q8, k8=k8, v_tiles=vt, scales=scales,
-                         attn=a, ca=ca, sa=sa, x1=x1, c2=c2, s2=s2, f=f, cg=cg, sg=sg)
+            trace.update(c1=c1, s1=s1, qkv=qkv, attn=a, ca=ca, sa=sa, x1=x1, c2=c2, s2=s2, f=f, cg=cg, sg=sg)
         return linear(cg, sg, ff2_l, residual=x1).view(B, T, d)
 
 

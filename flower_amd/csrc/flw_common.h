@@ -200,51 +200,103 @@ __device__ __forceinline__ float round_to(float x) {
   return x;
 }
 
+// Sum of x over an aligned group of `lanes` consecutive lanes (1, 2, 4, 8, 16 or 32), the same
+// bits in every lane of the group: quad butterflies (lane ^ 1, lane ^ 2) by DPP, then the mirrored
+// half row and row (lane 7 - i, 15 - i: the partner holds the other half's sum, and a + b == b + a),
+// then lane ^ 16. The pairing is ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) ... at every width.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float group_sum(float x, int lanes) {
+  if (lanes >= 2) x = x + dpp_f32<0xB1>(x);                        // quad_perm [1, 0, 3, 2]
+  if (lanes >= 4) x = x + dpp_f32<0x4E>(x);                        // quad_perm [2, 3, 0, 1]
+  if (lanes >= 8) x = x + dpp_f32<0x141>(x);                       // row_half_mirror
+  if (lanes >= 16) x = x + dpp_f32<0x140>(x);                      // row_mirror
+  if (lanes >= 32) x = x + __shfl_xor(x, 16, 64);
+  return x;
+}
+
 // The pre-attention transform of CausalSelfAttention.qkv_heads (flower/models/base.py:630-637) on
-// one lane's Vec16<T>::N consecutive values f of a head row of d values, every step rounded to the
-// tensor's dtype as the reference's torch ops round it:
-//   HeadRMSNorm (base.py:355-357, when `norm`): h = dtype(x * (1 / sqrt(mean(x^2) + eps))), fp32
-//     maths; the row's sum of squares is an fma chain over the lane's values, then a butterfly
-//     over the `lanes` lanes (an aligned power-of-two group, lane order = column order) that hold
-//     the row -- the same order wherever this is called, so every caller gets the same bits;
-//   RoPE (base.py:478-483, rotate_half :465-469; when cos_row is not null):
+// one lane's Vec16<T>::N consecutive values f of a head row of d values (d = 32, 64 or 128), every
+// step rounded to the tensor's dtype as the reference's torch ops round it:
+//   HeadRMSNorm (base.py:355-357, when `norm`): h = dtype(x * rsqrt(mean(x^2) + eps)), fp32 maths;
+//     the row's sum of squares is an fma chain over the lane's values, then group_sum over the
+//     `lanes` lanes that hold the row; the mean is an exact power-of-two scaling; rsqrt is the
+//     hardware v_rsq_f32 (1 ulp, like the reference's GPU torch.rsqrt);
+//   RoPE (base.py:478-483, rotate_half :465-469; when c is not null):
 //     out[2i]   = dtype(dtype(h[2i] c) + dtype(-h[2i+1] s)),
 //     out[2i+1] = dtype(dtype(h[2i+1] c) + dtype(h[2i] s)),
-//     c / s the lane's N entries of the [T, D] tables' row for this position.
-// Every lane of a group must call this together (it shuffles). An invalid lane (padding, zeros)
-// reads no table and keeps its zeros: with eps == 0 its r would be inf, and 0 * inf = NaN would
-// reach a caller's amax.
-template <typename T>
-__device__ __forceinline__ void head_norm_rope(float* f, bool norm, float eps, int d, int lanes, bool valid,
-                                               const T* cos_row, const T* sin_row) {
+//     c / s the lane's N entries of the [T, D] tables' row for this position (already loaded).
+// bf16 roundings go through the pair converter (v_cvt_pk_bf16_f32, nearest even) when every value
+// the wave transforms is finite and the norm's eps is positive (no NaN can arise then); otherwise
+// the wave takes the exact software rounding, which also makes every NaN the quiet 0x7FC0 that
+// torch's bf16 rounding gives -- the two agree bit for bit on every finite result. Every lane of a
+// group must call this together (it exchanges lanes); an invalid lane (padding, zeros) uses no
+// table values and keeps its zeros.
+template <typename T, bool HW>
+__device__ __forceinline__ void head_norm_rope_core(float* f, bool norm, float eps, int d, int lanes, bool valid,
+                                                    const float* c, const float* sn) {
   // Separate products and sums, as the reference's separate torch ops round them: no FMA
   // contraction in this function (hipcc contracts a * b + c by default, which would change the
   // fp32 results).
 #pragma clang fp contract(off)
   constexpr int N = Vec16<T>::N;
+  auto rnd2 = [](float& a, float& b) __attribute__((always_inline)) {
+    if constexpr (sizeof(T) == 2) {
+      if constexpr (HW) {
+        const uint32_t w = bf16x2_rne_raw(a, b);
+        a = __uint_as_float(w << 16);
+        b = __uint_as_float(w & 0xFFFF0000u);
+      } else {
+        a = round_bf16(a);
+        b = round_bf16(b);
+      }
+    }
+  };
   if (norm) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < N; ++i) ss = fmaf(f[i], f[i], ss);
-    for (int o = 1; o < lanes; o <<= 1) ss = ss + __shfl_xor(ss, o, 64);
-    const float r = 1.0f / __builtin_sqrtf(ss / (float)d + eps);   // IEEE sqrt and division
-#pragma unroll
-    for (int i = 0; i < N; ++i) f[i] = valid ? round_to<T>(f[i] * r) : 0.0f;
-  }
-  if (cos_row != nullptr && valid) {
-    float c[N], sn[N];
-    Vec16<T>::load(cos_row, c);
-    Vec16<T>::load(sin_row, sn);
+    ss = group_sum(ss, lanes);
+    const float r = __builtin_amdgcn_rsqf(__builtin_ldexpf(ss, -__builtin_ctz((unsigned)d)) + eps);
 #pragma unroll
     for (int i = 0; i < N; i += 2) {
-      const float a0 = round_to<T>(f[i] * c[i]);
-      const float b0 = round_to<T>(-f[i + 1] * sn[i]);
-      const float a1 = round_to<T>(f[i + 1] * c[i + 1]);
-      const float b1 = round_to<T>(f[i] * sn[i + 1]);
-      f[i] = round_to<T>(a0 + b0);
-      f[i + 1] = round_to<T>(a1 + b1);
+      float a = f[i] * r, b = f[i + 1] * r;
+      rnd2(a, b);
+      f[i] = valid ? a : 0.0f;
+      f[i + 1] = valid ? b : 0.0f;
     }
   }
+  if (c != nullptr && valid) {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      float a0 = f[i] * c[i], a1 = f[i + 1] * c[i + 1];
+      float b0 = -f[i + 1] * sn[i], b1 = f[i] * sn[i + 1];
+      rnd2(a0, a1);
+      rnd2(b0, b1);
+      float o0 = a0 + b0, o1 = a1 + b1;
+      rnd2(o0, o1);
+      f[i] = o0;
+      f[i + 1] = o1;
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void head_norm_rope(float* f, bool norm, float eps, int d, int lanes, bool valid,
+                                               const float* c, const float* sn) {
+  if constexpr (sizeof(T) == 2) {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int i = 0; i < Vec16<T>::N; ++i) { const uint32_t a = abs_bits(f[i]); mx = mx > a ? mx : a; }
+    const bool bad = mx >= 0x7F800000u || (norm && !(eps > 0.0f));
+    if (__builtin_amdgcn_ballot_w64(bad) == 0) {     // wave-uniform
+      head_norm_rope_core<T, true>(f, norm, eps, d, lanes, valid, c, sn);
+      return;
+    }
+  }
+  head_norm_rope_core<T, false>(f, norm, eps, d, lanes, valid, c, sn);
 }
 
 // LDS pointer type: the 32-bit LDS address of a __shared__ object is (uint32_t)(lds_u8_t*)p.

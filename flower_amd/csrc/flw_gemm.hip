@@ -46,6 +46,16 @@ struct GemmParams {
   int lds_epi;         // epilogue staged through LDS (N % 8 == 0, 16-byte aligned y / residual rows)
   uint32_t* gmax;      // optional: max |y| (fp32 bit patterns) per group of gcols output columns
   int gcols;           // power of two in [8, 256]
+  // Optional with gmax (gcols = head_dim in {32, 64, 128}): the attention's pre-quantisation
+  // transform of qkv_heads applied to the output columns n < xcols (the q and k heads) before
+  // they are stored and before their maxima are taken -- HeadRMSNorm when xnorm, RoPE when rcos
+  // is set ([xT, gcols] bf16 tables; output row m is position m % xT).
+  int xcols;           // 0: no transform
+  int xnorm;
+  float xeps;
+  int xT;
+  const uint16_t* rcos;
+  const uint16_t* rsin;
 };
 
 // The epilogue value of one output: bf16(v), or bf16(residual + bf16(v)) -- x + linear(h) with
@@ -206,11 +216,12 @@ __device__ __forceinline__ v8i swz_frag(const uint8_t* tile, int rb, int kc, int
 // With gmax, the max |y| over the tile's rows for each group of gcols columns (the per-head amax of
 // a QKV projection, gcols = head_dim) is reduced in the workgroup and folded into gmax with one
 // atomic max per group and tile (bit patterns of non-negative floats order as unsigned integers).
+template <bool XF = false>
 __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const float (&sxm)[2], const float* sw,
                                                 int sw_step, uint16_t* y, int64_t ys, const uint16_t* res,
                                                 int64_t rs, int M, int N, uint8_t* st0, uint8_t* st1, int m0,
                                                 int n0, int wave, int lane, uint32_t* gmax = nullptr,
-                                                int gcols = 0) {
+                                                int gcols = 0, const GemmParams* xf = nullptr) {
   const int wn = wave & 1, wm = wave >> 1, hh = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -245,11 +256,14 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
   lds_barrier();
   // Wave w stores rows 32 w .. 32 w + 31, two rows (2 x 512 bytes) per instruction.
   uint32_t lm = 0;                                // max |y| bf16 bits of this lane's chunks
-#pragma unroll 4
-  for (int q = 0; q < 16; ++q) {
+  // The q / k transform: this lane's 8 columns lie in one head (gcols / 8 lanes per head, an
+  // aligned group of the half-wave, the layout head_norm_rope reduces over); every lane of the
+  // group runs it, rows past M included (they use the last row's table row; their stores are
+  // skipped).
+  const bool xform = XF && n0 + 8 * (lane & 31) < xf->xcols;
+  auto store_row = [&](int q, uint4 v) __attribute__((always_inline)) {
     const int r = 32 * wave + 2 * q + (lane >> 5), ch = lane & 31;
     const int m = m0 + r, n = n0 + 8 * ch;
-    const uint4 v = *reinterpret_cast<const uint4*>((r < 128 ? st0 : st1) + (r & 127) * 512 + 16 * (ch ^ (r & 31)));
     if (m < M && n < N) {
       uint4 o = v;
       if (res) {
@@ -273,6 +287,57 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
         }
       }
     }
+  };
+  auto staged = [&](int q) __attribute__((always_inline)) {
+    const int r = 32 * wave + 2 * q + (lane >> 5), ch = lane & 31;
+    return *reinterpret_cast<const uint4*>((r < 128 ? st0 : st1) + (r & 127) * 512 + 16 * (ch ^ (r & 31)));
+  };
+  if (xform) {
+    // This lane's rows are m0 + 32 wave + (lane >> 5) + 2 q: their positions and the table entries of
+    // its 8 columns, loaded four rows at a time (one latency per four rows).
+    const int d = (8 * (lane & 31)) & (gcols - 1);
+    const int xlast = (int)((int64_t)(M - 1) % xf->xT);
+    int xt = (int)((int64_t)min(m0 + 32 * wave + (lane >> 5), M - 1) % xf->xT);
+    const bool rope = xf->rcos != nullptr;
+    uint4 tc[4], tsn[4];
+    auto fetch = [&](int bt) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int q = 4 * bt + e;
+        const int m = m0 + 32 * wave + 2 * q + (lane >> 5);
+        const int64_t toff = (int64_t)(m < M ? xt : xlast) * gcols + d;
+        if (rope) {
+          tc[e] = *reinterpret_cast<const uint4*>(xf->rcos + toff);
+          tsn[e] = *reinterpret_cast<const uint4*>(xf->rsin + toff);
+        }
+        xt += 2;                                  // the row two below (xT may be 1)
+        xt = xt >= xf->xT ? xt - xf->xT : xt;
+        xt = xt >= xf->xT ? xt - xf->xT : xt;
+      }
+    };
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) {
+      fetch(bt);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int q = 4 * bt + e;
+        float f[8], cf[8], sf[8];
+        Vec16<uint16_t>::unpack(staged(q), f);
+        if (rope) {
+          Vec16<uint16_t>::unpack(tc[e], cf);
+          Vec16<uint16_t>::unpack(tsn[e], sf);
+        }
+        head_norm_rope<uint16_t>(f, xf->xnorm != 0, xf->xeps, gcols, gcols >> 3, true, rope ? cf : nullptr, sf);
+        // every value is a bf16 value now (rounded by the transform): its upper half is the code
+        store_row(q, make_uint4((__float_as_uint(f[0]) >> 16) | (__float_as_uint(f[1]) & 0xFFFF0000u),
+                                (__float_as_uint(f[2]) >> 16) | (__float_as_uint(f[3]) & 0xFFFF0000u),
+                                (__float_as_uint(f[4]) >> 16) | (__float_as_uint(f[5]) & 0xFFFF0000u),
+                                (__float_as_uint(f[6]) >> 16) | (__float_as_uint(f[7]) & 0xFFFF0000u)));
+      }
+    }
+  } else {
+#pragma unroll 4
+    for (int q = 0; q < 16; ++q) store_row(q, staged(q));
   }
   // The next tile's loads refill st0 / st1: every wave's reads of the staged tile are done.
   __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
@@ -304,6 +369,7 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
 }
 
 // One 256 x 256 output tile: K loop over two LDS stages, then the scaled bf16 epilogue.
+template <bool XF = false>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
                                           int n0, int wave, int lane, int sbase, int nst, int split) {
   const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
@@ -401,8 +467,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
       const int m = min(m0 + 64 * wm + 32 * j + (lane & 31), p.M - 1);
       sxm[j] = p.sx[(int64_t)m * p.sx_step];
     }
-    staged_epilogue(acc, sxm, p.sw, p.sw_step, p.y, p.ys, p.res, p.rs, p.M, p.N, st0, st1, m0, n0, wave, lane,
-                    p.gmax, p.gcols);
+    staged_epilogue<XF>(acc, sxm, p.sw, p.sw_step, p.y, p.ys, p.res, p.rs, p.M, p.N, st0, st1, m0, n0, wave,
+                        lane, p.gmax, p.gcols, XF ? &p : nullptr);
     return;
   }
   float sxm[2];
@@ -609,7 +675,9 @@ __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0,
   lds_barrier();
 }
 
-template <int TM>
+// XF: the q / k transform epilogue of flw_fp8_scaled_mm_qk_norm_rope_amax, compiled as its own
+// instance so that the other GEMMs keep their register allocation.
+template <int TM, bool XF = false>
 __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p) {
   // One array per stage: every LDS access below names its stage at compile time, so the
   // compiler can see that the direct-to-LDS loads in flight write the other stage.
@@ -637,7 +705,7 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
     const int tm = first_m + (tt % (kGroupM * p.tiles_n)) % gm;
     const int tn = (tt % (kGroupM * p.tiles_n)) / gm;
     const int s0 = split * nst_all / p.splits, s1 = (split + 1) * nst_all / p.splits;
-    if constexpr (TM == 256) gemm_tile(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
+    if constexpr (TM == 256) gemm_tile<XF>(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
     else gemm_tile_128(p, st0, st1, tm * TM, tn * kFBN, wave, lane, s0, s1 - s0, split);
   }
 }
@@ -903,7 +971,7 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
                      const float* sx, int64_t sx_count, const float* sw, int64_t sw_count,
                      void* y, int64_t ys, hipStream_t s, const void* res = nullptr, int64_t rs = 0,
                      void* workspace = nullptr, size_t workspace_bytes = 0, uint32_t* gmax = nullptr,
-                     int gcols = 0) {
+                     int gcols = 0, const GemmParams* xform = nullptr) {
   FLW_REQUIRE(x8 && w8 && sx && sw && y, FLW_E_INVALID, "null pointer argument");
   FLW_REQUIRE(M > 0 && N > 0 && K > 0, FLW_E_INVALID, "empty GEMM");
   FLW_REQUIRE(K % 16 == 0, FLW_E_UNSUPPORTED, "K must be a multiple of 16, got %lld", (long long)K);
@@ -944,7 +1012,8 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
       if (p.splits == 1) p.part = nullptr;
     }
     const void* kern = narrow ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<128>)
-                              : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256>);
+                     : xform != nullptr ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, true>)
+                                        : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256>);
     // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per work item.
     const int64_t items = (int64_t)p.tiles_n * p.tiles_m * p.splits;
     const int64_t grid = items < compute_units() ? items : compute_units();
@@ -953,6 +1022,10 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
                   "the group amax needs an unsplit GEMM with N %% 8 == 0 and 16-byte aligned rows");
       p.gmax = gmax;
       p.gcols = gcols;
+      if (xform != nullptr) {
+        p.xcols = xform->xcols; p.xnorm = xform->xnorm; p.xeps = xform->xeps; p.xT = xform->xT;
+        p.rcos = xform->rcos; p.rsin = xform->rsin;
+      }
       const Timer tm = take_timer();
       const int ng = (int)(N / gcols);
       (void)launch_args(reinterpret_cast<const void*>(&fill_u32_kernel), dim3((unsigned)((ng + 255) / 256)),
@@ -1044,6 +1117,36 @@ extern "C" int flw_fp8_scaled_mm_group_amax(const uint8_t* x8, int64_t M, int64_
   FLW_REQUIRE(K % kFBK == 0, FLW_E_UNSUPPORTED, "the group amax needs K %% %d == 0", kFBK);
   return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y, y_row_stride,
                    static_cast<hipStream_t>(stream), nullptr, 0, nullptr, 0, amax_out, (int)group_cols);
+}
+
+extern "C" int flw_fp8_scaled_mm_qk_norm_rope_amax(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
+                                                  int64_t N, const float* x_scale, int64_t x_scale_count,
+                                                  const float* w_scale, int64_t w_scale_count, void* y,
+                                                  int64_t y_row_stride, int64_t head_dim, int64_t qk_cols, int qk_norm,
+                                                  float eps, const void* rope_cos, const void* rope_sin,
+                                                  int64_t seq_len, uint32_t* amax_out, void* stream) {
+  FLW_REQUIRE(amax_out != nullptr, FLW_E_INVALID, "null amax_out");
+  FLW_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128, FLW_E_UNSUPPORTED,
+              "head_dim must be 32/64/128, got %lld", (long long)head_dim);
+  FLW_REQUIRE(N % head_dim == 0 && qk_cols >= 0 && qk_cols <= N && qk_cols % head_dim == 0, FLW_E_INVALID,
+              "qk_cols must be a multiple of head_dim within N");
+  FLW_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), FLW_E_INVALID, "pass both RoPE tables or neither");
+  FLW_REQUIRE(seq_len > 0 && seq_len <= 0x7FFFFFFF && M % seq_len == 0, FLW_E_INVALID,
+              "seq_len must divide M (rows are (batch, position) pairs)");
+  FLW_REQUIRE(rope_cos == nullptr || (((uintptr_t)rope_cos & 15) == 0 && ((uintptr_t)rope_sin & 15) == 0),
+              FLW_E_INVALID, "RoPE tables must be 16-byte aligned");
+  FLW_REQUIRE(qk_norm == 0 || eps >= 0.0f, FLW_E_INVALID, "eps must be non-negative");
+  FLW_REQUIRE(K % kFBK == 0, FLW_E_UNSUPPORTED, "the fused epilogue needs K %% %d == 0", kFBK);
+  GemmParams xf{};
+  xf.xcols = (int)qk_cols;
+  xf.xnorm = qk_norm != 0;
+  xf.xeps = eps;
+  xf.xT = (int)seq_len;
+  xf.rcos = static_cast<const uint16_t*>(rope_cos);
+  xf.rsin = static_cast<const uint16_t*>(rope_sin);
+  return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y, y_row_stride,
+                   static_cast<hipStream_t>(stream), nullptr, 0, nullptr, 0, amax_out, (int)head_dim,
+                   qk_cols > 0 ? &xf : nullptr);
 }
 
 extern "C" int flw_fp8_scaled_mm_residual(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,

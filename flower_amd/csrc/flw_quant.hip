@@ -89,10 +89,15 @@ __device__ __forceinline__ int64_t vec_offset(const QTensor& t, int64_t r0, int6
 template <typename T>
 __device__ __forceinline__ void qk_transform(const QTensor& t, float* f, int64_t row, int64_t cv, int vpr,
                                              int64_t d3, bool valid) {
-  const int64_t off = row * d3 + cv * Vec16<T>::N;
-  head_norm_rope<T>(f, t.norm, t.eps, (int)d3, vpr, valid,
-                    t.rcos ? static_cast<const T*>(t.rcos) + off : nullptr,
-                    t.rsin ? static_cast<const T*>(t.rsin) + off : nullptr);
+  constexpr int N = Vec16<T>::N;
+  float c[N], sn[N];
+  const bool rope = t.rcos != nullptr && valid;
+  if (rope) {
+    const int64_t off = row * d3 + cv * N;
+    Vec16<T>::load(static_cast<const T*>(t.rcos) + off, c);
+    Vec16<T>::load(static_cast<const T*>(t.rsin) + off, sn);
+  }
+  head_norm_rope<T>(f, t.norm, t.eps, (int)d3, vpr, valid, t.rcos != nullptr ? c : nullptr, sn);
 }
 
 template <typename T, bool XFORM = false>
@@ -1163,6 +1168,90 @@ extern "C" int flw_vtile_from_bhtd(const uint8_t* codes, int64_t B, int64_t H, i
                     static_cast<hipStream_t>(stream), tm.start, tm.stop, codes, stride_b, stride_h, stride_t, H, T,
                     (int)D, v_tiles);
   return check_launch("flw_vtile_from_bhtd");
+}
+
+// ---------------------------------------------------------------- e4m3 codes -> values
+//
+// The dequantised tensor a straight-through FP8 path differentiates at: out[b, h, t, d] =
+// e4m3(code) * scale of its group, rounded to the output dtype (bf16: nearest even). Codes in
+// (B, H, T, D) rows or in the attention kernel's V tile layout; out contiguous (B, H, T, D). One
+// thread per 8 consecutive d of one row.
+namespace flw {
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ codes, int layout, int64_t H,
+                                                      int64_t T, int D, const float* __restrict__ scales,
+                                                      int64_t ssb, int64_t ssh, OutT* __restrict__ out,
+                                                      int64_t n8) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const int per_row = D / 8;
+  const int64_t row = i / per_row;                 // (b * H + h) * T + t
+  const int d0 = (int)(i % per_row) * 8;
+  const int64_t t = row % T, bh = row / T;
+  const int64_t b = bh / H, h = bh % H;
+  const float s = scales[b * ssb + h * ssh];
+  uint32_t c[8];
+  if (layout == FLW_LAYOUT_BHTD) {
+    const uint2 w = *reinterpret_cast<const uint2*>(codes + row * D + d0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { c[e] = (w.x >> (8 * e)) & 0xFFu; c[4 + e] = (w.y >> (8 * e)) & 0xFFu; }
+  } else {
+    // tile layout: element (key kk, dim d) of a 64-key tile at (d / 32) 2048 + (kk / 32) 1024 +
+    // ((d % 32) + 32 hb) 16 + bb, hb = (r / 4) % 2, bb = 4 (r / 8) + r % 4, r = kk % 32
+    const int64_t slice = ((T + 63) / 64) * 64 * D;
+    const int kk = (int)(t % 64), r = kk % 32;
+    const uint8_t* tile = codes + bh * slice + (t / 64) * 64 * D;
+    const int hb = (r / 4) % 2, bb = 4 * (r / 8) + r % 4;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = d0 + e;
+      c[e] = tile[(d / 32) * 2048 + (kk / 32) * 1024 + ((d % 32) + 32 * hb) * 16 + bb];
+    }
+  }
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = e4m3_to_f32(c[e]) * s;
+  if constexpr (sizeof(OutT) == 2) {
+    uint4 o;
+    o.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+    o.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+    o.z = f32_to_bf16_bits(v[4]) | (f32_to_bf16_bits(v[5]) << 16);
+    o.w = f32_to_bf16_bits(v[6]) | (f32_to_bf16_bits(v[7]) << 16);
+    *reinterpret_cast<uint4*>(out + row * D + d0) = o;
+  } else {
+    float4* o = reinterpret_cast<float4*>(out + row * D + d0);
+    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+}  // namespace flw
+
+extern "C" int flw_dequant_e4m3(const uint8_t* codes, int layout, int64_t B, int64_t H, int64_t T, int64_t D,
+                                const float* scales, int granularity, void* out, int out_dtype, void* stream) {
+  using namespace flw;
+  FLW_REQUIRE(codes != nullptr && scales != nullptr && out != nullptr, FLW_E_INVALID, "null pointer argument");
+  FLW_REQUIRE(B > 0 && H > 0 && T > 0, FLW_E_INVALID, "empty shape");
+  FLW_REQUIRE(D == 32 || D == 64 || D == 128, FLW_E_UNSUPPORTED, "head_dim must be 32/64/128, got %lld", (long long)D);
+  FLW_REQUIRE(layout == FLW_LAYOUT_BHTD || layout == FLW_LAYOUT_VTILE, FLW_E_INVALID, "bad layout %d", layout);
+  FLW_REQUIRE(out_dtype == FLW_BF16 || out_dtype == FLW_F32, FLW_E_UNSUPPORTED, "output dtype %d", out_dtype);
+  FLW_REQUIRE(granularity >= FLW_SCALE_TENSOR && granularity <= FLW_SCALE_BH, FLW_E_INVALID, "bad granularity %d",
+              granularity);
+  FLW_REQUIRE(((uintptr_t)codes & 7) == 0 && ((uintptr_t)out & 15) == 0, FLW_E_INVALID,
+              "codes must be 8-byte, out 16-byte aligned");
+  const int64_t n8 = B * H * T * D / 8;
+  FLW_REQUIRE((n8 + 255) / 256 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "tensor too large");
+  const int64_t ssb = granularity == FLW_SCALE_BH ? H : 0, ssh = granularity == FLW_SCALE_TENSOR ? 0 : 1;
+  const dim3 grid((unsigned)((n8 + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (out_dtype == FLW_BF16)
+    hipLaunchKernelGGL(dequant_kernel<uint16_t>, grid, dim3(256), 0, s, codes, layout, H, T, (int)D, scales, ssb,
+                       ssh, static_cast<uint16_t*>(out), n8);
+  else
+    hipLaunchKernelGGL(dequant_kernel<float>, grid, dim3(256), 0, s, codes, layout, H, T, (int)D, scales, ssb,
+                       ssh, static_cast<float*>(out), n8);
+  return check_launch("flw_dequant_e4m3");
 }
 
 // ---------------------------------------------------------------- allocation-free QKV quantiser

@@ -76,6 +76,10 @@ struct SwaParams {
   // the scale was derived from. A lane holding a larger |q| (a stale or wrong maximum) takes the
   // exact path for its values: IEEE division, clamp to +-448, then the cast.
   const uint32_t* qamax;
+  // Optional: the log-sum-exp of each query's scores, [B, H, T] fp32, natural log, in the units of
+  // the dequantised scores (q . k / sqrt(D)): lse = m + ln(sum_j exp(s_j - m)) -- what a
+  // recomputing backward (flw_swa_bf16_bwd) needs to rebuild P.
+  float* lse;
 };
 
 template <typename OutT> struct Store4;
@@ -462,6 +466,12 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   const float l_tot = pair_sum(l_run);
   const float inv = l_tot == 0.0f ? 0.0f : v_s / l_tot;
   const int qi = q0 + qcol;
+  if (p.lse != nullptr && hh == 0 && qi < T) {
+    // m c + log2(l / 448) is the base-2 log-sum-exp of the scores times log2(e): back to natural log
+    constexpr float kLn2 = 0.6931471805599453f;
+    p.lse[(int64_t)bh * T + qi] =
+        l_tot == 0.0f ? -INFINITY : (fmaf(m_run, c, __builtin_amdgcn_logf(l_tot)) - kLog2_448) * kLn2;
+  }
   if (qi < T) {
     OutT* op = static_cast<OutT*>(p.out) + b * p.osb + h * p.osh + (int64_t)qi * p.ost;
 #pragma unroll
@@ -488,7 +498,8 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
                    const uint8_t* vt, const float* qs, const float* ks, const float* vs, int64_t ssb, int64_t ssh,
                    void* out, int out_dtype, const int64_t* ost, int64_t B, int64_t H, int64_t T,
                    int64_t D, int64_t window, hipStream_t stream, Timer tm, const void* qx = nullptr,
-                   const int64_t* xst = nullptr, const float* qr = nullptr, const uint32_t* qamax = nullptr) {
+                   const int64_t* xst = nullptr, const float* qr = nullptr, const uint32_t* qamax = nullptr,
+                   float* lse = nullptr) {
   FLW_REQUIRE(q8 && k8 && vt && qs && ks && vs && out && qst && kst && ost, FLW_E_INVALID, "null pointer argument");
   if (qx != nullptr) {
     const int64_t vec = out_dtype == FLW_F32 ? 4 : 8;
@@ -527,6 +538,8 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.qx = qx;
   p.qr = qr;
   p.qamax = qx != nullptr ? qamax : nullptr;
+  p.lse = lse;
+  FLW_REQUIRE(lse == nullptr || ((uintptr_t)lse & 3) == 0, FLW_E_INVALID, "lse must be 4-byte aligned");
   if (qx != nullptr) { p.xsb = xst[0]; p.xsh = xst[1]; p.xst = xst[2]; }
   p.ramp = W > 0 ? (int)std::min<int64_t>(nM, (W - 1) / kBM + 1) : 0;
   p.group_slices = ((B * H) % 8 == 0 && (p.nwg & 7) == 0) ? (int)(B * H / 8) : (int)(B * H);
@@ -591,6 +604,20 @@ extern "C" int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, cons
   return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, ssb, ssh,
                  out, out_dtype, out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream),
                  take_timer());
+}
+
+extern "C" int flw_fp8_swa_fwd_lse(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                                   const int64_t* k_strides, const uint8_t* v_tiles, const float* q_scale,
+                                   const float* k_scale, const float* v_scale, int granularity, void* out,
+                                   int out_dtype, const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
+                                   int64_t D, int64_t window, float* lse, void* stream) {
+  FLW_REQUIRE(lse != nullptr, FLW_E_INVALID, "null lse");
+  int64_t ssb, ssh;
+  const int rc = scale_strides(granularity, H, &ssb, &ssh);
+  if (rc) return rc;
+  return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, ssb, ssh, out, out_dtype,
+                 out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream), take_timer(), nullptr, nullptr,
+                 nullptr, nullptr, lse);
 }
 
 extern "C" int flw_fp8_swa_fwd_qx(const void* q, const int64_t* q_strides, const uint8_t* q8_nonfinite,

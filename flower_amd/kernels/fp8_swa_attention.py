@@ -364,3 +364,124 @@ def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: to
                              _lib.stream_of(q8))
     _lib.check(rc, "fp8_swa_attention_from_codes")
     return out
+
+
+def dequantize_e4m3(codes: torch.Tensor, scales: torch.Tensor, shape, granularity: str = "head",
+                    layout: str = "bhtd", out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """(B, H, T, D) values e4m3(code) * scale of the code's group, rounded to ``out_dtype``
+    (flw_dequant_e4m3): ``codes`` as ``_per_tensor_fp8`` returns them (layout "bhtd", contiguous) or
+    in the attention kernel's V tile layout ("vtile", 1-D); ``scales`` one group's float32 scales."""
+    lib = _lib.load()
+    B, H, T, D = shape
+    if codes.dtype == torch.float8_e4m3fn:
+        codes = codes.view(torch.uint8)
+    G = _group_count(granularity, B, H)
+    if scales.numel() != G or scales.dtype != torch.float32 or not scales.is_contiguous():
+        raise ValueError(f"scales must be a contiguous float32 tensor of {G} elements")
+    want = lib.flw_vtile_bytes(B, H, T, D) if layout == "vtile" else B * H * T * D
+    if codes.dtype != torch.uint8 or codes.numel() != want or not codes.is_contiguous():
+        raise ValueError(f"codes must be {want} contiguous e4m3 codes ({layout})")
+    _lib.require_gpu(codes, scales)
+    out = torch.empty((B, H, T, D), dtype=out_dtype, device=codes.device)
+    rc = lib.flw_dequant_e4m3(codes.data_ptr(), _lib.LAYOUT_VTILE if layout == "vtile" else _lib.LAYOUT_BHTD,
+                              B, H, T, D, scales.data_ptr(), _lib.GRANULARITY[granularity], out.data_ptr(),
+                              _lib.dtype_code(out_dtype), _lib.stream_of(codes))
+    _lib.check(rc, "dequantize_e4m3")
+    return out
+
+
+class _Fp8SwaAttention(torch.autograd.Function):
+    """FP8 forward (the e4m3 quantiser pass pair, then the FP8 kernel) with the bf16 sliding-window
+    backward (flw_swa_bf16_bwd) at the dequantised Q, K, V: the straight-through estimator of
+    `_fake_quant_e4m3` (base.py:167-203, the gradient passes the quantisers unchanged) around the
+    attention's own backward, which rebuilds P from saved row statistics as swa_attention.py:307-359
+    does. The statistics (O and the log-sum-exp) are recomputed in the backward by the bf16 forward
+    (flw_swa_bf16_fwd) on the dequantised bf16 Q, K, V, so P is rebuilt from the same operands it
+    was normalised with: the gradient is that of bf16 attention at the dequantised point, which is
+    what the reference's fake-quant training path (`_fake_quant_e4m3`, then bf16 attention)
+    differentiates. (Rebuilding P from the FP8 forward's own log-sum-exp, which comes from the exact
+    fp32 scores of the codes, against the bf16-rounded dequantised operands misnormalises P by
+    exp(score difference): measured 7 % mean-relative on dQ at the 450M shape.)"""
+
+    @staticmethod
+    def forward(ctx, q, k, v, window, granularity):
+        lib = _lib.load()
+        B, H, T, D = q.shape
+        dt = _lib.dtype_code(q.dtype)
+        q, sq = _prepare(q.detach())
+        k, sk = _prepare(k.detach())
+        v, sv = _prepare(v.detach())
+        G = _group_count(granularity, B, H)
+        dev = q.device
+        q8 = torch.empty((B, H, T, D), dtype=torch.uint8, device=dev)
+        k8 = torch.empty_like(q8)
+        vt = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device=dev)
+        scales = torch.empty(3 * G, dtype=torch.float32, device=dev)
+        ws = _lib.workspace(3 * lib.flw_quant_workspace_bytes(B, H, T, D), dev)
+        stream = _lib.stream_of(q)
+        _lib.check(lib.flw_quant_qkv_e4m3(q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, H, T, D,
+                                          _lib.i64s(*sq, *sk, *sv), _lib.GRANULARITY[granularity], q8.data_ptr(),
+                                          k8.data_ptr(), vt.data_ptr(), scales.data_ptr(), ws.data_ptr(),
+                                          ws.numel(), stream), "fp8_swa_attention (quantise)")
+        out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+        s8 = _lib.i64s(H * T * D, T * D, D)
+        base = scales.data_ptr()
+        rc = lib.flw_fp8_swa_fwd(q8.data_ptr(), s8, k8.data_ptr(), s8, vt.data_ptr(), base, base + 4 * G,
+                                 base + 8 * G, _lib.GRANULARITY[granularity], out.data_ptr(), dt,
+                                 _lib.i64s(*out.stride()[:3]), B, H, T, D, int(window), stream)
+        _lib.check(rc, "fp8_swa_attention (forward)")
+        ctx.save_for_backward(q8, k8, vt, scales)
+        ctx.window, ctx.granularity, ctx.G, ctx.dtype = int(window), granularity, G, q.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        lib = _lib.load()
+        q8, k8, vt, scales = ctx.saved_tensors
+        B, H, T, D = q8.shape
+        G, gran = ctx.G, ctx.granularity
+        qd = dequantize_e4m3(q8, scales[:G], (B, H, T, D), gran)
+        kd = dequantize_e4m3(k8, scales[G:2 * G], (B, H, T, D), gran)
+        vd = dequantize_e4m3(vt, scales[2 * G:], (B, H, T, D), gran, layout="vtile")
+        stream = _lib.stream_of(qd)
+        ob = torch.empty_like(qd)
+        lse = torch.empty((B, H, T), dtype=torch.float32, device=qd.device)
+        _lib.check(lib.flw_swa_bf16_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), B, H, T, D, ctx.window,
+                                        ob.data_ptr(), lse.data_ptr(), stream), "fp8_swa_attention (recompute)")
+        do = dout.to(torch.bfloat16).contiguous()
+        dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+        ws = _lib.workspace(lib.flw_swa_bf16_bwd_workspace_bytes(B, H, T, D), q8.device)
+        _lib.check(lib.flw_swa_bf16_bwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ob.data_ptr(), do.data_ptr(),
+                                        lse.data_ptr(), B, H, T, D, ctx.window, dq.data_ptr(), dk.data_ptr(),
+                                        dv.data_ptr(), ws.data_ptr(), ws.numel(), stream),
+                   "fp8_swa_attention (backward)")
+        dt = ctx.dtype
+        return dq.to(dt), dk.to(dt), dv.to(dt), None, None
+
+
+def fp8_swa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, *,
+                      granularity: str = "head") -> torch.Tensor:
+    """Differentiable FP8 sliding-window causal attention (an extension of the reference's
+    forward-only kernel, fp8_swa_attention.py:71-76): the forward is ``fp8_swa_attention_forward``'s
+    (e4m3 Q / K / V with amax scales, e4m3 P, fp32 accumulation); the backward is the bf16
+    sliding-window backward at the dequantised Q, K, V (straight-through quantisers, as
+    `_fake_quant_e4m3` trains), from row statistics the bf16 forward recomputes there.
+    q / k / v: (B, H, T, D) bf16 or fp32 on the GPU, D in {32, 64, 128}; window > 0 (the
+    backward's requirement, swa_attention.py:378)."""
+    try:
+        _lib.load()
+    except RuntimeError as e:
+        raise RuntimeError(f"fp8_swa_attention requires the HIP library: {e}") from e
+    if q.dim() != 4:
+        raise ValueError(f"expected (B, H, T, D), got {tuple(q.shape)}")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("q, k, v must share a dtype, bfloat16 or float32")
+    if q.shape[-1] not in (32, 64, 128):
+        raise ValueError(f"head_dim must be 32/64/128 for the MFMA tiling, got {q.shape[-1]}")
+    if window <= 0:
+        raise ValueError("window must be positive; use flex for full-context attention")
+    _group_count(granularity, q.shape[0], q.shape[1])
+    _lib.require_gpu(q, k, v)
+    return _Fp8SwaAttention.apply(q, k, v, int(window), granularity)

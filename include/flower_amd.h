@@ -233,6 +233,27 @@ int flw_fp8_swa_fwd_qx(const void* q, const int64_t* q_strides, const uint8_t* q
                        const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
                        int64_t window, void* stream);
 
+/* flw_fp8_swa_fwd that also writes the log-sum-exp of every query's scores, lse [B, H, T] fp32
+ * (contiguous), natural log, in the units of the dequantised scores q . k / sqrt(D):
+ * lse = m + ln(sum_j exp(s_j - m)) over the band, with the kernel's running maximum m and its fp32
+ * row sum of the unquantised P (the sum the reference's l_i is, fp8_swa_attention.py:176) -- the
+ * statistic flw_swa_bf16_bwd takes to rebuild P, so the FP8 forward can be trained through with
+ * that backward (flower/kernels/swa_attention.py:307-359). -inf for a query with no key
+ * in its band (window <= 0). */
+int flw_fp8_swa_fwd_lse(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                        const int64_t* k_strides, const uint8_t* v_tiles, const float* q_scale,
+                        const float* k_scale, const float* v_scale, int granularity, void* out,
+                        int out_dtype, const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
+                        int64_t D, int64_t window, float* lse, void* stream);
+
+/* The dequantised values of e4m3 codes: out[b, h, t, d] = e4m3(code) * scale of (b, h)'s group
+ * (granularity as above), rounded to out_dtype (FLW_BF16: nearest even; FLW_F32: exact). Codes in
+ * FLW_LAYOUT_BHTD (contiguous) or FLW_LAYOUT_VTILE; out contiguous (B, H, T, D), 16-byte aligned.
+ * The tensors the straight-through estimator of `_fake_quant_e4m3` (flower/models/base.py:167-203)
+ * differentiates at: the backward of the FP8 attention runs on them. */
+int flw_dequant_e4m3(const uint8_t* codes, int layout, int64_t B, int64_t H, int64_t T, int64_t D,
+                     const float* scales, int granularity, void* out, int out_dtype, void* stream);
+
 /* Workspace of flw_fp8_swa_attention_forward (e4m3 Q, K, tiled V, scales, amax partials). */
 size_t flw_fp8_swa_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
 
@@ -336,6 +357,23 @@ int flw_fp8_scaled_mm_group_amax(const uint8_t* x8, int64_t M, int64_t K, const 
                                  const float* x_scale, int64_t x_scale_count, const float* w_scale,
                                  int64_t w_scale_count, void* y, int64_t y_row_stride, int64_t group_cols,
                                  uint32_t* amax_out, void* stream);
+
+/* flw_fp8_scaled_mm_group_amax for a QKV projection whose q and k heads feed the FP8 attention
+ * through `CausalSelfAttention.qkv_heads` (flower/models/base.py:618-639): before the q / k output
+ * columns (n < qk_cols) are stored and before their maxima are taken, each head row of head_dim
+ * values gets HeadRMSNorm (base.py:341-357, when qk_norm: fp32 maths, eps) and RoPE
+ * (base.py:436-483, when rope_cos / rope_sin are given: [seq_len, head_dim] bf16 tables; output
+ * row m is position m % seq_len), every step rounded to bf16 as the reference's torch ops round it
+ * -- bit for bit the transform flw_qk_norm_rope_quant_e4m3 applies. y then holds q', k', v and
+ * amax_out their per-head maxima, so the attention's quantiser needs neither an amax pass nor a
+ * transform (flw_fp8_swa_attention_forward_amax). head_dim 32 / 64 / 128; qk_cols a multiple of
+ * head_dim (2 * d_model for a fused QKV); seq_len divides M; the other requirements as
+ * flw_fp8_scaled_mm_group_amax. */
+int flw_fp8_scaled_mm_qk_norm_rope_amax(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,
+                                        const float* x_scale, int64_t x_scale_count, const float* w_scale,
+                                        int64_t w_scale_count, void* y, int64_t y_row_stride, int64_t head_dim,
+                                        int64_t qk_cols, int qk_norm, float eps, const void* rope_cos,
+                                        const void* rope_sin, int64_t seq_len, uint32_t* amax_out, void* stream);
 
 size_t flw_fp8_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int flw_fp8_scaled_mm_ws(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8, int64_t N,

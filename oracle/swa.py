@@ -19,6 +19,10 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
                          With per-head / per-(b,h) scales the scalars become per-slice values.
                          ``quantize_p=False`` skips the e4m3 rounding of p (then it must equal
                          the dense reference on dequantised inputs up to fp32 rounding).
+                         ``mfma_rel_err`` also returns, per output element, how far P codes that
+                         sit within the hardware dot product's error of an e4m3 rounding
+                         boundary can move it (the comparison with an MFMA kernel accepts either
+                         rounding of those codes).
 ``fp8_swa_attention``    quantise Q/K/V (``quant.per_tensor_fp8`` at a granularity) then simulate:
                          the FP8-simulated path end to end.
 
@@ -91,17 +95,43 @@ def _slice_scale(scale: np.ndarray, b: int, h: int) -> float:
     return float(s[bi, hi, 0, 0])
 
 
+def _p_code_flip(x: np.ndarray, rel: np.ndarray) -> np.ndarray:
+    """|e4m3(x') - e4m3(x)| over x' within a relative distance ``rel`` of x (x >= 0): the largest
+    change of the P code value when the pre-rounding value 448 p can move that far -- nonzero only
+    where 448 p lies within ``rel`` of an e4m3 rounding boundary."""
+    c = e4m3_to_f32(f32_to_e4m3(x))
+    lo = e4m3_to_f32(f32_to_e4m3((x * (1.0 - rel)).astype(F32)))
+    hi = e4m3_to_f32(f32_to_e4m3(np.minimum(x * (1.0 + rel), E4M3_MAX).astype(F32)))
+    return np.maximum(np.abs(hi - c), np.abs(c - lo)).astype(np.float64)
+
+
 def fp8_swa_simulate(q8, k8, v8, q_scale, k_scale, v_scale, window: int, block_n: int = 64,
-                     quantize_p: bool = True, chunk: int = 512) -> np.ndarray:
+                     quantize_p: bool = True, chunk: int = 512, mfma_rel_err: float | None = None,
+                     score_perturb=None):
     """Kernel-faithful FP8 SWA forward on e4m3 codes; returns fp32 (B, H, T, D).
 
     Scales are float32 arrays broadcastable to (B, H, 1, 1). Query rows are processed in
     chunks (vectorised), key blocks in the kernel's order, so the running max / rescale
     sequence matches a kernel that uses ``block_n``-key tiles aligned to multiples of
     ``block_n``.
+
+    ``mfma_rel_err`` (e.g. 2^-10, the bound tests/test_gpu_diag.py measures for gfx950's e4m3
+    MFMA): the hardware dot product may differ from the exact one by that fraction of the
+    largest |product| of the dot (bounded here by max|q| max|k| of the two rows), so a score --
+    and the row max it is compared with -- can move by that much, and a P code whose 448 p lies
+    that close (relatively: qk_scale times the two score errors) to an e4m3 rounding boundary can
+    round the other way. Then ``(out, allowance)`` is returned: allowance[b, h, i, d] bounds how
+    far such flips can move out[b, h, i, d] (the flipped code-value changes times |v|, carried
+    through the same rescales and normalisation as the output), so a kernel result is consistent
+    with this simulator when |kernel - out| <= tolerance + allowance.
+
+    ``score_perturb(s_raw, qa, ka) -> s_raw'`` (for the oracle's own tests): replaces each block's
+    raw dot products (fp32, before the scale) -- e.g. by adding errors within the MFMA bound, to
+    check that the allowance covers what such errors do to the output.
     """
     B, H, T, D = q8.shape
     out = np.zeros((B, H, T, D), dtype=F32)
+    allow = np.zeros((B, H, T, D), dtype=np.float64) if mfma_rel_err is not None else None
     sm = 1.0 / (D ** 0.5)
     for b in range(B):
         for h in range(H):
@@ -118,14 +148,27 @@ def fp8_swa_simulate(q8, k8, v8, q_scale, k_scale, v_scale, window: int, block_n
                 l = np.zeros((i1 - i0, 1), dtype=F32)
                 acc = np.zeros((i1 - i0, D), dtype=F32)
                 lo = max(0, i0 - window + 1) // block_n * block_n
+                if allow is not None:
+                    al = np.zeros((i1 - i0, D), dtype=np.float64)
+                    qa = np.abs(qf[i0:i1]).astype(F32)
+                    pm = np.zeros((i1 - i0, 1), dtype=np.float64)   # largest |product| of the max's dot
                 for n0 in range(lo, i1, block_n):
                     n1 = min(T, n0 + block_n)
                     jj = np.arange(n0, n1)[None, :]
                     valid = (jj <= ii) & (ii - jj < window)
                     # FP8 dot with fp32 accumulation: products of e4m3 values are exact; the
                     # sum is taken exactly (float64) and rounded once.
-                    s = (qf[i0:i1] @ kf[n0:n1].T).astype(F32) * qk_scale
+                    s = (qf[i0:i1] @ kf[n0:n1].T).astype(F32)
+                    if score_perturb is not None:
+                        s = score_perturb(s, qf[i0:i1], kf[n0:n1]).astype(F32)
+                    s = s * qk_scale
                     s = np.where(valid, s, -np.inf).astype(F32)
+                    if allow is not None:
+                        # largest |q_d k_d| of each dot: the MFMA's error bound scales with it
+                        pmax = (qa[:, None, :] * np.abs(kf[n0:n1]).astype(F32)[None, :, :]).max(axis=2)
+                        bmax = np.max(s, axis=1, keepdims=True)
+                        arg = np.argmax(s, axis=1)
+                        pm = np.where(bmax > m, pmax[np.arange(i1 - i0), arg][:, None], pm)
                     m_new = np.maximum(m, np.max(s, axis=1, keepdims=True))
                     m_safe = np.where(np.isneginf(m_new), F32(0), m_new)
                     p = np.exp(s - m_safe).astype(F32)
@@ -136,13 +179,20 @@ def fp8_swa_simulate(q8, k8, v8, q_scale, k_scale, v_scale, window: int, block_n
                     if quantize_p:
                         pq = e4m3_to_f32(f32_to_e4m3((p * F32(E4M3_MAX)).astype(F32)))
                         acc = (acc + (pq.astype(np.float64) @ vf[n0:n1]).astype(F32)).astype(F32)
+                        if allow is not None:
+                            # 448 p moves by exp(qk_scale (ds - dm)): both dots' error bounds
+                            rel = np.expm1(float(qk_scale) * mfma_rel_err * (pmax + pm))
+                            flip = np.where(valid, _p_code_flip((p * F32(E4M3_MAX)).astype(F32), rel), 0.0)
+                            al = al * alpha + flip @ np.abs(vf[n0:n1])
                     else:
                         acc = (acc + ((p * F32(E4M3_MAX)).astype(np.float64) @ vf[n0:n1])
                                .astype(F32)).astype(F32)
                     m = m_new
                 acc = acc * pv_scale
                 out[b, h, i0:i1] = acc / np.where(l == 0, F32(1), l)
-    return out
+                if allow is not None:
+                    allow[b, h, i0:i1] = al * float(pv_scale) / np.where(l == 0, 1.0, l.astype(np.float64))
+    return out if allow is None else (out, allow)
 
 
 def fp8_swa_attention(q, k, v, window: int, granularity: str = "tensor", block_n: int = 64):

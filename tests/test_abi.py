@@ -218,3 +218,49 @@ def test_noalloc_quantiser_refuses_shapes_beyond_its_scratch():
     assert rc == 2 and b"scratch" in lib.flw_last_error()
     rc = lib.flw_quant_qkv_e4m3_noalloc(P, P, P, L.BF16, 0, 64, 128, 64, strides, L.SCALE_HEAD, P, P, P, P, None)
     assert rc == 1 and b"empty" in lib.flw_last_error()
+
+
+@fake_pointers
+def test_qkv_epilogue_transform_refusals_on_the_host():
+    """flw_fp8_scaled_mm_qk_norm_rope_amax checks its transform arguments before any launch."""
+    from flower_amd import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = L.load()
+    P = 1 << 20
+
+    def call(M, N, D, qk, T, cos, sin):
+        return lib.flw_fp8_scaled_mm_qk_norm_rope_amax(P, M, 128, P, N, P, M, P, N, P, N, D, qk, 1, 1e-6, cos, sin,
+                                                       T, P, None)
+    assert call(128, 96, 48, 64, 128, None, None) == 2 and b"head_dim" in lib.flw_last_error()
+    assert call(128, 192, 64, 96, 128, None, None) == 1 and b"qk_cols" in lib.flw_last_error()
+    assert call(128, 192, 64, 128, 100, None, None) == 1 and b"seq_len" in lib.flw_last_error()
+    assert call(128, 192, 64, 128, 128, P, None) == 1 and b"both RoPE" in lib.flw_last_error()
+    rc = lib.flw_fp8_scaled_mm_qk_norm_rope_amax(P, 128, 128, P, 192, P, 128, P, 192, P, 192, 64, 128, 1, 1e-6,
+                                                 None, None, 128, None, None)
+    assert rc == 1 and b"null amax" in lib.flw_last_error()
+
+
+@fake_pointers
+def test_lse_forward_and_dequantiser_refusals_on_the_host():
+    from flower_amd import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = L.load()
+    P = 1 << 20
+    s64 = L.i64s(64 * 64, 64, 64)
+    rc = lib.flw_fp8_swa_fwd_lse(P, s64, P, s64, P, P, P, P, L.SCALE_HEAD, P, L.BF16, s64, 1, 1, 64, 64, 16, None, None)
+    assert rc == 1 and b"null lse" in lib.flw_last_error()
+    rc = lib.flw_fp8_swa_fwd_lse(P, s64, P, s64, P, P, P, P, L.SCALE_HEAD, P, L.BF16, s64, 1, 1, 64, 64, 16, P + 2,
+                                 None)
+    assert rc == 1 and b"lse" in lib.flw_last_error()
+    rc = lib.flw_dequant_e4m3(P, L.LAYOUT_BHTD, 1, 1, 64, 48, P, L.SCALE_HEAD, P, L.BF16, None)
+    assert rc == 2 and b"head_dim" in lib.flw_last_error()
+    rc = lib.flw_dequant_e4m3(P, 5, 1, 1, 64, 64, P, L.SCALE_HEAD, P, L.BF16, None)
+    assert rc == 1 and b"layout" in lib.flw_last_error()
+    rc = lib.flw_dequant_e4m3(P, L.LAYOUT_BHTD, 1, 1, 64, 64, P, 9, P, L.BF16, None)
+    assert rc == 1 and b"granularity" in lib.flw_last_error()
+    rc = lib.flw_dequant_e4m3(P, L.LAYOUT_BHTD, 1, 1, 0, 64, P, L.SCALE_HEAD, P, L.BF16, None)
+    assert rc == 1 and b"empty" in lib.flw_last_error()
+    rc = lib.flw_dequant_e4m3(P, L.LAYOUT_BHTD, 1, 1, 64, 64, P, L.SCALE_HEAD, P + 8, L.BF16, None)
+    assert rc == 1 and b"aligned" in lib.flw_last_error()

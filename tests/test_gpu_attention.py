@@ -20,6 +20,9 @@ from oracle.swa import fp8_swa_simulate, swa_banded
 pytestmark = pytest.mark.gpu
 
 MAX_REL, MEAN_REL = 2e-2, 5e-3
+# Rows of a slice that may exceed MAX_REL, each only within the simulator's MFMA allowance (P codes
+# within the hardware dot product's error of an e4m3 rounding boundary); see the head_dim 32 / 128 test.
+MAX_FLIP_ROWS = 4
 
 
 def run(q, k, v, W, granularity="tensor"):
@@ -208,12 +211,14 @@ def test_full_size_other_head_dims_match_oracle_on_sampled_slices(D):
     per-slice factors: two slices against the simulator, and every slice against the two-pass
     path and under a head reversal.
 
-    The max gate here is 3e-2: the FP8 MFMA's accumulation differs from the simulator's exact dot
-    product by up to ~3e-4 of the largest product (test_gpu_diag.py), and with these factors
-    some rows put most of their weight on a few keys. At D = 128, slice (1, 3), one P code (448 p
-    = 184.023, 1.2e-4 above the 176 / 192 midpoint, on a key holding 29 % of its row's weight)
-    rounds the other way: max 0.0201, mean 0.0014; flipping that code alone in the simulator
-    brings the row to within 0.018 of the kernel's."""
+    The gate is the attention tests' 2e-2 (max |d| / max |ref|), with one MFMA-aware exception:
+    the FP8 MFMA's accumulation differs from the simulator's exact dot product by up to 2^-10 of
+    the dot's largest product (tests/test_gpu_diag.py), so a P code whose 448 p lies that close to
+    an e4m3 rounding boundary may round the other way (at D = 128, slice (1, 3): 448 p = 184.023,
+    1.2e-4 above the 176 / 192 boundary, on a key holding 29 % of its row's weight, moves that row
+    by 0.0201). The simulator reports, per output element, how far such flips can move it
+    (``mfma_rel_err``); an element beyond 2e-2 must lie within 2e-2 plus that allowance, and at
+    most MAX_FLIP_ROWS rows of a slice may need it -- a regression that moves many rows fails."""
     B, H, T, W = 2, 4, 8192, 1000
     g = torch.Generator().manual_seed(128 + D)
     mk = lambda: (torch.randn(B, H, T, D, generator=g) * torch.randn(B, H, 1, 1, generator=g).exp()).to(torch.bfloat16)  # noqa: E731
@@ -225,9 +230,18 @@ def test_full_size_other_head_dims_match_oracle_on_sampled_slices(D):
     v8, vs = per_tensor_fp8(vn, "bh")
     for b, h in [(0, 1), (1, 3)]:
         sl = (slice(b, b + 1), slice(h, h + 1))
-        ref = fp8_swa_simulate(q8[sl], k8[sl], v8[sl], qs[sl], ks[sl], vs[sl], W, chunk=1024)
+        ref, allow = fp8_swa_simulate(q8[sl], k8[sl], v8[sl], qs[sl], ks[sl], vs[sl], W, chunk=1024,
+                                      mfma_rel_err=2.0 ** -10)
         mx, mean = rel_errors(out[sl], ref)
-        assert mx <= 3e-2 and mean <= MEAN_REL, (D, b, h, mx, mean)
+        tol = MAX_REL * np.abs(ref).max()
+        d = np.abs(out[sl].astype(np.float64) - ref)
+        beyond = d > tol
+        rows = np.unique(np.nonzero(beyond)[2])
+        print(f"[attn D{D}] slice ({b}, {h}): max-rel {mx:.4f} mean-rel {mean:.2e}; {beyond.sum()} elements in "
+              f"{len(rows)} rows beyond {MAX_REL} (rows {rows.tolist()[:8]})", flush=True)
+        assert mean <= MEAN_REL, (D, b, h, mean)
+        assert (d[beyond] <= tol + allow[beyond]).all(), (D, b, h, float((d - allow)[beyond].max() / tol))
+        assert len(rows) <= MAX_FLIP_ROWS, (D, b, h, rows.tolist())
     assert np.isfinite(out).all()
     _all_slices_checks(q, k, v, W, out, "bh")
 

@@ -104,11 +104,34 @@ def test_block_weight_cache_is_bit_identical():
     assert torch.equal(plain, cached) and torch.equal(cached, cached2)
 
 
-def test_fused_forward_matches_the_unfused_composition():
-    """The fused path (RMSNorm / GELU fused with the per-row quantisers, residual adds in the GEMM
-    epilogues, attention written in place) against the module-by-module composition: the two
-    differ only where torch's RMSNorm / GELU round differently in the last place."""
+def test_qk_epilogue_and_quantiser_routes_are_bit_identical():
+    """The fused block's two places for QK-norm + RoPE -- the QKV GEMM's epilogue (with the
+    per-head maxima, Q quantised on load) and the Q / K / V quantiser's pass pair -- apply the same
+    transform and derive the same scales and codes, so the block outputs are equal bit for bit
+    (ragged T, so the GEMM's last row tile is partial and positions wrap at the batch boundary)."""
+    blk = make_block(seed=9)
+    x = torch.randn(2, 300, CFG["d_model"], generator=torch.Generator().manual_seed(10)).to("cuda", torch.bfloat16)
+    assert blk._fusable(x)
+    blk.fuse_qk_epilogue = True
+    tr_e = {}
+    a = blk._forward_fused(x, trace=tr_e)
+    blk.fuse_qk_epilogue = False
+    tr_q = {}
+    b = blk._forward_fused(x, trace=tr_q)
+    torch.cuda.synchronize()
+    assert "amax" in tr_e and "q8" in tr_q
+    assert torch.equal(tr_e["q"].contiguous(), tr_q["q"]) and torch.equal(tr_e["k"].contiguous(), tr_q["k"])
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fuse_qk_epilogue", [True, False])
+def test_fused_forward_matches_the_unfused_composition(fuse_qk_epilogue):
+    """The fused path (RMSNorm / GELU fused with the per-row quantisers, QK-norm + RoPE in the QKV
+    epilogue or in the Q / K / V quantiser, residual adds in the GEMM epilogues, attention written
+    in place) against the module-by-module composition (QK-norm and RoPE in torch ops): the two
+    differ only where torch's RMSNorm / HeadRMSNorm / GELU round differently in the last place."""
     blk = make_block(seed=7)
+    blk.fuse_qk_epilogue = fuse_qk_epilogue
     g = torch.Generator().manual_seed(8)
     x = torch.randn(2, 512, CFG["d_model"], generator=g).to("cuda", torch.bfloat16)
     assert blk._fusable(x)
@@ -146,11 +169,12 @@ def test_config5_full_shape_stage_by_stage():
       (iii) the RMSNorm, attention-output and GELU row quantisers: codes and scales bit-exact
             against the per-row recipe on their own h, and h within 1 bf16 ulp of the oracle's
             RMSNorm / GELU on the sampled rows;
-      (iv)  the attention's quantisation point (qkv_heads, base.py:618-639): the fused quantiser's
-            QK-normed and rotated q', k' against the oracle's HeadRMSNorm + RoPE of the QKV output
-            on the sampled rows (the per-value bounds of the fused-quantiser tests), and its e4m3
-            codes and per-head scales of q', k', v bit-exact against the per-head recipe on the
-            whole tensors (so the maxima are those of the transformed tensors).
+      (iv)  the attention's quantisation point (qkv_heads, base.py:618-639) in the QKV epilogue:
+            the stored q', k' against the oracle's HeadRMSNorm + RoPE of the raw projection (the
+            plain GEMM on the same codes) on the sampled rows (the per-value bounds of the
+            fused-quantiser tests) and bit for bit against the Q / K / V quantiser's transform on
+            the whole tensors; v untouched; the epilogue's per-head maxima equal to max |q'|,
+            |k'|, |v| (the attention stage (i) then checks the codes derived from them).
     The traced call returns the same bits as the untraced one."""
     from flower_amd.block import Fp8DecoderBlock, init_block_
     from flower_amd.precision import fp8_weight_cache
@@ -180,27 +204,36 @@ def test_config5_full_shape_stage_by_stage():
     x2 = x.view(M, d)
     w8 = [(to_np(w.view(torch.uint8)), to_np(s)) for w, s in wq]
 
-    # (iv) the quantisation point: q', k' on sampled rows against the oracle's transform of the QKV
-    # output; codes and per-head scales of q', k', v bit-exact on the whole tensors
+    # (iv) the quantisation point in the QKV epilogue: the raw projection (the plain GEMM on the same
+    # codes) against the fused output -- v bit for bit; q', k' on sampled rows against the oracle's
+    # HeadRMSNorm + RoPE of the raw heads, and on the whole tensors bit for bit against the Q / K / V
+    # quantiser's transform; the epilogue's maxima are those of q', k', v.
+    from flower_amd import _lib as L
+    from flower_amd.kernels import qk_norm_rope_quant_e4m3
+    lib = L.load()
     qkv = tr["qkv"].view(M, 3 * d)
-    cos, sin = (to_np(t) for t in blk.attn.rope.tables(T, torch.bfloat16, "cuda"))
-    raw = cpu(qkv).reshape(len(rows), 3, H, D)
+    raw = torch.empty_like(qkv)
+    L.check(lib.flw_fp8_scaled_mm(tr["c1"].data_ptr(), M, d, wq[0][0].data_ptr(), 3 * d, tr["s1"].data_ptr(), M,
+                                  wq[0][1].data_ptr(), 3 * d, raw.data_ptr(), 3 * d, L.stream_of(raw)), "raw qkv")
+    assert torch.equal(qkv[:, 2 * d:], raw[:, 2 * d:])
+    cos_t, sin_t = blk.attn.rope.tables(T, torch.bfloat16, "cuda")
+    rq, rk, rv = (blk.attn._split(t) for t in raw.view(B, T, 3 * d).chunk(3, dim=-1))
+    _, _, _, _, qt, kt = qk_norm_rope_quant_e4m3(rq, rk, rv, qk_norm=True, eps=blk.attn.qk_norm.eps, rope_cos=cos_t,
+                                                 rope_sin=sin_t, granularity="head", return_transformed=True)
+    assert torch.equal(tr["q"].contiguous(), qt) and torch.equal(tr["k"].contiguous(), kt)
+    cos, sin = to_np(cos_t), to_np(sin_t)
+    raw_rows = cpu(raw).reshape(len(rows), 3, H, D)
     pos = rows % T
     for i, name in enumerate(("q", "k")):
-        want = rope(head_rmsnorm(raw[:, i], blk.attn.qk_norm.eps, "bf16"), cos[pos][:, None], sin[pos][:, None], "bf16")
-        got = to_np(tr[name].transpose(1, 2).reshape(M, H, D).index_select(0, ridx))
+        want = rope(head_rmsnorm(raw_rows[:, i], blk.attn.qk_norm.eps, "bf16"), cos[pos][:, None], sin[pos][:, None],
+                    "bf16")
+        got = cpu(qkv).reshape(len(rows), 3, H, D)[:, i]
         d_ = np.abs(got.astype(np.float64) - want)
         assert (d_ > 0).mean() < 2e-3 and (d_ <= 2.0 ** -7 * (np.abs(want) + 1.0)).all(), (name, float(d_.max()))
+    want_amax = qkv.view(M, 3 * H, D).float().abs().amax(dim=(0, 2))
+    assert torch.equal(tr["amax"], want_amax.view(torch.int32))
     vv = blk.attn._split(tr["qkv"].chunk(3, dim=-1)[2])
-    quant = []
-    for i, (vals, codes) in enumerate(((tr["q"], tr["q8"]), (tr["k"], tr["k8"]), (vv, None))):
-        c_, s_ = per_tensor_fp8(to_np(vals.contiguous()), "head")
-        quant.append((c_, s_))
-        if codes is not None:
-            assert np.array_equal(to_np(codes), c_), i
-        assert np.array_equal(to_np(tr["scales"][i * H:(i + 1) * H]).view(np.uint32),
-                              np.asarray(s_, np.float32).reshape(-1).view(np.uint32)), i
-    np.testing.assert_array_equal(to_np(tr["v_tiles"]), vtile_permute(quant[2][0]))
+    quant = [per_tensor_fp8(to_np(t.contiguous()), "head") for t in (tr["q"], tr["k"], vv)]
 
     # (iii) row quantisers: codes / scales on their own h; h against the oracle on sampled rows
     for c, s, h in (("c1", "s1", "h1"), ("c2", "s2", "h2"), ("cg", "sg", "hg")):
@@ -220,10 +253,10 @@ def test_config5_full_shape_stage_by_stage():
     assert dd.max() <= 1 and (dd > 0).mean() < 0.02, ("hg", dd.max(), (dd > 0).mean())
     assert np.abs(got[~big] - want[~big]).max() < 2e-6
 
-    # (ii) the four linears on their own codes
+    # (ii) the four linears on their own codes (QKV: the raw projection, before the q / k transform)
     def closed(cname, sname, wi):
         return round_bf16(scaled_mm(cpu(tr[cname]), w8[wi][0], to_np(tr[sname])[rows], w8[wi][1]))
-    _gemm_close(cpu(qkv), closed("c1", "s1", 0), "qkv")
+    _gemm_close(cpu(raw), closed("c1", "s1", 0), "qkv")
     _gemm_close(cpu(tr["f"]), closed("c2", "s2", 2), "ff1")
     for yname, res, cn, sn, wi in (("x1", x2, "ca", "sa", 1), ("out", tr["x1"], "cg", "sg", 3)):
         y = cpu(out.view(M, d)) if yname == "out" else cpu(tr[yname])

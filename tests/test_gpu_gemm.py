@@ -364,3 +364,62 @@ def test_group_amax_rejects_bad_groups():
     rc = lb.flw_fp8_scaled_mm_group_amax(p, 128, 80, p, 128, s.data_ptr(), 128, s.data_ptr(), 128, p, 128, 64, p,
                                          L.stream_of(t))
     assert rc == 2 and b"K %" in lb.flw_last_error()
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("qk_norm,use_rope", [(True, True), (False, True), (True, False)])
+def test_qk_norm_rope_amax_epilogue(D, qk_norm, use_rope):
+    """flw_fp8_scaled_mm_qk_norm_rope_amax: the QKV projection with qkv_heads' HeadRMSNorm and RoPE
+    (flower/models/base.py:618-639) applied to the q / k columns in the epilogue. Against the plain
+    GEMM y0 on the same codes: the v columns bit for bit; q', k' bit for bit against the Q / K / V
+    quantiser's transform of y0's heads (flw_qk_norm_rope_quant_e4m3, the same arithmetic), and
+    within the fused-quantiser tests' bounds of the oracle's HeadRMSNorm + RoPE of y0; the maxima
+    those of q', k', v. B2 T300: M = 600 (a partial last row tile, positions wrapping at the batch
+    boundary); called twice on one amax buffer."""
+    from flower_amd import _lib as L
+    from flower_amd.attention import RotaryEmbedding
+    from flower_amd.kernels import qk_norm_rope_quant_e4m3
+    from oracle.block import head_rmsnorm, rope
+    lb = L.load()
+    B, T, H, K = 2, 300, 4, 256
+    M, d = B * T, H * D
+    N = 3 * d
+    x8, w8 = codes((M, K), 21), codes((N, K), 22)
+    rng = np.random.default_rng(23)
+    sx = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32) * np.repeat(rng.lognormal(0, 1, 3 * H), D).astype(np.float32)
+    tx8, tw8 = torch.from_numpy(x8).cuda(), torch.from_numpy(w8).cuda()
+    tsx, tsw = torch.from_numpy(sx).cuda(), torch.from_numpy(sw).cuda()
+    cos, sin = RotaryEmbedding(D, T).tables(T, torch.bfloat16, "cuda") if use_rope else (None, None)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    y0 = torch.empty_like(y)
+    amax = torch.full((3 * H,), -1, dtype=torch.int32, device="cuda")
+    for _ in range(2):
+        L.check(lb.flw_fp8_scaled_mm_qk_norm_rope_amax(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), M,
+                                                       tsw.data_ptr(), N, y.data_ptr(), N, D, 2 * d, int(qk_norm),
+                                                       1e-6, L.ptr(cos), L.ptr(sin), T, amax.data_ptr(),
+                                                       L.stream_of(y)), "qkv epilogue")
+    L.check(lb.flw_fp8_scaled_mm(tx8.data_ptr(), M, K, tw8.data_ptr(), N, tsx.data_ptr(), M, tsw.data_ptr(), N,
+                                 y0.data_ptr(), N, L.stream_of(y)), "mm")
+    torch.cuda.synchronize()
+    assert torch.equal(y[:, 2 * d:], y0[:, 2 * d:])
+    split = lambda t: t.view(B, T, H, D).transpose(1, 2)          # noqa: E731
+    q0, k0, v0 = (split(t) for t in y0.chunk(3, dim=-1))
+    _, _, _, _, qt, kt = qk_norm_rope_quant_e4m3(q0, k0, v0, qk_norm=qk_norm, eps=1e-6, rope_cos=cos, rope_sin=sin,
+                                                 granularity="head", return_transformed=True)
+    q1, k1, _ = (split(t) for t in y.chunk(3, dim=-1))
+    assert torch.equal(q1.contiguous(), qt) and torch.equal(k1.contiguous(), kt)
+    for raw, got in ((q0, q1), (k0, k1)):
+        want = raw.float().cpu().numpy()
+        if qk_norm:
+            want = head_rmsnorm(want, 1e-6, "bf16")
+        if use_rope:
+            want = rope(want, cos.float().cpu().numpy(), sin.float().cpu().numpy(), "bf16")
+        g = got.float().cpu().numpy()
+        dd = np.abs(g.astype(np.float64) - want)
+        if qk_norm:
+            assert (dd > 0).mean() < 2e-3 and (dd <= 2.0 ** -7 * (np.abs(want) + 1.0)).all(), float(dd.max())
+        else:
+            assert np.array_equal(g.view(np.uint32), want.view(np.uint32))
+    want_amax = y.float().abs().reshape(M, 3 * H, D).amax(dim=(0, 2)).view(torch.int32)
+    assert torch.equal(amax, want_amax)

@@ -171,15 +171,30 @@ def test_module_fp8_route_at_the_reference_measurement_shape():
     assert torch.isfinite(out).all()
 
 
-def test_module_fp8_route_is_forward_only():
+def test_module_fp8_route_trains_through_the_differentiable_fp8_attention():
+    """With gradients needed the FP8 route is qkv_heads in torch + fp8_swa_attention: its output
+    equals the inference route's (the fused HIP QK-norm + RoPE) to the transform's last-place
+    differences, and gradients reach the projection weights through the FP8 attention's backward
+    (against the same loss through the differentiable bf16 route on the same module, the
+    reference's FP8 error band: relative Frobenius < 0.15)."""
     m = _module(256, 4, 128, 64, seed=74)
-    x = torch.randn(1, 128, 256, device="cuda", dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match="forward-only"):
-        m(x)
-    with pytest.raises(RuntimeError, match="forward-only"):
-        m.forward_unfused(x)
+    x = torch.randn(1, 128, 256, generator=torch.Generator().manual_seed(75)).to("cuda", torch.bfloat16)
+    y = m(x)
+    assert y.requires_grad
     with torch.no_grad():
-        assert m(x).shape == x.shape
+        y_inf = m(x)
+    rel = float((y.detach().float() - y_inf.float()).norm() / y_inf.float().norm())
+    assert rel < 1e-2, rel
+    y.float().square().mean().backward()
+    g_fp8 = m.qkv.weight.grad.detach().float().clone()
+    assert torch.isfinite(g_fp8).all() and g_fp8.abs().sum() > 0
+    m.zero_grad()
+    m.attn_precision = "bf16"
+    m(x).float().square().mean().backward()
+    g_bf16 = m.qkv.weight.grad.detach().float()
+    rel_g = float((g_fp8 - g_bf16).norm() / g_bf16.norm())
+    print(f"[model] fp8 route qkv weight grad vs the bf16 route: {rel_g:.3f}")
+    assert rel_g < 0.15, rel_g
 
 
 def test_module_bf16_route_trains_through_the_hip_kernel():

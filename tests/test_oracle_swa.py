@@ -123,3 +123,43 @@ def test_flop_count_closed_form():
     assert attention_flops(1, 16, 32768, 64, 4096) == 4 * 64 * 2_013_298_688
     T, W = 37, 11
     assert in_window_pairs(T, W) == int(causal_window_mask(T, W).sum())
+
+
+def test_p_code_flip_marks_only_values_near_an_e4m3_boundary():
+    """The e4m3 values 176 and 192 have their rounding boundary at 184: 184.023 (the value the
+    gfx950 MFMA rounded the other way at D = 128) flips by 16 when the value may move 2e-4, not
+    when it may move 1e-5; 180 never flips at 2e-4; 448 stays in range."""
+    from oracle.swa import _p_code_flip
+    x = np.array([184.023, 184.023, 180.0, 448.0, 0.0], np.float32)
+    rel = np.array([2e-4, 1e-5, 2e-4, 1e-3, 1e-3])
+    np.testing.assert_array_equal(_p_code_flip(x, rel), [16.0, 0.0, 0.0, 0.0, 0.0])
+
+
+def test_mfma_allowance_covers_score_errors_within_the_bound():
+    """Planted errors: every raw dot product moved by up to its bound (2^-10 of its largest
+    |product|, random sign) changes the simulator's output by no more than the allowance the
+    unperturbed run reports (plus the fp32-level change of l and the rescales, far below it); with
+    no error allowed the allowance is zero."""
+    from oracle.quant import per_tensor_fp8
+    from oracle.swa import fp8_swa_simulate
+    rng = np.random.default_rng(5)
+    B, H, T, D, W = 1, 1, 384, 64, 160
+    q, k, v = (rng.standard_normal((B, H, T, D)).astype(np.float32) * 2.5 for _ in range(3))
+    c = [per_tensor_fp8(t, "bh") for t in (q, k, v)]
+    args = (c[0][0], c[1][0], c[2][0], c[0][1], c[1][1], c[2][1], W)
+    out, allow = fp8_swa_simulate(*args, mfma_rel_err=2.0 ** -10, chunk=128)
+    assert np.array_equal(out, fp8_swa_simulate(*args, chunk=128))
+    assert (allow > 0).any()
+    _, zero = fp8_swa_simulate(*args, mfma_rel_err=0.0, chunk=128)
+    assert not zero.any()
+
+    def perturb(s, qa, ka):
+        pmax = (np.abs(qa)[:, None, :] * np.abs(ka)[None, :, :]).max(axis=2)
+        return s + rng.uniform(-1.0, 1.0, s.shape) * 2.0 ** -10 * pmax
+
+    for _ in range(3):
+        moved = fp8_swa_simulate(*args, chunk=128, score_perturb=perturb)
+        d = np.abs(moved.astype(np.float64) - out)
+        assert (d <= allow + 2e-3 * np.abs(out).max()).all(), float((d - allow).max())
+    # the planted errors do flip codes: without the allowance some element moves further
+    assert (np.abs(moved.astype(np.float64) - out) > 1e-3 * np.abs(out).max()).any()
