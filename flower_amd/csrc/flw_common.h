@@ -99,6 +99,12 @@ typedef float flw_f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t bf16x2_rne_raw(float a, float b) {   // NaN payloads kept
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((flw_f32x2{a, b}), flw_bf16x2));
 }
+// Two 16-bit lanes of one register: max over packed halves is one v_pk_max_u16.
+typedef unsigned short flw_u16x2 __attribute__((ext_vector_type(2)));
+// Per-half max of |bf16| bit patterns (sign cleared; NaN orders above inf) of packed pair w into m.
+__device__ __forceinline__ flw_u16x2 abs_max_bf16x2(flw_u16x2 m, uint32_t w) {
+  return __builtin_elementwise_max(m, __builtin_bit_cast(flw_u16x2, w & 0x7FFF7FFFu));
+}
 // Every NaN half of a packed bf16 pair made 0x7FC0.
 __device__ __forceinline__ uint32_t bf16x2_canon_nan(uint32_t w) {
   w = (w & 0x7FFFu) > 0x7F80u ? (w & 0xFFFF0000u) | 0x7FC0u : w;
@@ -224,35 +230,43 @@ __device__ __forceinline__ float group_sum(float x, int lanes) {
 //     the row's sum of squares is an fma chain over the lane's values, then group_sum over the
 //     `lanes` lanes that hold the row; the mean is an exact power-of-two scaling; rsqrt is the
 //     hardware v_rsq_f32 (1 ulp, like the reference's GPU torch.rsqrt);
-//   RoPE (base.py:478-483, rotate_half :465-469; when c is not null):
+//   RoPE (base.py:478-483, rotate_half :465-469; when `rope`):
 //     out[2i]   = dtype(dtype(h[2i] c) + dtype(-h[2i+1] s)),
 //     out[2i+1] = dtype(dtype(h[2i+1] c) + dtype(h[2i] s)),
 //     c / s the lane's N entries of the [T, D] tables' row for this position (already loaded).
 // bf16 roundings go through the pair converter (v_cvt_pk_bf16_f32, nearest even) when every value
 // the wave transforms is finite and the norm's eps is positive (no NaN can arise then); otherwise
 // the wave takes the exact software rounding, which also makes every NaN the quiet 0x7FC0 that
-// torch's bf16 rounding gives -- the two agree bit for bit on every finite result. Every lane of a
+// torch's bf16 rounding gives -- the two agree bit for bit on every finite result. With pk (bf16
+// only), the words of the result pairs are also written there, packed as stored (value 2i in the
+// low half), by the last step that ran; pk keeps what it held when no step runs. Every lane of a
 // group must call this together (it exchanges lanes); an invalid lane (padding, zeros) uses no
-// table values and keeps its zeros.
+// table values and keeps its zeros. c / sn always name register arrays (read only when `rope`): a
+// pointer chosen at run time between an array and null would force the arrays into scratch memory.
 template <typename T, bool HW>
 __device__ __forceinline__ void head_norm_rope_core(float* f, bool norm, float eps, int d, int lanes, bool valid,
-                                                    const float* c, const float* sn) {
+                                                    bool rope, const float* c, const float* sn,
+                                                    uint32_t* pk = nullptr) {
   // Separate products and sums, as the reference's separate torch ops round them: no FMA
   // contraction in this function (hipcc contracts a * b + c by default, which would change the
   // fp32 results).
 #pragma clang fp contract(off)
   constexpr int N = Vec16<T>::N;
-  auto rnd2 = [](float& a, float& b) __attribute__((always_inline)) {
+  // Rounds a and b to T; for bf16 also returns them packed (a in the low half).
+  auto rnd2 = [](float& a, float& b) __attribute__((always_inline)) -> uint32_t {
     if constexpr (sizeof(T) == 2) {
       if constexpr (HW) {
         const uint32_t w = bf16x2_rne_raw(a, b);
         a = __uint_as_float(w << 16);
         b = __uint_as_float(w & 0xFFFF0000u);
+        return w;
       } else {
         a = round_bf16(a);
         b = round_bf16(b);
+        return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xFFFF0000u);
       }
     }
+    return 0u;
   };
   if (norm) {
     float ss = 0.0f;
@@ -263,12 +277,13 @@ __device__ __forceinline__ void head_norm_rope_core(float* f, bool norm, float e
 #pragma unroll
     for (int i = 0; i < N; i += 2) {
       float a = f[i] * r, b = f[i + 1] * r;
-      rnd2(a, b);
+      const uint32_t w = rnd2(a, b);
       f[i] = valid ? a : 0.0f;
       f[i + 1] = valid ? b : 0.0f;
+      if (pk != nullptr) pk[i / 2] = valid ? w : 0u;
     }
   }
-  if (c != nullptr && valid) {
+  if (rope && valid) {
 #pragma unroll
     for (int i = 0; i < N; i += 2) {
       float a0 = f[i] * c[i], a1 = f[i + 1] * c[i + 1];
@@ -276,27 +291,28 @@ __device__ __forceinline__ void head_norm_rope_core(float* f, bool norm, float e
       rnd2(a0, a1);
       rnd2(b0, b1);
       float o0 = a0 + b0, o1 = a1 + b1;
-      rnd2(o0, o1);
+      const uint32_t w = rnd2(o0, o1);
       f[i] = o0;
       f[i + 1] = o1;
+      if (pk != nullptr) pk[i / 2] = w;
     }
   }
 }
 
 template <typename T>
 __device__ __forceinline__ void head_norm_rope(float* f, bool norm, float eps, int d, int lanes, bool valid,
-                                               const float* c, const float* sn) {
+                                               bool rope, const float* c, const float* sn) {
   if constexpr (sizeof(T) == 2) {
     uint32_t mx = 0;
 #pragma unroll
     for (int i = 0; i < Vec16<T>::N; ++i) { const uint32_t a = abs_bits(f[i]); mx = mx > a ? mx : a; }
     const bool bad = mx >= 0x7F800000u || (norm && !(eps > 0.0f));
     if (__builtin_amdgcn_ballot_w64(bad) == 0) {     // wave-uniform
-      head_norm_rope_core<T, true>(f, norm, eps, d, lanes, valid, c, sn);
+      head_norm_rope_core<T, true>(f, norm, eps, d, lanes, valid, rope, c, sn);
       return;
     }
   }
-  head_norm_rope_core<T, false>(f, norm, eps, d, lanes, valid, c, sn);
+  head_norm_rope_core<T, false>(f, norm, eps, d, lanes, valid, rope, c, sn);
 }
 
 // LDS pointer type: the 32-bit LDS address of a __shared__ object is (uint32_t)(lds_u8_t*)p.

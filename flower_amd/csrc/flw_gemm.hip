@@ -7,6 +7,8 @@
 // 2 x 2 grid of 64 x 64 wave tiles (2 x 2 v_mfma_f32_32x32x64_f8f6f4 per 64-deep K step);
 // K advances 128 per stage through double-buffered LDS in fragment order (conflict-free
 // ds_read_b128), the next stage's global loads overlapping the current stage's MFMAs.
+#include <type_traits>
+
 #include "flw_common.h"
 
 // m0 is clobbered by the direct-to-LDS loads below; nothing else here uses it.
@@ -216,12 +218,36 @@ __device__ __forceinline__ v8i swz_frag(const uint8_t* tile, int rb, int kc, int
 // With gmax, the max |y| over the tile's rows for each group of gcols columns (the per-head amax of
 // a QKV projection, gcols = head_dim) is reduced in the workgroup and folded into gmax with one
 // atomic max per group and tile (bit patterns of non-negative floats order as unsigned integers).
-template <bool XF = false>
+//
+// XD > 0 (= gcols, the head dim): the q / k transform of xf on the columns n < xf->xcols. A tile
+// holding such columns is read head-major: lane = XD / 8 lanes per head row (its 8 columns at
+// d = 8 (lane % (XD / 8))) x 512 / XD rows, each lane taking the same d of every head in the tile
+// for its row, so one load of the row's RoPE table entries serves all 256 / XD heads (the tables
+// are shared by every head of a position). The table loads of the next row batch are issued
+// before the current batch is transformed, the first batch's before the staging.
+template <int XD = 0>
 __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const float (&sxm)[2], const float* sw,
                                                 int sw_step, uint16_t* y, int64_t ys, const uint16_t* res,
                                                 int64_t rs, int M, int N, uint8_t* st0, uint8_t* st1, int m0,
                                                 int n0, int wave, int lane, uint32_t* gmax = nullptr,
                                                 int gcols = 0, const GemmParams* xf = nullptr) {
+  constexpr int LPR = XD > 0 ? XD / 8 : 1;        // lanes per head row
+  constexpr int RPP = 64 / LPR;                   // rows per batch
+  constexpr int NB = XD > 0 ? 32 / RPP : 1;       // batches over the wave's 32 rows
+  constexpr int HPT = XD > 0 ? 256 / XD : 1;      // heads per tile
+  const bool xform = XD > 0 && n0 < xf->xcols;    // uniform
+  const bool rope = XD > 0 && xform && xf->rcos != nullptr;
+  const int xsub = lane / LPR, xdc = lane % LPR;
+  // Table entries (8 columns from d = 8 xdc) of batch b's row; rows past M use the last row's.
+  auto xtab = [&](int b, uint4& c, uint4& s) __attribute__((always_inline)) {
+    const int m = min(m0 + 32 * wave + RPP * b + xsub, M - 1);
+    const int64_t off = (int64_t)((uint32_t)m % (uint32_t)xf->xT) * XD + 8 * xdc;
+    c = *reinterpret_cast<const uint4*>(xf->rcos + off);
+    s = *reinterpret_cast<const uint4*>(xf->rsin + off);
+  };
+  uint4 tc = make_uint4(0, 0, 0, 0), tsn = tc;
+  if (rope) xtab(0, tc, tsn);
+
   const int wn = wave & 1, wm = wave >> 1, hh = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -254,15 +280,9 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
   lds_barrier();
-  // Wave w stores rows 32 w .. 32 w + 31, two rows (2 x 512 bytes) per instruction.
-  uint32_t lm = 0;                                // max |y| bf16 bits of this lane's chunks
-  // The q / k transform: this lane's 8 columns lie in one head (gcols / 8 lanes per head, an
-  // aligned group of the half-wave, the layout head_norm_rope reduces over); every lane of the
-  // group runs it, rows past M included (they use the last row's table row; their stores are
-  // skipped).
-  const bool xform = XF && n0 + 8 * (lane & 31) < xf->xcols;
-  auto store_row = [&](int q, uint4 v) __attribute__((always_inline)) {
-    const int r = 32 * wave + 2 * q + (lane >> 5), ch = lane & 31;
+  // Stores chunk ch (8 columns) of tile row r, with the residual; mx takes its max |y| bf16 bits
+  // (per 16-bit half).
+  auto store_at = [&](int r, int ch, uint4 v, flw_u16x2& mx) __attribute__((always_inline)) {
     const int m = m0 + r, n = n0 + 8 * ch;
     if (m < M && n < N) {
       uint4 o = v;
@@ -278,82 +298,110 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
       }
       *reinterpret_cast<uint4*>(y + (int64_t)m * ys + n) = o;
       if (gmax) {
-        const uint32_t w4[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = w4[e] & 0x7FFFu, hi = (w4[e] >> 16) & 0x7FFFu;
-          lm = lm > lo ? lm : lo;
-          lm = lm > hi ? lm : hi;
-        }
+        mx = abs_max_bf16x2(mx, o.x);
+        mx = abs_max_bf16x2(mx, o.y);
+        mx = abs_max_bf16x2(mx, o.z);
+        mx = abs_max_bf16x2(mx, o.w);
       }
     }
   };
-  auto staged = [&](int q) __attribute__((always_inline)) {
-    const int r = 32 * wave + 2 * q + (lane >> 5), ch = lane & 31;
+  auto staged_at = [&](int r, int ch) __attribute__((always_inline)) {
     return *reinterpret_cast<const uint4*>((r < 128 ? st0 : st1) + (r & 127) * 512 + 16 * (ch ^ (r & 31)));
   };
-  if (xform) {
-    // This lane's rows are m0 + 32 wave + (lane >> 5) + 2 q: their positions and the table entries of
-    // its 8 columns, loaded four rows at a time (one latency per four rows).
-    const int d = (8 * (lane & 31)) & (gcols - 1);
-    const int xlast = (int)((int64_t)(M - 1) % xf->xT);
-    int xt = (int)((int64_t)min(m0 + 32 * wave + (lane >> 5), M - 1) % xf->xT);
-    const bool rope = xf->rcos != nullptr;
-    uint4 tc[4], tsn[4];
-    auto fetch = [&](int bt) __attribute__((always_inline)) {
+  flw_u16x2 lm = {0, 0};                          // max |y| bf16 bits of this lane's chunks
+  flw_u16x2 lmh[HPT];                             // head-major: per head of the tile
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int q = 4 * bt + e;
-        const int m = m0 + 32 * wave + 2 * q + (lane >> 5);
-        const int64_t toff = (int64_t)(m < M ? xt : xlast) * gcols + d;
-        if (rope) {
-          tc[e] = *reinterpret_cast<const uint4*>(xf->rcos + toff);
-          tsn[e] = *reinterpret_cast<const uint4*>(xf->rsin + toff);
+  for (int h = 0; h < HPT; ++h) lmh[h] = flw_u16x2{0, 0};
+  if (XD > 0 && xform) {
+    // One row batch: the transform of every q / k head of the tile on its 8 columns, with the
+    // pair converter (HW) or the exact software rounding, chosen once for the batch.
+    auto batch = [&](auto hw, int r, const uint4 (&v)[HPT], const float* cf, const float* sf)
+        __attribute__((always_inline)) {
+#pragma unroll
+      for (int h = 0; h < HPT; ++h) {
+        const int nh = n0 + h * XD;               // uniform
+        if (nh >= N) break;
+        uint4 o = v[h];
+        if (nh < xf->xcols) {
+          float f[8];
+          Vec16<uint16_t>::unpack(o, f);
+          uint32_t pk[4] = {o.x, o.y, o.z, o.w};
+          head_norm_rope_core<uint16_t, decltype(hw)::value>(f, xf->xnorm != 0, xf->xeps, XD, LPR, true, rope,
+                                                             cf, sf, pk);
+          o = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         }
-        xt += 2;                                  // the row two below (xT may be 1)
-        xt = xt >= xf->xT ? xt - xf->xT : xt;
-        xt = xt >= xf->xT ? xt - xf->xT : xt;
+        store_at(r, h * LPR + xdc, o, lmh[h]);
       }
     };
+#pragma unroll 1
+    for (int b = 0; b < NB; ++b) {
+      uint4 nc = tc, ns = tsn;
+      if (rope && b + 1 < NB) xtab(b + 1, nc, ns);
+      const int r = 32 * wave + RPP * b + xsub;
+      uint4 v[HPT];
+      flw_u16x2 fm = {0, 0};                      // max |x| of the values transformed
 #pragma unroll
-    for (int bt = 0; bt < 4; ++bt) {
-      fetch(bt);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int q = 4 * bt + e;
-        float f[8], cf[8], sf[8];
-        Vec16<uint16_t>::unpack(staged(q), f);
-        if (rope) {
-          Vec16<uint16_t>::unpack(tc[e], cf);
-          Vec16<uint16_t>::unpack(tsn[e], sf);
+      for (int h = 0; h < HPT; ++h) {
+        v[h] = staged_at(r, h * LPR + xdc);
+        if (n0 + h * XD < min(N, xf->xcols)) {
+          fm = abs_max_bf16x2(fm, v[h].x);
+          fm = abs_max_bf16x2(fm, v[h].y);
+          fm = abs_max_bf16x2(fm, v[h].z);
+          fm = abs_max_bf16x2(fm, v[h].w);
         }
-        head_norm_rope<uint16_t>(f, xf->xnorm != 0, xf->xeps, gcols, gcols >> 3, true, rope ? cf : nullptr, sf);
-        // every value is a bf16 value now (rounded by the transform): its upper half is the code
-        store_row(q, make_uint4((__float_as_uint(f[0]) >> 16) | (__float_as_uint(f[1]) & 0xFFFF0000u),
-                                (__float_as_uint(f[2]) >> 16) | (__float_as_uint(f[3]) & 0xFFFF0000u),
-                                (__float_as_uint(f[4]) >> 16) | (__float_as_uint(f[5]) & 0xFFFF0000u),
-                                (__float_as_uint(f[6]) >> 16) | (__float_as_uint(f[7]) & 0xFFFF0000u)));
       }
+      float cf[8] = {}, sf[8] = {};
+      if (rope) {
+        Vec16<uint16_t>::unpack(tc, cf);
+        Vec16<uint16_t>::unpack(tsn, sf);
+      }
+      // The pair converter only where no NaN can arise: every input finite, eps > 0.
+      const bool bad = (fm[0] > fm[1] ? fm[0] : fm[1]) >= 0x7F80u || (xf->xnorm != 0 && !(xf->xeps > 0.0f));
+      if (__builtin_amdgcn_ballot_w64(bad) == 0)
+        batch(std::true_type{}, r, v, cf, sf);
+      else
+        batch(std::false_type{}, r, v, cf, sf);
+      tc = nc;
+      tsn = ns;
     }
   } else {
+    // Wave w stores rows 32 w .. 32 w + 31, two rows (2 x 512 bytes) per instruction.
 #pragma unroll 4
-    for (int q = 0; q < 16; ++q) store_row(q, staged(q));
+    for (int q = 0; q < 16; ++q) {
+      const int r = 32 * wave + 2 * q + (lane >> 5), ch = lane & 31;
+      store_at(r, ch, staged_at(r, ch), lm);
+    }
   }
   // The next tile's loads refill st0 / st1: every wave's reads of the staged tile are done.
   __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
   lds_barrier();
   if (gmax) {
-    // Lanes ch .. ch + gcols / 8 - 1 of each half-wave cover one group's columns.
-    const int lpg = gcols >> 3;
-    for (int o = 1; o < lpg; o <<= 1) {
-      const uint32_t t = (uint32_t)__shfl_xor((int)lm, o, 64);
-      lm = lm > t ? lm : t;
-    }
-    const uint32_t t = (uint32_t)__shfl_xor((int)lm, 32, 64);
-    lm = lm > t ? lm : t;
     uint32_t* red = reinterpret_cast<uint32_t*>(st0);          // [8 waves][32 groups at most]
-    const int ch = lane & 31;
-    if (lane < 32 && (ch & (lpg - 1)) == 0) red[wave * 32 + ch / lpg] = lm;
+    if (XD > 0 && xform) {
+      // Every lane of the wave holds rows of every head: the wave's max per head.
+#pragma unroll
+      for (int h = 0; h < HPT; ++h) {
+        uint32_t v = lmh[h][0] > lmh[h][1] ? lmh[h][0] : lmh[h][1];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t t = (uint32_t)__shfl_xor((int)v, o, 64);
+          v = v > t ? v : t;
+        }
+        if (lane == 0) red[wave * 32 + h] = v;
+      }
+    } else {
+      // Lanes ch .. ch + gcols / 8 - 1 of each half-wave cover one group's columns.
+      const int lpg = gcols >> 3;
+      uint32_t lmx = lm[0] > lm[1] ? lm[0] : lm[1];
+      for (int o = 1; o < lpg; o <<= 1) {
+        const uint32_t t = (uint32_t)__shfl_xor((int)lmx, o, 64);
+        lmx = lmx > t ? lmx : t;
+      }
+      const uint32_t t = (uint32_t)__shfl_xor((int)lmx, 32, 64);
+      lmx = lmx > t ? lmx : t;
+      const int ch = lane & 31;
+      if (lane < 32 && (ch & (lpg - 1)) == 0) red[wave * 32 + ch / lpg] = lmx;
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     lds_barrier();
     const int ngr = 256 / gcols, tid = wave * 64 + lane;
@@ -369,7 +417,7 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
 }
 
 // One 256 x 256 output tile: K loop over two LDS stages, then the scaled bf16 epilogue.
-template <bool XF = false>
+template <int XD = 0>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
                                           int n0, int wave, int lane, int sbase, int nst, int split) {
   const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
@@ -467,8 +515,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
       const int m = min(m0 + 64 * wm + 32 * j + (lane & 31), p.M - 1);
       sxm[j] = p.sx[(int64_t)m * p.sx_step];
     }
-    staged_epilogue<XF>(acc, sxm, p.sw, p.sw_step, p.y, p.ys, p.res, p.rs, p.M, p.N, st0, st1, m0, n0, wave,
-                        lane, p.gmax, p.gcols, XF ? &p : nullptr);
+    staged_epilogue<XD>(acc, sxm, p.sw, p.sw_step, p.y, p.ys, p.res, p.rs, p.M, p.N, st0, st1, m0, n0, wave,
+                        lane, p.gmax, p.gcols, XD > 0 ? &p : nullptr);
     return;
   }
   float sxm[2];
@@ -675,9 +723,9 @@ __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0,
   lds_barrier();
 }
 
-// XF: the q / k transform epilogue of flw_fp8_scaled_mm_qk_norm_rope_amax, compiled as its own
-// instance so that the other GEMMs keep their register allocation.
-template <int TM, bool XF = false>
+// XD > 0: the q / k transform epilogue of flw_fp8_scaled_mm_qk_norm_rope_amax for head dim XD,
+// compiled as instances of their own so that the other GEMMs keep their register allocation.
+template <int TM, int XD = 0>
 __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p) {
   // One array per stage: every LDS access below names its stage at compile time, so the
   // compiler can see that the direct-to-LDS loads in flight write the other stage.
@@ -705,7 +753,7 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
     const int tm = first_m + (tt % (kGroupM * p.tiles_n)) % gm;
     const int tn = (tt % (kGroupM * p.tiles_n)) / gm;
     const int s0 = split * nst_all / p.splits, s1 = (split + 1) * nst_all / p.splits;
-    if constexpr (TM == 256) gemm_tile<XF>(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
+    if constexpr (TM == 256) gemm_tile<XD>(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
     else gemm_tile_128(p, st0, st1, tm * TM, tn * kFBN, wave, lane, s0, s1 - s0, split);
   }
 }
@@ -1012,8 +1060,10 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
       if (p.splits == 1) p.part = nullptr;
     }
     const void* kern = narrow ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<128>)
-                     : xform != nullptr ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, true>)
-                                        : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256>);
+                     : xform == nullptr ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256>)
+                     : gcols == 32 ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, 32>)
+                     : gcols == 64 ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, 64>)
+                     : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, 128>);
     // Persistent: one workgroup per CU (each holds 128 KB of LDS), at most one per work item.
     const int64_t items = (int64_t)p.tiles_n * p.tiles_m * p.splits;
     const int64_t grid = items < compute_units() ? items : compute_units();

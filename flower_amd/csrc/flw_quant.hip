@@ -90,14 +90,14 @@ template <typename T>
 __device__ __forceinline__ void qk_transform(const QTensor& t, float* f, int64_t row, int64_t cv, int vpr,
                                              int64_t d3, bool valid) {
   constexpr int N = Vec16<T>::N;
-  float c[N], sn[N];
+  float c[N] = {}, sn[N] = {};
   const bool rope = t.rcos != nullptr && valid;
   if (rope) {
     const int64_t off = row * d3 + cv * N;
     Vec16<T>::load(static_cast<const T*>(t.rcos) + off, c);
     Vec16<T>::load(static_cast<const T*>(t.rsin) + off, sn);
   }
-  head_norm_rope<T>(f, t.norm, t.eps, (int)d3, vpr, valid, t.rcos != nullptr ? c : nullptr, sn);
+  head_norm_rope<T>(f, t.norm, t.eps, (int)d3, vpr, valid, t.rcos != nullptr, c, sn);
 }
 
 template <typename T, bool XFORM = false>
