@@ -1,6 +1,6 @@
 """Benchmark of the FP8 sliding-window-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|c2_train|swa_bf16|swa_bf16_450m]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|c2_train|swa_bf16|swa_bf16_450m|fp8_train_450m]
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
@@ -32,6 +32,8 @@ beside it, in GEMM TFLOP/s.
 --workload swa_bf16 / swa_bf16_450m measure the bf16 sliding-window attention training op (forward
 with log-sum-exp, then the backward) at the reference's measurement shape B1 H20 T4096 D64 W2048 /
 its 450M model shape B2 H20 T8192 D64 W2048; roofline = the backward entry point.
+--workload fp8_train_450m measures the differentiable FP8 attention (fp8_swa_attention: FP8 forward,
+bf16 backward at the dequantised Q, K, V) as one autograd training step at the 450M model shape.
 --workload c2_train measures the C2 linear as an FP8 training step (forward, dgrad and wgrad GEMMs
 with their quantisers), beside torch's bf16 matmuls of the same three products.
 Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
@@ -79,6 +81,8 @@ WORKLOADS = {
     # reference's own measurement shape (swa_attention.py:10-14, :40-43) and its 450M model shape
     "swa_bf16": dict(B=1, H=20, T=4096, D=64, W=2048, ref="B1 H20 T4096 D64 W2048"),
     "swa_bf16_450m": dict(B=2, H=20, T=8192, D=64, W=2048, ref="B2 H20 T8192 D64 W2048"),
+    # the differentiable FP8 attention (FP8 forward, bf16 backward) as a training step, 450M shape
+    "fp8_train_450m": dict(B=2, H=20, T=8192, D=64, W=2048, granularity="head", ref="B2 H20 T8192 D64 W2048"),
 }
 DATA = {
     "lognormal_heads": "synthetic (seeded; bf16 N(0,1) x a lognormal(0,1) factor per head)",
@@ -533,6 +537,9 @@ def main():
                          "matmul, FP8 _scaled_mm with per-row x per-column and per-tensor scales) at "
                          "the C2 shape and C5's four linear shapes, the reference point for the "
                          "library's own GEMMs; prints one JSON line per shape")
+    ap.add_argument("--qk-route", choices=("epilogue", "quantiser"), default="epilogue",
+                    help="c5 only: where the block applies HeadRMSNorm + RoPE to q and k -- in the QKV "
+                         "GEMM's epilogue (the default) or in both quantiser passes")
     ap.add_argument("--issue-probe", action="store_true",
                     help="instead of a workload, measure the per-SIMD issue cost of the attention "
                          "loop's instruction classes and their overlap with the FP8 MFMA "
@@ -566,6 +573,8 @@ def main():
         line = run_swa_bf16(cfg, args)
     elif args.workload == "c2_train":
         line = run_linear_train(cfg, args)
+    elif args.workload == "fp8_train_450m":
+        line = run_fp8_train(cfg, args)
     else:
         line = run_attention(cfg, args)
     print(json.dumps(line), flush=True)
@@ -663,6 +672,7 @@ def run_block(cfg, args):
     blk = Fp8DecoderBlock(d, cfg["num_heads"], cfg["ffn_dim"], cfg["W"])
     init_block_(blk, std=cfg["w_std"], seed=0)
     blk = blk.to("cuda", torch.bfloat16)
+    blk.fuse_qk_epilogue = args.qk_route == "epilogue"
     g = torch.Generator().manual_seed(0)
     x = torch.randn(B, T, d, generator=g).to("cuda", torch.bfloat16)
     flops = block_flops(T, B, d, cfg["ffn_dim"], cfg["num_heads"], cfg["W"])
@@ -690,6 +700,7 @@ def run_block(cfg, args):
         "config": {"workload": "Fp8DecoderBlock forward, BASELINE C5", "B": B, "T": T, "d_model": d,
                    "num_heads": cfg["num_heads"], "ffn_dim": cfg["ffn_dim"], "window": cfg["W"],
                    "qk_norm": blk.attn.qk_norm is not None, "rope_base": blk.attn.rope._base,
+                   "qk_route": args.qk_route,
                    "scales": "per-head attention, per-row x per-channel linears"},
         "roofline": {"bound": "mfma", "achieved": round(flops / (ms * 1e-3) / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
@@ -800,6 +811,75 @@ def run_swa_bf16(cfg, args):
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_swa_bf16(cfg)
     return line
+
+
+def bench_fp8_train(cfg, steps, warmup):
+    """One autograd training step of fp8_swa_attention (bf16 q, k, v with requires_grad, a seeded
+    dO): the forward (the e4m3 quantiser pair over Q, K, V, then the FP8 kernel) and the backward
+    (three e4m3 dequantisers, the bf16 forward recomputing O and the log-sum-exp at the dequantised
+    values, the bf16 backward), each bracketed by events on the current stream."""
+    from flower_amd.kernels import fp8_swa_attention
+    B, H, T, D, W = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["W"]
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, T, D, generator=g).to("cuda", torch.bfloat16) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def fwd():
+        return fp8_swa_attention(q, k, v, W, granularity=cfg["granularity"])
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        fwd().backward(do)
+
+    _spin_up(step)
+    for _ in range(warmup):
+        step()
+    wall_ms = _wall_ms(step, steps)
+    ev = _events(steps, per=3)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        q.grad = k.grad = v.grad = None
+        ev[i][0].record()
+        out = fwd()
+        ev[i][1].record()
+        out.backward(do)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    f_ms = np.array([a.elapsed_time(b) for a, b, _ in ev])
+    b_ms = np.array([b.elapsed_time(c) for _, b, c in ev])
+    pairs = B * H * in_window_pairs(T, W)
+    return dict(ms_per_step=wall_ms, fwd_ms=float(f_ms.mean()), bwd_ms=float(b_ms.mean()),
+                fwd_flops=4 * D * pairs, bwd_flops=10 * D * pairs)
+
+
+def run_fp8_train(cfg, args):
+    """The differentiable FP8 attention, one training step. FLOPs per in-window pair: forward 4*D
+    (on the FP8 MFMA), backward 10*D (bf16 MFMA); the backward's recomputed bf16 forward (4*D more)
+    is not counted. roofline = the FP8 forward (its share of the step on the FP8 peak)."""
+    r = bench_fp8_train(cfg, args.steps, args.warmup)
+    flops = r["fwd_flops"] + r["bwd_flops"]
+    value = flops / (r["ms_per_step"] * 1e-3) / 1e12
+    f_tf = r["fwd_flops"] / (r["fwd_ms"] * 1e-3) / 1e12
+    b_tf = r["bwd_flops"] / (r["bwd_ms"] * 1e-3) / 1e12
+    return {
+        "metric": "FP8 SWA attention training step TFLOPS (FP8 forward, bf16 backward at the dequantised "
+                  "Q/K/V), 450M model shape",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "spin_up_s": SPIN_UP_S, "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8_e4m3 forward, bf16 backward (fp32 softmax / accumulate)", "data": DATA["swa_bf16"],
+        "config": {"workload": f"fp8_swa_attention forward + backward, {cfg['ref']}", "B": cfg["B"], "H": cfg["H"],
+                   "T": cfg["T"], "D": cfg["D"], "window": cfg["W"], "causal": True,
+                   "scales": cfg["granularity"]},
+        "roofline": {"bound": "mfma", "achieved": round(f_tf, 2), "peak": 5000.0, "unit": "TFLOP/s",
+                     "frac": round(f_tf / 5000.0, 4), "traffic": None,
+                     "kernel": "the FP8 forward (quantiser pair + swa_fwd_kernel<64, bf16>), events around it",
+                     "kernel_ms": round(r["fwd_ms"], 4), "flop_per_launch": r["fwd_flops"]},
+        "backward": {"bound": "mfma", "achieved": round(b_tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(b_tf / BF16_PEAK_TFLOPS, 4), "ms": round(r["bwd_ms"], 4),
+                     "kernels": "3 x dequant + swa_bf16_fwd (recompute) + flw_swa_bf16_bwd"},
+    }
 
 
 def bench_linear_train(cfg, steps, warmup):

@@ -35,7 +35,7 @@ COMMON = [
 # Attention: MFMA accumulators in ordinary VGPRs (the online-softmax rescale works on them in
 # place instead of copying through AGPRs), and no IEEE mode, since in IEEE mode every fmax operand
 # of the row max is first re-quietened (one extra VALU op per score); NaN inputs still give NaN
-# rows without it. The GEMM keeps the default form: its 256 accumulators per lane live in AGPRs.
+# rows without it. The other sources keep the compiler's default forms.
 PER_SOURCE = {"flw_swa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans", "-mno-amdgpu-ieee"]}
 NOISE = "'-packed-fp32-ops' is not a recognized feature"
 
