@@ -229,15 +229,25 @@ template <int XD = 0>
 __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const float (&sxm)[2], const float* sw,
                                                 int sw_step, uint16_t* y, int64_t ys, const uint16_t* res,
                                                 int64_t rs, int M, int N, uint8_t* st0, uint8_t* st1, int m0,
-                                                int n0, int wave, int lane, uint32_t* gmax = nullptr,
+                                                int n0, int wave, int lane_id, uint32_t* gmax = nullptr,
                                                 int gcols = 0, const GemmParams* xf = nullptr) {
+  // In the transform instances the lane id reaches the epilogue through an opaque copy, so the LDS
+  // addresses derived from it are computed per tile instead of being hoisted out of the tile loop
+  // into registers held through every K loop (where they spilled and slowed the K loop).
+  int lane = lane_id;
+  if constexpr (XD > 0) asm volatile("" : "+v"(lane));
   constexpr int LPR = XD > 0 ? XD / 8 : 1;        // lanes per head row
   constexpr int RPP = 64 / LPR;                   // rows per batch
   constexpr int NB = XD > 0 ? 32 / RPP : 1;       // batches over the wave's 32 rows
   constexpr int HPT = XD > 0 ? 256 / XD : 1;      // heads per tile
   const bool xform = XD > 0 && n0 < xf->xcols;    // uniform
   const bool rope = XD > 0 && xform && xf->rcos != nullptr;
-  const int xsub = lane / LPR, xdc = lane % LPR;
+  // The head-major lane coordinates are recomputed in every epilogue: derived from an opaque copy
+  // of the lane id, they and the LDS / table addresses built on them cannot be hoisted out of the
+  // tile loop, where they would hold registers (or scratch) through every K loop.
+  int xl = lane;
+  if constexpr (XD > 0) asm volatile("" : "+v"(xl));
+  const int xsub = xl / LPR, xdc = xl % LPR;
   // Table entries (8 columns from d = 8 xdc) of batch b's row; rows past M use the last row's.
   auto xtab = [&](int b, uint4& c, uint4& s) __attribute__((always_inline)) {
     const int m = min(m0 + 32 * wave + RPP * b + xsub, M - 1);
