@@ -68,6 +68,9 @@ SIGNATURES = {
     "flw_fp8_swa_fwd_scale_strides": (c_int, [c_void_p, _P64, c_void_p, _P64, c_void_p, c_void_p, c_void_p,
                                               c_void_p, c_int64, c_int64, c_void_p, c_int, _P64, c_int64,
                                               c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "flw_fp8_swa_fwd_bhtd": (c_int, [c_void_p, _P64, c_void_p, _P64, c_void_p, _P64, c_void_p, c_void_p,
+                                     c_void_p, c_int64, c_int64, c_void_p, c_int, _P64, c_int64, c_int64,
+                                     c_int64, c_int64, c_int64, c_void_p]),
     "flw_fp8_swa_fwd_qx": (c_int, [c_void_p, _P64, c_void_p, c_void_p, c_void_p, _P64, c_void_p, c_void_p,
                                    c_void_p, c_void_p, c_int, c_void_p, c_int, _P64, c_int64, c_int64, c_int64,
                                    c_int64, c_int64, c_void_p]),

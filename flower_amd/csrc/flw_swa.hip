@@ -58,6 +58,8 @@ struct SwaParams {
   int64_t qsb, qsh, qst;      // byte strides of q8
   int64_t ksb, ksh, kst;      // byte strides of k8
   int64_t vt_slice;           // bytes per (b, h) slice of the tiled V
+  int64_t vsb, vsh, vst;      // byte strides of V when it is given as (B, H, T, D) codes (vt then
+                              // points at those codes; the kernel instance with VB set)
   const float* qs;
   const float* ks;
   const float* vs;
@@ -109,6 +111,40 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* lds, int off) {
   return r;
 }
 
+// A V tile staged as (B, H, T, D) rows: 64 rows of D bytes, 16-byte chunk c of row r at c ^ vswz(r).
+// The swizzle keeps both accesses free of bank conflicts: the staging writes (16 lanes = 16
+// consecutive chunks of consecutive rows) and the transposed reads below (a 16-lane group reads
+// one 16-byte chunk of 8 rows r0 + {0-3, 8-11}: the row bits 3 and, at D = 128, 1 pick the chunk).
+template <int D>
+__device__ __forceinline__ int vswz(int r) {
+  if (D == 128) return ((r >> 1) & 1) | (((r >> 3) & 1) << 1);
+  return (r >> 3) & 1;
+}
+
+// The PV operand fragment of dims 32 db .. 32 db + 31 from a staged (B, H, T, D) V tile, byte for
+// byte the tiled V's fragment (load_frag): lane (d = lane % 32, h = lane / 32) holds keys
+// 32 kb + 8 a + 4 h + c in byte 16 kb + 4 a + c. ds_read_b64_tr_b8 works on groups of 16 lanes: lane
+// 2 j + a of a group supplies the address of 8 consecutive bytes (row j, columns 8 a .. 8 a + 7 of
+// the group's 16) and lane n receives column n of the 8 rows, byte j from row j. Four reads give
+// the 32 keys: read t covers rows 16 (t % 2) + 32 (t / 2) + 4 h + {0-3, 8-11}.
+template <int D>
+__device__ __forceinline__ v8i vtr_frag(const uint8_t* lds, int db, int lane) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  const int s = lane & 15, j = s >> 1, a = s & 1, g1 = (lane >> 4) & 1, h = lane >> 5;
+  const int r0 = 4 * h + (j < 4 ? j : j + 4);
+  const int off = r0 * D + 16 * ((2 * db + g1) ^ vswz<D>(r0)) + 8 * a;
+  v8i out;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const v2i w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (lds_v2i*)(lds_u8_t*)(lds + off + (16 * (t & 1) + 32 * (t >> 1)) * D));
+    out[2 * t] = w.x;
+    out[2 * t + 1] = w.y;
+  }
+  return out;
+}
+
 // A K fragment (32 keys x 64 bytes for this lane) from its swizzled region (offsets from the lane).
 __device__ __forceinline__ v8i load_kfrag(const uint8_t* lds, int region, int x0, int x1) {
   const uint4 a = *reinterpret_cast<const uint4*>(lds + region + x0);
@@ -143,7 +179,12 @@ struct Scores {
 
 // At D <= 64 the kernel takes 120 VGPRs (D = 32: 110), so four workgroups (16 waves) share a CU;
 // the launch bound only asks for three. D = 128 asks for two (its O^T needs 64 VGPRs more).
-template <int D, typename OutT>
+// VB: V arrives as (B, H, T, D) e4m3 codes (the reference's layout, strides vsb / vsh / vst). Its
+// tiles are staged as they are (64 key rows of D bytes, 16-byte chunk c of row r at c ^ vswz(r))
+// and the PV operand is read with ds_read_b64_tr_b8, which hands each lane one dim of 8 key rows:
+// the same bytes in the same order as the tiled V's fragment reads, so the results are those of
+// the tiled-V instance.
+template <int D, typename OutT, bool VB = false>
 __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParams p) {
   constexpr int NDC = D >= 64 ? D / 64 : 1;   // 64-deep K chunks of the QK^T product
   constexpr int NDB = D / 32;                  // 32-row blocks of O^T
@@ -258,8 +299,10 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
 
   // K rows: scalar tile base + a fixed 32-bit offset per thread; V tiles are contiguous.
   const uint8_t* kbase = p.k8 + b * p.ksb + h * p.ksh;
-  const uint8_t* vbase = p.vt + (int64_t)bh * p.vt_slice;
+  const uint8_t* vbase = VB ? p.vt + b * p.vsb + h * p.vsh : p.vt + (int64_t)bh * p.vt_slice;
   uint32_t koff[CPT], ldsk[CPT];
+  // VB: the chunk's V row offset and its swizzled place in the staged tile.
+  uint32_t voff[VB ? CPT : 1], ldsv[VB ? CPT : 1];
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int i = min(tid + 256 * j, KCH - 1);
@@ -267,6 +310,10 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
     const int d0 = 16 * g;
     const int blk = kk >> 5, krow = kk & 31, dc = d0 >> 6, h2 = (d0 >> 5) & 1, cc = (d0 >> 4) & 1;
     koff[j] = (uint32_t)(kk * p.kst + 16 * g);
+    if constexpr (VB) {
+      voff[j] = (uint32_t)(kk * p.vst + 16 * g);
+      ldsv[j] = (uint32_t)(kk * D + 16 * (g ^ vswz<D>(kk)));
+    }
     // Chunk (krow + 32 h2) of fragment region (blk, dc, cc), its index XORed with 4 (h2 + 2 cc):
     // the 16 lanes of a ds_write_b128 phase (4 rows x 4 chunks) then fall in 16 distinct bank
     // groups, and the fragment reads below (one region and one lane half per phase) stay a
@@ -282,7 +329,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(kbase), 0, (int)((int64_t)(T - 1) * p.kst + D), kBufferFlags);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(vbase), 0, (int)p.vt_slice, kBufferFlags);
+      const_cast<uint8_t*>(vbase), 0, VB ? (int)((int64_t)(T - 1) * p.vst + D) : (int)p.vt_slice, kBufferFlags);
   auto load_tile = [&](int n0) __attribute__((always_inline)) {
     const int ks = n0 * (int)p.kst, vs = (n0 >> 6) * VT_BYTES;
 #pragma unroll
@@ -290,8 +337,11 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
       const int i = tid + 256 * j;
       if (KCH % 256 == 0 || i < KCH) {
         const auto kv = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)(koff[j] + (uint32_t)ks), 0, 0);
-        const auto vv = __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * i, vs, 0);
         kreg[j] = make_uint4(kv[0], kv[1], kv[2], kv[3]);
+        // VB: V rows past T read as zero, the tiled V's padding keys
+        std::remove_const_t<decltype(kv)> vv;
+        if constexpr (VB) vv = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(voff[j] + (uint32_t)(n0 * (int)p.vst)), 0, 0);
+        else vv = __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * i, vs, 0);
         vreg[j] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
       }
     }
@@ -302,7 +352,11 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
       const int i = tid + 256 * j;
       if (KCH % 256 == 0 || i < KCH) {
         *reinterpret_cast<uint4*>(&lds_k[buf][ldsk[j]]) = kreg[j];
-        *reinterpret_cast<uint4*>(&lds_v[buf][16 * i]) = vreg[j];
+        if constexpr (VB) {
+          *reinterpret_cast<uint4*>(&lds_v[buf][ldsv[j]]) = vreg[j];
+        } else {
+          *reinterpret_cast<uint4*>(&lds_v[buf][16 * i]) = vreg[j];
+        }
       }
     }
   };
@@ -426,7 +480,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
     __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      const v8i vf = load_frag(lv, (db * 2 * 64 + lane) * 16);
+      const v8i vf = VB ? vtr_frag<D>(lv, db, lane) : load_frag(lv, (db * 2 * 64 + lane) * 16);
       o[db] *= alpha;
       o[db] = mfma_32x32x64_f8(vf, pf, o[db]);
     }
@@ -488,9 +542,11 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
 
 
 template <int D>
-static void launch_d(const SwaParams& p, int out_dtype, dim3 grid, hipStream_t s, Timer tm) {
-  const void* k = out_dtype == FLW_F32 ? reinterpret_cast<const void*>(&swa_fwd_kernel<D, float>)
-                                       : reinterpret_cast<const void*>(&swa_fwd_kernel<D, uint16_t>);
+static void launch_d(const SwaParams& p, int out_dtype, bool vb, dim3 grid, hipStream_t s, Timer tm) {
+  const void* k = vb ? (out_dtype == FLW_F32 ? reinterpret_cast<const void*>(&swa_fwd_kernel<D, float, true>)
+                                             : reinterpret_cast<const void*>(&swa_fwd_kernel<D, uint16_t, true>))
+                     : (out_dtype == FLW_F32 ? reinterpret_cast<const void*>(&swa_fwd_kernel<D, float>)
+                                             : reinterpret_cast<const void*>(&swa_fwd_kernel<D, uint16_t>));
   (void)launch_ext(k, grid, dim3(256), 0, s, p, tm.start, tm.stop);
 }
 
@@ -499,8 +555,13 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
                    void* out, int out_dtype, const int64_t* ost, int64_t B, int64_t H, int64_t T,
                    int64_t D, int64_t window, hipStream_t stream, Timer tm, const void* qx = nullptr,
                    const int64_t* xst = nullptr, const float* qr = nullptr, const uint32_t* qamax = nullptr,
-                   float* lse = nullptr) {
+                   float* lse = nullptr, const int64_t* vst = nullptr) {
   FLW_REQUIRE(q8 && k8 && vt && qs && ks && vs && out && qst && kst && ost, FLW_E_INVALID, "null pointer argument");
+  if (vst != nullptr) {
+    for (int i = 0; i < 3; ++i)
+      FLW_REQUIRE(vst[i] % 16 == 0 && vst[i] >= 0, FLW_E_INVALID, "v8 strides must be non-negative multiples of 16 bytes");
+    FLW_REQUIRE((T - 1) * vst[2] + D < ((int64_t)1 << 31), FLW_E_UNSUPPORTED, "one (b, h) slice of v8 must span < 2^31 bytes");
+  }
   if (qx != nullptr) {
     const int64_t vec = out_dtype == FLW_F32 ? 4 : 8;
     FLW_REQUIRE(xst != nullptr && qr != nullptr, FLW_E_INVALID, "null Q strides / reciprocals");
@@ -531,6 +592,7 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.qsb = qst[0]; p.qsh = qst[1]; p.qst = qst[2];
   p.ksb = kst[0]; p.ksh = kst[1]; p.kst = kst[2];
   p.vt_slice = ((T + 63) / 64) * 64 * D;
+  if (vst != nullptr) { p.vsb = vst[0]; p.vsh = vst[1]; p.vst = vst[2]; }
   p.qs = qs; p.ks = ks; p.vs = vs; p.ssb = ssb; p.ssh = ssh;
   p.out = out; p.osb = ost[0]; p.osh = ost[1]; p.ost = ost[2];
   p.H = (int)H; p.T = (int)T; p.W = (int)W; p.nM = (int)nM;
@@ -544,9 +606,10 @@ static int swa_fwd(const uint8_t* q8, const int64_t* qst, const uint8_t* k8, con
   p.ramp = W > 0 ? (int)std::min<int64_t>(nM, (W - 1) / kBM + 1) : 0;
   p.group_slices = ((B * H) % 8 == 0 && (p.nwg & 7) == 0) ? (int)(B * H / 8) : (int)(B * H);
   dim3 grid((unsigned)p.nwg);
-  if (D == 32) launch_d<32>(p, out_dtype, grid, stream, tm);
-  else if (D == 64) launch_d<64>(p, out_dtype, grid, stream, tm);
-  else launch_d<128>(p, out_dtype, grid, stream, tm);
+  const bool vb = vst != nullptr;
+  if (D == 32) launch_d<32>(p, out_dtype, vb, grid, stream, tm);
+  else if (D == 64) launch_d<64>(p, out_dtype, vb, grid, stream, tm);
+  else launch_d<128>(p, out_dtype, vb, grid, stream, tm);
   return check_launch("flw_fp8_swa_fwd");
 }
 
@@ -590,6 +653,18 @@ extern "C" int flw_fp8_swa_fwd_scale_strides(const uint8_t* q8, const int64_t* q
   return swa_fwd(q8, q_strides, k8, k_strides, v_tiles, q_scale, k_scale, v_scale, scale_stride_b,
                  scale_stride_h, out, out_dtype, out_strides, B, H, T, D, window,
                  static_cast<hipStream_t>(stream), take_timer());
+}
+
+extern "C" int flw_fp8_swa_fwd_bhtd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                                    const int64_t* k_strides, const uint8_t* v8, const int64_t* v_strides,
+                                    const float* q_scale, const float* k_scale, const float* v_scale,
+                                    int64_t scale_stride_b, int64_t scale_stride_h, void* out, int out_dtype,
+                                    const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                                    int64_t window, void* stream) {
+  FLW_REQUIRE(v_strides != nullptr, FLW_E_INVALID, "null v8 strides");
+  return swa_fwd(q8, q_strides, k8, k_strides, v8, q_scale, k_scale, v_scale, scale_stride_b, scale_stride_h,
+                 out, out_dtype, out_strides, B, H, T, D, window, static_cast<hipStream_t>(stream), take_timer(),
+                 nullptr, nullptr, nullptr, nullptr, nullptr, v_strides);
 }
 
 extern "C" int flw_fp8_swa_fwd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,

@@ -301,6 +301,10 @@ def _group_count(granularity: str, B: int, H: int) -> int:
     return {"tensor": 1, "head": H, "bh": B * H}[granularity]
 
 
+# Element strides (b, h) of each granularity's scale array: per tensor 0/0, per head 0/1, per (b, h) H/1.
+_SCALE_STRIDES = {"tensor": lambda H: (0, 0), "head": lambda H: (0, 1), "bh": lambda H: (H, 1)}
+
+
 def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: torch.Tensor,
                                  scales: torch.Tensor, window: int, *, granularity: str = "head",
                                  out_dtype: torch.dtype = torch.bfloat16,
@@ -308,8 +312,9 @@ def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: to
     """The attention kernel alone on pre-quantised operands (the ``_fp8_swa_fwd_kernel`` launch,
     fp8_swa_attention.py:249-258): q8 / k8 (B, H, T, D) e4m3 codes (uint8 or float8_e4m3fn, as
     ``_per_tensor_fp8`` returns them), V either in the kernel's tile layout (1-D, as
-    ``qk_norm_rope_quant_e4m3`` returns it) or as (B, H, T, D) codes (permuted into the tile layout
-    first, one pass), scales [3 * groups] (q, k, v) float32 on the device.
+    ``qk_norm_rope_quant_e4m3`` returns it) or as (B, H, T, D) codes (read as they are by
+    flw_fp8_swa_fwd_bhtd, the kernel instance that stages V into the tile layout itself), scales
+    [3 * groups] (q, k, v) float32 on the device.
     ``out``: optional (B, H, T, D) destination of ``out_dtype`` with D contiguous.
 
     The kernel is given only B, H, T, D and strides, so every operand's shape, dtype and size is
@@ -346,22 +351,23 @@ def fp8_swa_attention_from_codes(q8: torch.Tensor, k8: torch.Tensor, v_tiles: to
         raise ValueError(f"all operands must be on one device, got {sorted(map(str, devices))}")
     _lib.require_gpu(q8, k8, v_tiles, scales)
     q8, k8, v_tiles = (t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t for t in (q8, k8, v_tiles))
-    if v_tiles.dim() == 4:
-        v4 = v_tiles if v_tiles.stride(-1) == 1 and all(s % 16 == 0 for s in v_tiles.stride()[:3]) \
-            else v_tiles.contiguous()
-        v_tiles = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device=q8.device)
-        rc = lib.flw_vtile_from_bhtd(v4.data_ptr(), B, H, T, D, *v4.stride()[:3], v_tiles.data_ptr(),
-                                     _lib.stream_of(q8))
-        _lib.check(rc, "fp8_swa_attention_from_codes (V layout)")
     if out is None:
         out = torch.empty((B, H, T, D), dtype=out_dtype, device=q8.device)
     s8 = _lib.i64s(*q8.stride()[:3])
     sk = _lib.i64s(*k8.stride()[:3])
+    so = _lib.i64s(*out.stride()[:3])
     base = scales.data_ptr()
-    rc = lib.flw_fp8_swa_fwd(q8.data_ptr(), s8, k8.data_ptr(), sk, v_tiles.data_ptr(), base, base + 4 * G,
-                             base + 8 * G, _lib.GRANULARITY[granularity], out.data_ptr(),
-                             _lib.dtype_code(out.dtype), _lib.i64s(*out.stride()[:3]), B, H, T, D, int(window),
-                             _lib.stream_of(q8))
+    if v_tiles.dim() == 4:
+        v4 = v_tiles if v_tiles.stride(-1) == 1 and all(s % 16 == 0 for s in v_tiles.stride()[:3]) \
+            else v_tiles.contiguous()
+        ssb, ssh = _SCALE_STRIDES[granularity](H)
+        rc = lib.flw_fp8_swa_fwd_bhtd(q8.data_ptr(), s8, k8.data_ptr(), sk, v4.data_ptr(), _lib.i64s(*v4.stride()[:3]),
+                                      base, base + 4 * G, base + 8 * G, ssb, ssh, out.data_ptr(),
+                                      _lib.dtype_code(out.dtype), so, B, H, T, D, int(window), _lib.stream_of(q8))
+    else:
+        rc = lib.flw_fp8_swa_fwd(q8.data_ptr(), s8, k8.data_ptr(), sk, v_tiles.data_ptr(), base, base + 4 * G,
+                                 base + 8 * G, _lib.GRANULARITY[granularity], out.data_ptr(),
+                                 _lib.dtype_code(out.dtype), so, B, H, T, D, int(window), _lib.stream_of(q8))
     _lib.check(rc, "fp8_swa_attention_from_codes")
     return out
 

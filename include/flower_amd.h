@@ -197,7 +197,7 @@ int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, in
 /* FP8 causal sliding-window attention forward on pre-quantised operands, replacing the launch
  * of `_fp8_swa_fwd_kernel` (flower/kernels/fp8_swa_attention.py:249-258):
  *   q8, k8: (B, H, T, D) e4m3 with element strides q_strides[3] / k_strides[3] = {b, h, t};
- *   v_tiles: FLW_LAYOUT_VTILE e4m3 V (BHTD V codes: permute them with flw_vtile_from_bhtd);
+ *   v_tiles: FLW_LAYOUT_VTILE e4m3 V (BHTD V codes: flw_fp8_swa_fwd_bhtd reads them as they are);
  *   scales: 1, H or B*H floats each (granularity);
  *   out: (B, H, T, D) fp32 or bf16 with strides out_strides[3].
  * Query i attends to keys j with j <= i and i - j < window; window <= 0 gives zeros.
@@ -218,6 +218,19 @@ int flw_fp8_swa_fwd_scale_strides(const uint8_t* q8, const int64_t* q_strides, c
                                   int64_t scale_stride_h, void* out, int out_dtype,
                                   const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
                                   int64_t window, void* stream);
+
+/* The launch of `_fp8_swa_fwd_kernel` (flower/kernels/fp8_swa_attention.py:249-258) with every
+ * operand as the reference passes it: q8, k8, v8 (B, H, T, D) e4m3 codes as `_per_tensor_fp8`
+ * returns them (:242-244), with byte strides {b, h, t} (multiples of 16, D contiguous), and the
+ * scales indexed by element strides as in flw_fp8_swa_fwd_scale_strides. V is read in that layout
+ * (no separate permutation pass): the kernel stages each V tile into the layout its MFMA operand
+ * reads, so the output is flw_fp8_swa_fwd's on flw_vtile_from_bhtd(v8), bit for bit. */
+int flw_fp8_swa_fwd_bhtd(const uint8_t* q8, const int64_t* q_strides, const uint8_t* k8,
+                         const int64_t* k_strides, const uint8_t* v8, const int64_t* v_strides,
+                         const float* q_scale, const float* k_scale, const float* v_scale,
+                         int64_t scale_stride_b, int64_t scale_stride_h, void* out, int out_dtype,
+                         const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                         int64_t window, void* stream);
 
 /* flw_fp8_swa_fwd with Q in its input dtype, quantised on load by the attention kernel (the
  * `_per_tensor_fp8(q)` of flower/kernels/fp8_swa_attention.py:242 moved into the kernel's

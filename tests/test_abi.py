@@ -81,6 +81,12 @@ def test_host_only_calls_work_without_a_gpu():
     s = _lib.i64s(0, 0, 0)
     rc = lib.flw_fp8_swa_fwd(16, s, 16, s, 16, 16, 16, 16, 0, 16, 1, s, 1, 1, 64, 96, 16, None)
     assert rc == 2 and b"head_dim" in lib.flw_last_error()
+    # V as (B, H, T, D) codes: strides checked before launch (multiples of 16 bytes)
+    s16, s8 = _lib.i64s(64 * 64, 64 * 64, 64), _lib.i64s(64 * 64, 64 * 64, 72)
+    rc = lib.flw_fp8_swa_fwd_bhtd(16, s16, 16, s16, 16, None, 16, 16, 16, 0, 1, 16, 1, s16, 1, 1, 64, 64, 16, None)
+    assert rc == 1 and b"null v8 strides" in lib.flw_last_error()
+    rc = lib.flw_fp8_swa_fwd_bhtd(16, s16, 16, s16, 16, s8, 16, 16, 16, 0, 1, 16, 1, s16, 1, 1, 64, 64, 16, None)
+    assert rc == 1 and b"v8 strides" in lib.flw_last_error()
     rc = lib.flw_fp8_linear(16, 8, 64, 64, 16, 16, 16, 16, 7, 16, 16, 16, 1 << 20, None)
     assert rc == 1 and b"unknown GEMM mode" in lib.flw_last_error()
     rc = lib.flw_fp8_linear(16, 8, 80, 80, 16, 16, 16, 16, 1, 16, 16, None, 0, None)   # W8A16

@@ -501,6 +501,44 @@ def test_attention_from_bhtd_codes(D, T):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("D,T,gran", [(64, 300, "head"), (32, 64, "tensor"), (128, 130, "bh"), (64, 8192, "bh")])
+def test_bhtd_v_entry_is_bit_identical_to_the_tiled_v_entry(D, T, gran):
+    """flw_fp8_swa_fwd_bhtd (V as (B, H, T, D) codes, staged into the tile layout by the kernel)
+    against flw_fp8_swa_fwd on flw_vtile_from_bhtd of the same codes: bit for bit, with V read
+    through the model's (B, T, H, D) layout as a strided view (rows past T are the padding keys),
+    the scales through the granularity's element strides, bf16 and fp32 outputs."""
+    from flower_amd import _lib as L
+    from flower_amd.kernels.fp8_swa_attention import _per_tensor_fp8
+    lib = L.load()
+    B, H, W = 2, 3, 77 if T < 8192 else 1024
+    q, k = (seeded((B, H, T, D), s, torch.bfloat16) for s in (91, 92))
+    v = seeded((B, H, T, D), 93, torch.bfloat16)
+    (q8, qs), (k8, ks), (v8c, vs) = (_per_tensor_fp8(t, gran) for t in (q, k, v))
+    q8, k8 = q8.view(torch.uint8), k8.view(torch.uint8)
+    vbuf = torch.empty((B, T, H, D), dtype=torch.uint8, device="cuda")    # the model's layout
+    vbuf.copy_(v8c.view(torch.uint8).transpose(1, 2))
+    v8 = vbuf.transpose(1, 2)                                   # (B, H, T, D) view, strides (THD, D, HD)
+    assert not v8.is_contiguous() and v8.stride()[:3] == (T * H * D, D, H * D)
+    vt = torch.empty(lib.flw_vtile_bytes(B, H, T, D), dtype=torch.uint8, device="cuda")
+    L.check(lib.flw_vtile_from_bhtd(v8.data_ptr(), B, H, T, D, *v8.stride()[:3], vt.data_ptr(), L.stream_of(v8)),
+            "permute")
+    ssb, ssh = {"tensor": (0, 0), "head": (0, 1), "bh": (H, 1)}[gran]
+    s8, sk, sv = (L.i64s(*t.stride()[:3]) for t in (q8, k8, v8))
+    for dt in (torch.bfloat16, torch.float32):
+        want = torch.empty((B, H, T, D), dtype=dt, device="cuda")
+        got = torch.full_like(want, float("nan"))
+        so = L.i64s(*want.stride()[:3])
+        L.check(lib.flw_fp8_swa_fwd_scale_strides(q8.data_ptr(), s8, k8.data_ptr(), sk, vt.data_ptr(), qs.data_ptr(),
+                                                  ks.data_ptr(), vs.data_ptr(), ssb, ssh, want.data_ptr(),
+                                                  L.dtype_code(dt), so, B, H, T, D, W, L.stream_of(q8)), "tiled")
+        L.check(lib.flw_fp8_swa_fwd_bhtd(q8.data_ptr(), s8, k8.data_ptr(), sk, v8.data_ptr(), sv, qs.data_ptr(),
+                                         ks.data_ptr(), vs.data_ptr(), ssb, ssh, got.data_ptr(), L.dtype_code(dt), so,
+                                         B, H, T, D, W, L.stream_of(q8)), "bhtd")
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16 if dt == torch.bfloat16 else torch.int32),
+                           want.view(torch.int16 if dt == torch.bfloat16 else torch.int32)), (D, T, gran, dt)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_small_and_large_grid_kernels_agree_bit_for_bit(dtype):
     """A slice's output does not depend on the grid it runs in (dispatch order, XCD grouping, the
