@@ -591,20 +591,25 @@ __global__ __launch_bounds__(kThreads) void cols_quant_t_kernel(const T* __restr
 // is written too when h_out is given.
 constexpr int kActRmsnorm = 0, kActGelu = 1, kActNone = 2;   // kActNone: h = x (flw_quant_rows_e4m3)
 
-// erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7): erf(|x|) = 1 - poly(t) exp(-x^2),
-// t = 1 / (1 + p |x|); two transcendental and six fused multiply-adds instead of the device
-// library's full-precision erff. In GELU, (0.5 x)(1 + erf(x / sqrt 2)), that error is far below
-// the bf16 rounding of the result.
-__device__ __forceinline__ float erf_as(float x) {
+// GELU with erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7): erf(|z|) = 1 - q(t) exp(-z^2),
+// t = 1 / (1 + p |z|); two transcendental and six fused multiply-adds instead of the device
+// library's full-precision erff, an error far below the bf16 rounding of the result. With
+// z = x / sqrt 2 folded into the constants (p / sqrt 2, exp2(x * (x * -log2(e) / 2))) and
+// u = 1 - q e = erf(|z|):
+//   (0.5 x) (1 + erf(z)) = x * RN(0.5 +- 0.5 u)  (+ for x >= 0, - below; the same roundings as
+//   RN(0.5 x) * RN(1 +- u), since scaling by 0.5 is exact), so 1 + erf still cancels to 0 for
+//   very negative x, as the reference's fp32 evaluation does.
+__device__ __forceinline__ float gelu_as(float x) {
   const float a = __builtin_fabsf(x);
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, a, 1.0f));
   float q = fmaf(1.061405429f, t, -1.453152027f);
   q = fmaf(q, t, 1.421413741f);
   q = fmaf(q, t, -0.284496736f);
   q = fmaf(q, t, 0.254829592f);
   q *= t;
-  const float e = __builtin_amdgcn_exp2f(-a * a * 1.4426950408889634f);
-  return __builtin_copysignf(fmaf(-q, e, 1.0f), x);
+  const float e = __builtin_amdgcn_exp2f(x * (x * (-0.5f * 1.4426950408889634f)));
+  const float u = fmaf(-q, e, 1.0f);
+  return x * fmaf(__builtin_copysignf(0.5f, x), u, 0.5f);
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
@@ -667,7 +672,7 @@ __global__ __launch_bounds__(kThreads) void rows_act_quant_kernel(
       float f[8];
       unpack(hb[i], f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = (0.5f * f[e]) * (1.0f + erf_as(f[e] * 0.70710678118654752f));
+      for (int e = 0; e < 8; ++e) f[e] = gelu_as(f[e]);
       hb[i] = pack(f);
       __builtin_amdgcn_sched_barrier(0);        // one vector's erf at a time: bounded registers
     }
