@@ -318,6 +318,34 @@ __device__ __forceinline__ void head_norm_rope(float* f, bool norm, float eps, i
 // LDS pointer type: the 32-bit LDS address of a __shared__ object is (uint32_t)(lds_u8_t*)p.
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
+// A 64-key x D tile of e4m3 codes (D = 32, 64, 128) staged in LDS as rows: row r (key r) at r D,
+// its 16-byte chunk c at position c ^ vrow_swizzle(r, D). The swizzle keeps both accesses free of
+// bank conflicts: writes of consecutive chunks of consecutive rows, and the transposed reads of
+// vtile_run (a 16-lane group reads one 16-byte chunk of the 8 rows r0 + {0-3, 8-11}: row bits 3 and,
+// at D = 128, 1 pick the chunk).
+__device__ __forceinline__ int vrow_swizzle(int r, int D) {
+  return D == 128 ? (((r >> 1) & 1) | (((r >> 3) & 1) << 1)) : ((r >> 3) & 1);
+}
+__device__ __forceinline__ int vrow_offset(int r, int c16, int D) { return r * D + 16 * (c16 ^ vrow_swizzle(r, D)); }
+
+// One 16-byte run of the tiled-V layout (FLW_LAYOUT_VTILE: dim d, key block kb of 32 keys, half
+// hb; byte 4 a + c = key 32 kb + 8 a + 4 hb + c) read from a row-staged tile, for lane n of a
+// 16-lane group whose lanes take dims d0 .. d0 + 15 (d0 a multiple of 16) with the same kb, hb.
+// ds_read_b64_tr_b8 works on groups of 16 lanes (measured lane layout): lane 2 j + a supplies the
+// address of 8 consecutive bytes (row j, columns 8 a .. 8 a + 7 of the group's 16) and lane n
+// receives column n of the 8 rows, byte j from row j. Two reads (rows 32 kb + 4 hb + {0-3, 8-11}
+// and the same + 16) give the run. Every lane of the group must call this together.
+__device__ __forceinline__ uint4 vtile_run(const uint8_t* tile, int D, int d0, int kb, int hb, int n) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  const int j = n >> 1, a = n & 1;
+  const int r0 = 32 * kb + 4 * hb + (j < 4 ? j : j + 4);      // r0 + 16 has the same swizzle
+  const uint8_t* src = tile + vrow_offset(r0, d0 >> 4, D) + 8 * a;
+  const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(lds_u8_t*)src);
+  const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(lds_u8_t*)(src + 16 * D));
+  return make_uint4((uint32_t)lo.x, (uint32_t)lo.y, (uint32_t)hi.x, (uint32_t)hi.y);
+}
+
 // s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
 // (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt / lgkmcnt left free).
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }

@@ -183,14 +183,6 @@ __device__ __forceinline__ float clamp448(float y) {
 }
 
 
-// Byte offset of element (key kk, dim d) inside a 64 x D VTILE tile.
-__device__ __forceinline__ uint32_t vtile_offset(uint32_t kk, uint32_t d) {
-  const uint32_t r = kk & 31u;
-  const uint32_t h = (r >> 2) & 1u;
-  const uint32_t b = ((r >> 3) << 2) | (r & 3u);
-  return (d >> 5) * 2048u + (kk >> 5) * 1024u + ((d & 31u) + 32u * h) * 16u + b;
-}
-
 // e4m3 codes of N values, packed little-endian (N = 4 or 8), on the fast or the exact path.
 template <int N>
 __device__ __forceinline__ void codes_of(const float* f, float s, float r, bool fast, uint32_t* w) {
@@ -320,12 +312,12 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
           if (V::N == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
           else *reinterpret_cast<uint32_t*>(dst) = w[0];
         } else {
-          const uint32_t lrow = (uint32_t)(v / vpr), d = (uint32_t)((v % vpr) * V::N);
-          uint8_t* tl = tile_lds + (lrow >> 6) * (64u * (uint32_t)p.d3);
+          // the chunk's rows staged as they are (vrow_offset), re-read in the tile order below
+          const int lrow = (int)(v / vpr), d = (int)((v % vpr) * V::N), D = (int)p.d3;
+          uint8_t* dst = tile_lds + (lrow >> 6) * 64 * D + vrow_offset(lrow & 63, d >> 4, D) + (d & 15);
           const bool pad = v >= nvec;
-#pragma unroll
-          for (int i = 0; i < V::N; ++i)
-            tl[vtile_offset(lrow & 63u, d + i)] = pad ? 0 : (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+          if (V::N == 8) *reinterpret_cast<uint2*>(dst) = pad ? make_uint2(0, 0) : make_uint2(w[0], w[1]);
+          else *reinterpret_cast<uint32_t*>(dst) = pad ? 0u : w[0];
         }
       } else {
         // out = x + (dq - x), each step rounded to T (base.py:200-203)
@@ -355,12 +347,21 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantParams p) {
     }
   }
   if (vtile) {
+    // Each 16-byte run of the tiled layout (run index i of a tile: dim 32 (i / 128) + i % 32, key
+    // block (i / 64) % 2, half (i / 32) % 2) gathered from the staged rows by transposed reads; 16
+    // consecutive runs per 16-lane group, stored contiguously. The chunk holds whole tiles of 4 D
+    // runs each (a multiple of 128), so every 16-lane group is whole.
     __syncthreads();
+    const int D = (int)p.d3;
     const int64_t ntiles = (p.d2 + 63) >> 6;
-    const int64_t nbytes = (r1p - r0) * p.d3;
+    const int nruns = (int)((r1p - r0) * D / 16), tile_runs = 4 * D;
     uint8_t* dst = t.out8 + (slice * ntiles + (r0 >> 6)) * 64 * p.d3;
-    for (int64_t o = threadIdx.x * 16; o < nbytes; o += kThreads * 16)
-      *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(tile_lds + o);
+    for (int i = threadIdx.x; i < nruns; i += kThreads) {
+      const int tl = i / tile_runs, ir = i % tile_runs;
+      const uint4 run = vtile_run(tile_lds + tl * 64 * D, D, 32 * (ir >> 7) + (ir & 16), (ir >> 6) & 1,
+                                  (ir >> 5) & 1, ir & 15);
+      *reinterpret_cast<uint4*>(dst + 16 * (int64_t)i) = run;
+    }
   }
 }
 

@@ -111,38 +111,14 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* lds, int off) {
   return r;
 }
 
-// A V tile staged as (B, H, T, D) rows: 64 rows of D bytes, 16-byte chunk c of row r at c ^ vswz(r).
-// The swizzle keeps both accesses free of bank conflicts: the staging writes (16 lanes = 16
-// consecutive chunks of consecutive rows) and the transposed reads below (a 16-lane group reads
-// one 16-byte chunk of 8 rows r0 + {0-3, 8-11}: the row bits 3 and, at D = 128, 1 pick the chunk).
-template <int D>
-__device__ __forceinline__ int vswz(int r) {
-  if (D == 128) return ((r >> 1) & 1) | (((r >> 3) & 1) << 1);
-  return (r >> 3) & 1;
-}
-
-// The PV operand fragment of dims 32 db .. 32 db + 31 from a staged (B, H, T, D) V tile, byte for
-// byte the tiled V's fragment (load_frag): lane (d = lane % 32, h = lane / 32) holds keys
-// 32 kb + 8 a + 4 h + c in byte 16 kb + 4 a + c. ds_read_b64_tr_b8 works on groups of 16 lanes: lane
-// 2 j + a of a group supplies the address of 8 consecutive bytes (row j, columns 8 a .. 8 a + 7 of
-// the group's 16) and lane n receives column n of the 8 rows, byte j from row j. Four reads give
-// the 32 keys: read t covers rows 16 (t % 2) + 32 (t / 2) + 4 h + {0-3, 8-11}.
+// The PV operand fragment of dims 32 db .. 32 db + 31 from a row-staged V tile (vrow_offset),
+// byte for byte the tiled V's fragment (load_frag): lane (d = lane % 32, h = lane / 32) holds the
+// runs of key blocks 0 and 1 for its dim (vtile_run).
 template <int D>
 __device__ __forceinline__ v8i vtr_frag(const uint8_t* lds, int db, int lane) {
-  typedef int v2i __attribute__((ext_vector_type(2)));
-  typedef __attribute__((address_space(3))) v2i lds_v2i;
-  const int s = lane & 15, j = s >> 1, a = s & 1, g1 = (lane >> 4) & 1, h = lane >> 5;
-  const int r0 = 4 * h + (j < 4 ? j : j + 4);
-  const int off = r0 * D + 16 * ((2 * db + g1) ^ vswz<D>(r0)) + 8 * a;
-  v8i out;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const v2i w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-        (lds_v2i*)(lds_u8_t*)(lds + off + (16 * (t & 1) + 32 * (t >> 1)) * D));
-    out[2 * t] = w.x;
-    out[2 * t + 1] = w.y;
-  }
-  return out;
+  const int n = lane & 15, d0 = 32 * db + 16 * ((lane >> 4) & 1), h = lane >> 5;
+  const uint4 a = vtile_run(lds, D, d0, 0, h, n), b = vtile_run(lds, D, d0, 1, h, n);
+  return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
 
 // A K fragment (32 keys x 64 bytes for this lane) from its swizzled region (offsets from the lane).
@@ -180,7 +156,7 @@ struct Scores {
 // At D <= 64 the kernel takes 120 VGPRs (D = 32: 110), so four workgroups (16 waves) share a CU;
 // the launch bound only asks for three. D = 128 asks for two (its O^T needs 64 VGPRs more).
 // VB: V arrives as (B, H, T, D) e4m3 codes (the reference's layout, strides vsb / vsh / vst). Its
-// tiles are staged as they are (64 key rows of D bytes, 16-byte chunk c of row r at c ^ vswz(r))
+// tiles are staged as they are (64 key rows of D bytes, swizzled as vrow_offset places them)
 // and the PV operand is read with ds_read_b64_tr_b8, which hands each lane one dim of 8 key rows:
 // the same bytes in the same order as the tiled V's fragment reads, so the results are those of
 // the tiled-V instance.
@@ -312,7 +288,7 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void swa_fwd_kernel(SwaParam
     koff[j] = (uint32_t)(kk * p.kst + 16 * g);
     if constexpr (VB) {
       voff[j] = (uint32_t)(kk * p.vst + 16 * g);
-      ldsv[j] = (uint32_t)(kk * D + 16 * (g ^ vswz<D>(kk)));
+      ldsv[j] = (uint32_t)vrow_offset(kk, g, D);
     }
     // Chunk (krow + 32 h2) of fragment region (blk, dc, cc), its index XORed with 4 (h2 + 2 cc):
     // the 16 lanes of a ds_write_b128 phase (4 rows x 4 chunks) then fall in 16 distinct bank
