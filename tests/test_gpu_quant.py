@@ -218,7 +218,9 @@ def test_nan_input_gives_nan_scale_and_codes_like_the_reference():
 
 
 @pytest.mark.parametrize("shape,dtype", [((2, 3, 100, 64), torch.bfloat16), ((1, 2, 64, 32), torch.float32),
-                                         ((1, 1, 257, 128), torch.bfloat16)])
+                                         ((1, 1, 257, 128), torch.bfloat16), ((1, 2, 1, 64), torch.bfloat16),
+                                         ((2, 1, 129, 32), torch.bfloat16), ((1, 1, 200, 128), torch.float32),
+                                         ((1, 3, 63, 64), torch.float32)])
 def test_vtile_layout_is_the_documented_permutation(shape, dtype):
     L = lib()
     lb = L.load()
