@@ -11,14 +11,16 @@ Layout and parameter names follow flower/models/base.py:
                               configs/sweep13_450m_longctx_fp8.yaml:109) -> RoPE of q, k
                               (base.py:634, always, base ``rope_base``) -> e4m3 (the quantisation
                               point, base.py:636-637) -> FP8 SWA -> ``out`` Linear(d, d);
-                              forward-only like the FP8 kernel (fp8_swa_attention.py:71-76)
+                              differentiable through fp8_swa_attention when gradients are needed
+                              (the block's own fused ``forward`` runs without them)
   ``Fp8FeedForward``          base.py:514-525 GELU layout (``net.0`` Linear(d, ffn), GELU,
                               ``net.3`` Linear(ffn, d); dropout is identity in eval)
   ``Fp8DecoderBlock``         base.py:698-722: x + attn(ln1(x)), then + ff(ln2(x))
 
 ``forward`` runs the fused path on bf16 GPU inputs (RMSNorm and GELU fused with the next
-linear's per-row e4m3 quantisation, QK-norm + RoPE fused with the Q / K / V quantiser, residual
-adds in the GEMM epilogues, the attention writing its (B, T, H, D) output in place: library kernels
+linear's per-row e4m3 quantisation, QK-norm + RoPE and the per-head maxima in the QKV GEMM's
+epilogue (or, with ``fuse_qk_epilogue = False``, in the Q / K / V quantiser), residual adds in the
+GEMM epilogues, the attention writing its (B, T, H, D) output in place: library kernels
 only, no torch elementwise kernels);
 ``forward_unfused`` is the module-by-module composition (torch norms / GELU / adds around the
 library's linears and attention). Wrap calls in ``fp8_weight_cache(block)`` to quantise the
