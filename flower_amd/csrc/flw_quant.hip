@@ -1180,55 +1180,73 @@ extern "C" int flw_vtile_from_bhtd(const uint8_t* codes, int64_t B, int64_t H, i
 //
 // The dequantised tensor a straight-through FP8 path differentiates at: out[b, h, t, d] =
 // e4m3(code) * scale of its group, rounded to the output dtype (bf16: nearest even). Codes in
-// (B, H, T, D) rows or in the attention kernel's V tile layout; out contiguous (B, H, T, D). One
-// thread per 8 consecutive d of one row.
+// (B, H, T, D) rows or in the attention kernel's V tile layout; out contiguous (B, H, T, D). The
+// codes are converted by v_cvt_pk_f32_fp8 (exact: every e4m3 value is an fp32 value).
 namespace flw {
 
+// Eight values e4m3(code) * scale to OutT (bf16: round to nearest even, NaN as 0x7FC0).
 template <typename OutT>
-__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ codes, int layout, int64_t H,
-                                                      int64_t T, int D, const float* __restrict__ scales,
-                                                      int64_t ssb, int64_t ssh, OutT* __restrict__ out,
-                                                      int64_t n8) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n8) return;
-  const int per_row = D / 8;
-  const int64_t row = i / per_row;                 // (b * H + h) * T + t
-  const int d0 = (int)(i % per_row) * 8;
-  const int64_t t = row % T, bh = row / T;
-  const int64_t b = bh / H, h = bh % H;
-  const float s = scales[b * ssb + h * ssh];
-  uint32_t c[8];
-  if (layout == FLW_LAYOUT_BHTD) {
-    const uint2 w = *reinterpret_cast<const uint2*>(codes + row * D + d0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { c[e] = (w.x >> (8 * e)) & 0xFFu; c[4 + e] = (w.y >> (8 * e)) & 0xFFu; }
-  } else {
-    // tile layout: element (key kk, dim d) of a 64-key tile at (d / 32) 2048 + (kk / 32) 1024 +
-    // ((d % 32) + 32 hb) 16 + bb, hb = (r / 4) % 2, bb = 4 (r / 8) + r % 4, r = kk % 32
-    const int64_t slice = ((T + 63) / 64) * 64 * D;
-    const int kk = (int)(t % 64), r = kk % 32;
-    const uint8_t* tile = codes + bh * slice + (t / 64) * 64 * D;
-    const int hb = (r / 4) % 2, bb = 4 * (r / 8) + r % 4;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = d0 + e;
-      c[e] = tile[(d / 32) * 2048 + (kk / 32) * 1024 + ((d % 32) + 32 * hb) * 16 + bb];
-    }
-  }
+__device__ __forceinline__ void dequant8_store(uint32_t w0, uint32_t w1, float sc, OutT* dst) {
   float v[8];
+  const uint32_t w[2] = {w0, w1};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = e4m3_to_f32(c[e]) * s;
+  for (int i = 0; i < 2; ++i) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);     // bytes 0, 1
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);      // bytes 2, 3
+    v[4 * i] = lo[0] * sc; v[4 * i + 1] = lo[1] * sc; v[4 * i + 2] = hi[0] * sc; v[4 * i + 3] = hi[1] * sc;
+  }
   if constexpr (sizeof(OutT) == 2) {
-    uint4 o;
-    o.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-    o.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-    o.z = f32_to_bf16_bits(v[4]) | (f32_to_bf16_bits(v[5]) << 16);
-    o.w = f32_to_bf16_bits(v[6]) | (f32_to_bf16_bits(v[7]) << 16);
-    *reinterpret_cast<uint4*>(out + row * D + d0) = o;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(bf16x2_rne(v[0], v[1]), bf16x2_rne(v[2], v[3]),
+                                                bf16x2_rne(v[4], v[5]), bf16x2_rne(v[6], v[7]));
   } else {
-    float4* o = reinterpret_cast<float4*>(out + row * D + d0);
+    float4* o = reinterpret_cast<float4*>(dst);
     o[0] = make_float4(v[0], v[1], v[2], v[3]);
     o[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// (B, H, T, D) codes: one thread per 8 consecutive values (n8 < 2^31).
+template <typename OutT>
+__global__ __launch_bounds__(256) void dequant_bhtd_kernel(const uint8_t* __restrict__ codes, int H, int T, int D,
+                                                           const float* __restrict__ scales, int ssb, int ssh,
+                                                           OutT* __restrict__ out, int n8) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const int per_row = D >> 3;
+  const int row = i / per_row, bh = row / T;
+  const float sc = scales[(bh / H) * ssb + (bh % H) * ssh];
+  const uint2 w = *reinterpret_cast<const uint2*>(codes + (int64_t)i * 8);
+  dequant8_store<OutT>(w.x, w.y, sc, out + (int64_t)i * 8);
+}
+
+// The attention's V tile layout: one workgroup per 64-key tile of a (b, h) slice. The tile is
+// copied to LDS as it is (runs of 16 keys, run rho = 128 (d / 32) + 64 kb + 32 hb + d % 32 for dim
+// d, key block kb, half hb; byte 4 a + c of a run = key 32 kb + 8 a + 4 hb + c), then each 16-lane
+// group transposes 8 consecutive runs (dims d0 .. d0 + 7) with ds_read_b64_tr_b8 -- lane 2 j + a
+// supplies the address of bytes 8 a .. 8 a + 7 of run j, lane n receives byte n of the 8 runs -- so
+// lane n holds dims d0 .. d0 + 7 of key 32 kb + 8 (n / 4) + 4 hb + n % 4, stored as one row piece.
+template <typename OutT>
+__global__ __launch_bounds__(256) void dequant_vtile_kernel(const uint8_t* __restrict__ codes, int H, int T, int D,
+                                                            const float* __restrict__ scales, int ssb, int ssh,
+                                                            OutT* __restrict__ out) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  __shared__ __align__(16) uint8_t lt[64 * 128];
+  const int ntiles = (T + 63) >> 6;
+  const int bh = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
+  const float sc = scales[(bh / H) * ssb + (bh % H) * ssh];
+  const uint8_t* src = codes + ((int64_t)bh * ntiles + tile) * 64 * D;
+  for (int i = threadIdx.x; i < 4 * D; i += 256)
+    *reinterpret_cast<uint4*>(lt + 16 * i) = *reinterpret_cast<const uint4*>(src + 16 * i);
+  __syncthreads();
+  const int lane16 = threadIdx.x & 15, j = lane16 >> 1, a = lane16 & 1;
+  const int octs = D >> 3;                      // 8-dim groups per (kb, hb)
+  for (int g = threadIdx.x >> 4; g < 4 * octs; g += 16) {   // uniform per 16-lane group
+    const int d0 = 8 * (g % octs), hb = (g / octs) & 1, kb = g / (2 * octs);
+    const int rho0 = 128 * (d0 >> 5) + 64 * kb + 32 * hb + (d0 & 31);
+    const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(lds_u8_t*)(lt + 16 * (rho0 + j) + 8 * a));
+    const int t = 64 * tile + 32 * kb + 8 * (lane16 >> 2) + 4 * hb + (lane16 & 3);
+    if (t < T) dequant8_store<OutT>((uint32_t)r.x, (uint32_t)r.y, sc, out + ((int64_t)bh * T + t) * D + d0);
   }
 }
 
@@ -1247,16 +1265,29 @@ extern "C" int flw_dequant_e4m3(const uint8_t* codes, int layout, int64_t B, int
   FLW_REQUIRE(((uintptr_t)codes & 7) == 0 && ((uintptr_t)out & 15) == 0, FLW_E_INVALID,
               "codes must be 8-byte, out 16-byte aligned");
   const int64_t n8 = B * H * T * D / 8;
-  FLW_REQUIRE((n8 + 255) / 256 <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "tensor too large");
-  const int64_t ssb = granularity == FLW_SCALE_BH ? H : 0, ssh = granularity == FLW_SCALE_TENSOR ? 0 : 1;
-  const dim3 grid((unsigned)((n8 + 255) / 256));
+  FLW_REQUIRE(n8 < ((int64_t)1 << 31) - 256 && B * H * ((T + 63) / 64) <= 0x7FFFFFFF, FLW_E_UNSUPPORTED,
+              "tensor too large");
+  const int ssb = granularity == FLW_SCALE_BH ? (int)H : 0, ssh = granularity == FLW_SCALE_TENSOR ? 0 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (out_dtype == FLW_BF16)
-    hipLaunchKernelGGL(dequant_kernel<uint16_t>, grid, dim3(256), 0, s, codes, layout, H, T, (int)D, scales, ssb,
-                       ssh, static_cast<uint16_t*>(out), n8);
-  else
-    hipLaunchKernelGGL(dequant_kernel<float>, grid, dim3(256), 0, s, codes, layout, H, T, (int)D, scales, ssb,
-                       ssh, static_cast<float*>(out), n8);
+  const bool bf = out_dtype == FLW_BF16;
+  if (layout == FLW_LAYOUT_BHTD) {
+    const dim3 grid((unsigned)((n8 + 255) / 256));
+    if (bf)
+      hipLaunchKernelGGL(dequant_bhtd_kernel<uint16_t>, grid, dim3(256), 0, s, codes, (int)H, (int)T, (int)D, scales,
+                         ssb, ssh, static_cast<uint16_t*>(out), (int)n8);
+    else
+      hipLaunchKernelGGL(dequant_bhtd_kernel<float>, grid, dim3(256), 0, s, codes, (int)H, (int)T, (int)D, scales,
+                         ssb, ssh, static_cast<float*>(out), (int)n8);
+  } else {
+    FLW_REQUIRE(((uintptr_t)codes & 15) == 0, FLW_E_INVALID, "tile-layout codes must be 16-byte aligned");
+    const dim3 grid((unsigned)(B * H * ((T + 63) / 64)));
+    if (bf)
+      hipLaunchKernelGGL(dequant_vtile_kernel<uint16_t>, grid, dim3(256), 0, s, codes, (int)H, (int)T, (int)D, scales,
+                         ssb, ssh, static_cast<uint16_t*>(out));
+    else
+      hipLaunchKernelGGL(dequant_vtile_kernel<float>, grid, dim3(256), 0, s, codes, (int)H, (int)T, (int)D, scales,
+                         ssb, ssh, static_cast<float*>(out));
+  }
   return check_launch("flw_dequant_e4m3");
 }
 

@@ -260,7 +260,7 @@ int flw_fp8_swa_fwd_lse(const uint8_t* q8, const int64_t* q_strides, const uint8
                         int64_t D, int64_t window, float* lse, void* stream);
 
 /* The dequantised values of e4m3 codes: out[b, h, t, d] = e4m3(code) * scale of (b, h)'s group
- * (granularity as above), rounded to out_dtype (FLW_BF16: nearest even; FLW_F32: exact). Codes in
+ * (granularity as above) as an fp32 product, rounded to out_dtype (FLW_BF16: nearest even). Codes in
  * FLW_LAYOUT_BHTD (contiguous) or FLW_LAYOUT_VTILE; out contiguous (B, H, T, D), 16-byte aligned.
  * The tensors the straight-through estimator of `_fake_quant_e4m3` (flower/models/base.py:167-203)
  * differentiates at: the backward of the FP8 attention runs on them. */
