@@ -100,7 +100,7 @@ DATA = {
 # 131,088 KiB of FETCH_SIZE against 262,144 KiB of WRITE_SIZE (scale 1.0). The attention kernel
 # reads Q in bf16 (quantised on load); "quant" is the deferred-Q quantise pair.
 TRAFFIC = {
-    "c3": {"swa_fwd": 209_382_656, "quant": 403_708_672},
+    "c3": {"swa_fwd": 209_343_898, "quant": 403_801_190},
     "c4": {"swa_fwd": 209_952_154, "quant": 403_344_998},
     "c2": {"gemm": 117_834_752, "w8a16": 134_490_112},
     "swa_bf16_450m": {"bwd": 554_757_120, "fwd": 169_459_712},
