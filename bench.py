@@ -1,6 +1,6 @@
 """Benchmark of the FP8 sliding-window-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|c2_train|swa_bf16|swa_bf16_450m|fp8_train_450m]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|c2_train|ref_fp8|swa_bf16|swa_bf16_450m|fp8_train_450m]
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
