@@ -28,6 +28,9 @@
 
 #include "flw_common.h"
 
+// m0 is clobbered by the direct-to-LDS tile loads (TileLoadLds); nothing else here uses it.
+#pragma clang diagnostic ignored "-Winline-asm"
+
 namespace flw {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -80,35 +83,39 @@ __device__ __forceinline__ int nat_off(int r, int c) {
   return r * 256 + 16 * (c ^ (((r & 3) << 2) | ((r >> 2) & 3)));
 }
 
-// Global -> registers for one 64-row tile of a (T, D) bf16 slice: 64 * D / 8 chunks of 16 bytes
-// over 256 threads (a whole number of chunks per thread for D = 32 / 64 / 128), through a buffer
-// descriptor covering the slice's T rows, so rows past T read as zero with no compare. The row
-// offset goes into the VGPR offset, which the descriptor's range check covers.
+// Buffer descriptors cover a slice's T rows, so rows past T read as zero with no compare; row
+// offsets go into the VGPR offset, which the descriptor's range check covers.
 constexpr int kBufferFlags = 0x00020000;   // buffer descriptor word 3 for raw dword access (gfx9)
 
+// Global -> LDS for one 64-row tile of a (T, D) bf16 slice, straight into the natural swizzled
+// layout (buffer_load_dwordx4 ... lds: each lane's 16 bytes land at M0 + 16 lane, no VGPR round
+// trip, so a kernel holds no prefetch registers): wave w fills rows RPI (NI w + t) .. + RPI - 1
+// with instruction t, the lane at LDS slot p of row r loading the global chunk that nat_off puts
+// at slot p (the swizzle is an XOR, its own inverse). Rows past T read as zero through the
+// descriptor's range check. Issued from inline assembly, so the compiler does not wait for these
+// loads before every LDS read; callers wait (vmcnt) before the barrier that publishes a tile.
 template <int D>
-struct TileLoad {
+struct TileLoadLds {
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int CPT = 64 * CPR / 256;        // chunks per thread
-  static_assert(CPT * 256 == 64 * CPR, "whole chunks per thread");
+  static constexpr int RPI = 64 / CPR;              // rows per wave instruction
+  static constexpr int NI = 64 / RPI / 4;           // instructions per wave per tile
   __amdgpu_buffer_rsrc_t rs;
-  uint4 r[CPT];
-  __device__ __forceinline__ void init(const uint16_t* base, int T) {
+  uint32_t off[NI];
+  __device__ __forceinline__ void init(const uint16_t* base, int T, int wave, int lane) {
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, T * D * 2, kBufferFlags);
-  }
-  __device__ __forceinline__ void load(int row0, int tid) {
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int i = tid + 256 * j;
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (row0 + i / CPR) * (2 * D) + 16 * (i % CPR), 0, 0);
-      r[j] = make_uint4(v[0], v[1], v[2], v[3]);
+    for (int t = 0; t < NI; ++t) {
+      const int r = RPI * (NI * wave + t) + lane / CPR, slot = lane % CPR;
+      const int c = (nat_off<D>(r, slot) - r * 2 * D) / 16;
+      off[t] = (uint32_t)(r * 2 * D + 16 * c);
     }
   }
-  __device__ __forceinline__ void store_nat(uint8_t* lds, int tid) const {
+  __device__ __forceinline__ void load(uint8_t* lds, int row0, int wave) const {
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int i = tid + 256 * j;
-      *reinterpret_cast<uint4*>(lds + nat_off<D>(i / CPR, i % CPR)) = r[j];
+    for (int t = 0; t < NI; ++t) {
+      const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(lds + RPI * (NI * wave + t) * 2 * D);
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :: "s"(dst), "v"(off[t] + (uint32_t)(row0 * 2 * D)), "s"(rs) : "memory", "m0");
     }
   }
 };
@@ -243,14 +250,12 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
   for (int db = 0; db < NDB; ++db) o[db] = v16f{};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  TileLoad<D> tk, tv;
-  tk.init(K, T);
-  tv.init(V, T);
+  TileLoadLds<D> tk, tv;
+  tk.init(K, T, wave, lane);
+  tv.init(V, T, wave, lane);
   if (nt > 0) {
-    tk.load(lo, tid);
-    tv.load(lo, tid);
-    tk.store_nat(lk[0], tid);
-    tv.store_nat(lv[0], tid);
+    tk.load(lk[0], lo, wave);
+    tv.load(lv[0], lo, wave);
   }
   wait_all_loads();
 
@@ -258,8 +263,8 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
     const int buf = j & 1;
     const bool pre = j + 1 < nt;
     if (pre) {
-      tk.load(lo + (j + 1) * 64, tid);
-      tv.load(lo + (j + 1) * 64, tid);
+      tk.load(lk[buf ^ 1], lo + (j + 1) * 64, wave);
+      tv.load(lv[buf ^ 1], lo + (j + 1) * 64, wave);
     }
     if (j >= ta && j <= tb) {
       const int n0 = lo + 64 * j;
@@ -311,10 +316,7 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
     }
     // The other buffer was last read in step j - 1, which every wave finished before the barrier
     // that ended it; one barrier per tile publishes the new tile.
-    if (pre) {
-      tk.store_nat(lk[buf ^ 1], tid);
-      tv.store_nat(lv[buf ^ 1], tid);
-    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): this wave's tile loads landed
     __syncthreads();
   }
 
@@ -404,9 +406,9 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
   // dS = 1 * (0 - 0) = 0 and P^T dO = 0: they add nothing, without a compare. Keys past T are
   // computed on zeros and never stored. Only the band 0 <= i - j < W is masked, and only in
   // the 32 x 32 blocks it cuts.
-  TileLoad<D> tq, tdo;
-  tq.init(p.q + slice, T);
-  tdo.init(p.dout + slice, T);
+  TileLoadLds<D> tq, tdo;
+  tq.init(p.q + slice, T, wave, lane);
+  tdo.init(p.dout + slice, T, wave, lane);
   // Wave 0 carries L of the tile's 64 queries (stored as -L log2(e)), wave 1 their Delta; both
   // through buffer descriptors over the slice's T values, so queries past T read as 0.
   const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(LSE), 0, T * 4, kBufferFlags);
@@ -423,11 +425,9 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
   };
   float st = 0.0f;
   if (nt > 0) {
-    tq.load(lo, tid);
-    tdo.load(lo, tid);
+    tq.load(lq[0], lo, wave);
+    tdo.load(ldo[0], lo, wave);
     st = load_stat(lo);
-    tq.store_nat(lq[0], tid);
-    tdo.store_nat(ldo[0], tid);
     store_stat(0, st);
   }
   wait_all_loads();
@@ -437,8 +437,8 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
     const int buf = j & 1;
     const bool pre = j + 1 < nt;
     if (pre) {
-      tq.load(lo + (j + 1) * 64, tid);
-      tdo.load(lo + (j + 1) * 64, tid);
+      tq.load(lq[buf ^ 1], lo + (j + 1) * 64, wave);
+      tdo.load(ldo[buf ^ 1], lo + (j + 1) * 64, wave);
       st = load_stat(lo + (j + 1) * 64);
     }
     if (j >= ta && j <= tb) {
@@ -485,11 +485,8 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
         }
       }
     }
-    if (pre) {
-      tq.store_nat(lq[buf ^ 1], tid);
-      tdo.store_nat(ldo[buf ^ 1], tid);
-      store_stat(buf ^ 1, st);
-    }
+    if (pre) store_stat(buf ^ 1, st);
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): this wave's tile loads landed
     __syncthreads();
   }
 
@@ -545,14 +542,12 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 3) void swa_bf16_dq_kernel(SwaB
   const int ta = q0 < T ? (wk0 - lo) / 64 : 1;
   const int tb = q0 < T ? (wk1 - lo) / 64 : 0;
 
-  TileLoad<D> tk, tv;
-  tk.init(K, T);
-  tv.init(V, T);
+  TileLoadLds<D> tk, tv;
+  tk.init(K, T, wave, lane);
+  tv.init(V, T, wave, lane);
   if (nt > 0) {
-    tk.load(lo, tid);
-    tv.load(lo, tid);
-    tk.store_nat(lk[0], tid);
-    tv.store_nat(lv[0], tid);
+    tk.load(lk[0], lo, wave);
+    tv.load(lv[0], lo, wave);
   }
   wait_all_loads();
 
@@ -560,8 +555,8 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 3) void swa_bf16_dq_kernel(SwaB
     const int buf = j & 1;
     const bool pre = j + 1 < nt;
     if (pre) {
-      tk.load(lo + (j + 1) * 64, tid);
-      tv.load(lo + (j + 1) * 64, tid);
+      tk.load(lk[buf ^ 1], lo + (j + 1) * 64, wave);
+      tv.load(lv[buf ^ 1], lo + (j + 1) * 64, wave);
     }
     if (j >= ta && j <= tb) {
       const int n0 = lo + 64 * j;
@@ -595,10 +590,7 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 3) void swa_bf16_dq_kernel(SwaB
         }
       }
     }
-    if (pre) {
-      tk.store_nat(lk[buf ^ 1], tid);
-      tv.store_nat(lv[buf ^ 1], tid);
-    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): this wave's tile loads landed
     __syncthreads();
   }
 
