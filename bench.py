@@ -1,6 +1,6 @@
 """Benchmark of the FP8 sliding-window-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|c2_train|ref_fp8|swa_bf16|swa_bf16_450m|fp8_train_450m]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c4|c1|c2|c5|c2_train|ref_fp8|swa_bf16|swa_bf16_450m|fp8_train_450m|fp8_block_train_450m]
 
 Default workload (the headline metric): fp8_swa_attention_forward on
 B=4, H=16, T=8192, D=64, window=1024, causal; Q/K/V bf16 ~ N(0, 1) with each head scaled by a
@@ -36,6 +36,10 @@ its 450M model shape B2 H20 T8192 D64 W2048; roofline = the backward entry point
 bf16 backward at the dequantised Q, K, V) as one autograd training step at the 450M model shape.
 --workload c2_train measures the C2 linear as an FP8 training step (forward, dgrad and wgrad GEMMs
 with their quantisers), beside torch's bf16 matmuls of the same three products.
+--workload fp8_block_train_450m measures one 450M block (d 1280, 20 heads, SwiGLU 3392, W 2048,
+QK-norm + RoPE; B2 x T8192) forward + backward with its Linears converted to FP8 (tensorwise, the
+reference's configs' recipe), beside rowwise and bf16 Linears, in ms per block: the reference's
+own FP8-linear training measurement (precision.py:3-9, an RTX 5090, reported as context).
 Other configs are parity-test cases; c1 / c4 are accepted here for measurement only.
 --library-gemm-reference runs no workload: it times hipBLASLt (through torch) at the GEMM shapes,
 the reference point for the library's own GEMMs.
@@ -83,6 +87,12 @@ WORKLOADS = {
     "swa_bf16_450m": dict(B=2, H=20, T=8192, D=64, W=2048, ref="B2 H20 T8192 D64 W2048"),
     # the differentiable FP8 attention (FP8 forward, bf16 backward) as a training step, 450M shape
     "fp8_train_450m": dict(B=2, H=20, T=8192, D=64, W=2048, granularity="head", ref="B2 H20 T8192 D64 W2048"),
+    # one 450M block (vanilla_matched: d 1280, 20 heads, SwiGLU 3392, W 2048) forward + backward
+    # with its Linears converted to FP8: the reference's own FP8-linear training measurement
+    # (precision.py:3-9: 13.61 ms tensorwise, 18.72 rowwise, 18.87 bf16 per block on an RTX 5090,
+    # compiled) -- other hardware, so context only, not a baseline
+    "fp8_block_train_450m": dict(B=2, T=8192, recipe="tensorwise", w_std=0.02,
+                                 reference_rtx5090_ms={"tensorwise": 13.61, "rowwise": 18.72, "bf16": 18.87}),
 }
 DATA = {
     "lognormal_heads": "synthetic (seeded; bf16 N(0,1) x a lognormal(0,1) factor per head)",
@@ -92,6 +102,7 @@ DATA = {
     "c2": "synthetic (seeded; bf16 x N(0,1) with 0.1% outliers x20; weight N(0,0.02), random init)",
     "c5": "synthetic (seeded; bf16 x N(0,1); every Linear weight N(0,0.02), random init)",
     "swa_bf16": "synthetic (seeded; bf16 q, k, v, dO ~ N(0,1))",
+    "block_train": "synthetic (seeded; bf16 x, dy ~ N(0,1); every Linear weight N(0,0.02), random init)",
 }
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on each workload, as
@@ -575,6 +586,8 @@ def main():
         line = run_linear_train(cfg, args)
     elif args.workload == "fp8_train_450m":
         line = run_fp8_train(cfg, args)
+    elif args.workload == "fp8_block_train_450m":
+        line = run_block_train(cfg, args)
     else:
         line = run_attention(cfg, args)
     print(json.dumps(line), flush=True)
@@ -879,6 +892,94 @@ def run_fp8_train(cfg, args):
         "backward": {"bound": "mfma", "achieved": round(b_tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(b_tf / BF16_PEAK_TFLOPS, 4), "ms": round(r["bwd_ms"], 4),
                      "kernels": "3 x dequant + swa_bf16_fwd (recompute) + flw_swa_bf16_bwd"},
+    }
+
+
+def bench_block_train(cfg, steps, warmup, recipe):
+    """One training step (forward + backward, weight gradients included) of the 450M block
+    (flower_amd.block.TransformerBlock, block_config()): its five Linears converted by
+    convert_model_to_fp8 with ``recipe`` (None: left in bf16, torch's GEMMs), the attention on the
+    HIP bf16 sliding-window kernels, norms / RoPE / SwiGLU / residual adds in torch."""
+    import copy
+    import torch.nn as nn
+    from flower_amd.block import TransformerBlock, block_config, init_block_
+    from flower_amd.precision import convert_model_to_fp8
+    B, T = cfg["B"], cfg["T"]
+    conf = block_config()
+    block = init_block_(TransformerBlock(conf), std=cfg["w_std"], seed=0).to("cuda", torch.bfloat16)
+    stack = nn.Module()
+    stack.blocks = nn.ModuleList([copy.deepcopy(block)])
+    if recipe is not None:
+        convert_model_to_fp8(stack, recipe=recipe, keep_bf16_blocks=0, verbose=False)
+    blk = stack.blocks[0]
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(B, T, conf.d_model, generator=g).to("cuda", torch.bfloat16).requires_grad_(True)
+    dy = torch.randn(B, T, conf.d_model, generator=g).to("cuda", torch.bfloat16)
+
+    def step():
+        x.grad = None
+        for prm in blk.parameters():
+            prm.grad = None
+        blk(x)[0].backward(dy)
+
+    _spin_up(step)
+    for _ in range(warmup):
+        step()
+    wall_ms = _wall_ms(step, steps)
+    ev = _events(steps, per=3)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        x.grad = None
+        for prm in blk.parameters():
+            prm.grad = None
+        ev[i][0].record()
+        out = blk(x)[0]
+        ev[i][1].record()
+        out.backward(dy)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    f_ms = np.array([a.elapsed_time(b) for a, b, _ in ev])
+    b_ms = np.array([b.elapsed_time(c) for _, b, c in ev])
+    lin = sum(m.weight.numel() for m in blk.modules() if isinstance(m, nn.Linear))
+    D, H, W = conf.d_model // conf.num_heads, conf.num_heads, conf.local_window
+    pairs = B * H * in_window_pairs(T, W)
+    return dict(ms_per_step=wall_ms, fwd_ms=float(f_ms.mean()), bwd_ms=float(b_ms.mean()),
+                linear_flops=6 * lin * B * T, attn_flops=14 * D * pairs,
+                converted=sum(type(m).__name__ == "Fp8Linear" for m in blk.modules()))
+
+
+def run_block_train(cfg, args):
+    """The 450M block's training step with FP8 Linears (cfg recipe, tensorwise as the reference's
+    configs), beside the same block with rowwise FP8 and with bf16 Linears, each in ms per block
+    (the reference's unit); FLOPs counted as 6 x Linear weights x tokens plus 14 D per in-window
+    attention pair (forward 4 D, backward 10 D). ``value`` is the FP8 block's TFLOP/s."""
+    runs = {name: bench_block_train(cfg, args.steps, args.warmup, rec)
+            for name, rec in (("tensorwise", "tensorwise"), ("rowwise", "rowwise"), ("bf16", None))}
+    main = runs[cfg["recipe"]]
+    flops = main["linear_flops"] + main["attn_flops"]
+    ref = cfg["reference_rtx5090_ms"]
+    return {
+        "metric": "450M block training step (forward + backward) with FP8 Linears, TFLOPS and ms per block",
+        "value": round(flops / (main["ms_per_step"] * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "spin_up_s": SPIN_UP_S,
+        "ms_per_step": round(main["ms_per_step"], 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": f"fp8_e4m3 Linears ({cfg['recipe']}; FP8 forward, dgrad and wgrad), bf16 attention and elementwise",
+        "data": DATA["block_train"],
+        "config": {"workload": "TransformerBlock forward + backward, 450M vanilla_matched", "B": cfg["B"],
+                   "T": cfg["T"], "d_model": 1280, "num_heads": 20, "ffn": "swiglu 3392", "window": 2048,
+                   "qk_norm": True, "recipe": cfg["recipe"], "converted_linears": main["converted"]},
+        "roofline": {"bound": "mfma", "achieved": round(flops / (main["ms_per_step"] * 1e-3) / 1e12, 2),
+                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(flops / (main["ms_per_step"] * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel": "the whole block step (wall time)",
+                     "kernel_ms": round(main["ms_per_step"], 4), "flop_per_launch": flops},
+        "ms_per_block": {k: round(v["ms_per_step"], 4) for k, v in runs.items()},
+        "forward_ms": {k: round(v["fwd_ms"], 4) for k, v in runs.items()},
+        "backward_ms": {k: round(v["bwd_ms"], 4) for k, v in runs.items()},
+        "speedup_vs_bf16": {k: round(runs["bf16"]["ms_per_step"] / v["ms_per_step"], 3)
+                            for k, v in runs.items() if k != "bf16"},
+        "reference_rtx5090_ms_per_block": ref,
     }
 
 

@@ -257,5 +257,77 @@ def block_flops(T: int, B: int, d_model: int, ffn_dim: int, num_heads: int, wind
     return linear + 4 * (d_model // num_heads) * B * num_heads * pairs
 
 
+def swiglu_hidden_dim(ffn_dim: int, param_match: bool = True) -> int:
+    """SwiGLU hidden width for a nominal ``ffn_dim`` (base.py:370-383): with ``param_match`` the
+    three d x h matrices get the parameters of GELU's two, 2/3 of the width rounded to a multiple
+    of 64 (5120 -> 3392)."""
+    if not param_match:
+        return ffn_dim
+    return max(64, round(((ffn_dim * 2) // 3) / 64) * 64)
+
+
+class FeedForward(nn.Module):
+    """base.py:485-552 without dropout (0 in the 450M configs): the GELU MLP (``net.0``, GELU,
+    ``net.3``) or SwiGLU (``down(silu(gate(x)) * up(x))``), by ``config.ffn_activation``. Plain
+    nn.Linear layers, which ``convert_model_to_fp8`` replaces by Fp8Linear as the reference's
+    conversion replaces them by Float8Linear."""
+
+    def __init__(self, config) -> None:
+        super().__init__()
+        d, ffn = config.d_model, config.ffn_dim
+        bias = bool(getattr(config, "use_bias", True))
+        self.activation = getattr(config, "ffn_activation", "gelu")
+        if self.activation not in {"gelu", "swiglu"}:
+            raise ValueError(f"ffn_activation must be 'gelu' or 'swiglu', got {self.activation!r}")
+        if self.activation == "gelu":
+            self.net = nn.Sequential(nn.Linear(d, ffn, bias=bias), nn.GELU(), nn.Identity(),
+                                     nn.Linear(ffn, d, bias=bias))
+            self.net[-1]._is_residual_out = True
+        else:
+            hidden = swiglu_hidden_dim(ffn, bool(getattr(config, "ffn_param_match", True)))
+            self.hidden_dim = hidden
+            self.gate = nn.Linear(d, hidden, bias=bias)
+            self.up = nn.Linear(d, hidden, bias=bias)
+            self.down = nn.Linear(hidden, d, bias=bias)
+            self.down._is_residual_out = True
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.activation == "gelu":
+            return self.net(x)
+        return self.down(torch.nn.functional.silu(self.gate(x)) * self.up(x))
+
+
+class TransformerBlock(nn.Module):
+    """base.py:698-722 for training: ``x + attn(ln1(x))``, then ``+ ff(ln2(x))``, returning
+    ``(x, memory)`` as the reference's block does. The attention is ``CausalSelfAttention`` (the
+    HIP bf16 sliding-window kernels, or the FP8 route with ``attn_precision: "fp8"``) with the
+    config's window; RMSNorm norms (``norm_type: rmsnorm``, the 450M configs' choice)."""
+
+    def __init__(self, config) -> None:
+        super().__init__()
+        if getattr(config, "norm_type", "rmsnorm") != "rmsnorm":
+            raise ValueError("only norm_type 'rmsnorm' is built")
+        self.ln1 = RMSNorm(config.d_model)
+        self.attn = CausalSelfAttention(config, getattr(config, "local_window", None))
+        self.ln2 = RMSNorm(config.d_model)
+        self.ff = FeedForward(config)
+
+    def forward(self, x: torch.Tensor, memory: torch.Tensor | None = None):
+        x = x + self.attn(self.ln1(x))
+        x = x + self.ff(self.ln2(x))
+        return x, memory
+
+
+def block_config(**overrides) -> SimpleNamespace:
+    """The 450M ``vanilla_matched`` block (configs/sweep13_450m_longctx_fp8.yaml:94-113): d_model
+    1280, 20 heads, ffn 5120 as param-matched SwiGLU (3392), window 2048, RoPE 10000, QK-norm,
+    RMSNorm, no biases, bf16 attention."""
+    cfg = dict(d_model=1280, num_heads=20, ffn_dim=5120, ffn_activation="swiglu", ffn_param_match=True,
+               local_window=2048, rope_base=10000.0, qk_norm=True, norm_type="rmsnorm", use_bias=False,
+               max_seq_len=8192, attn_precision="bf16")
+    cfg.update(overrides)
+    return SimpleNamespace(**cfg)
+
+
 __all__ = ["RMSNorm", "Fp8CausalSelfAttention", "Fp8FeedForward", "Fp8DecoderBlock", "init_block_",
-           "block_flops"]
+           "block_flops", "swiglu_hidden_dim", "FeedForward", "TransformerBlock", "block_config"]

@@ -172,7 +172,8 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmParams p) {
 
 // ---------------------------------------------------------------- 256 x 256 tile, direct-to-LDS
 //
-// For K % 128 == 0 (every model shape). Workgroup tile 256 (n) x 256 (m), 8 waves (two per SIMD)
+// For K % 64 == 0 (every model shape; K % 128 == 64 ends on a 64-deep stage). Workgroup tile
+// 256 (n) x 256 (m), 8 waves (two per SIMD)
 // in a 2 x 4 grid of 128 (n) x 64 (m) wave tiles: per 64-deep K chunk a wave reads 4 + 2
 // fragments (12 KB of LDS) for 8 v_mfma_f32_32x32x64_f8f6f4 (512 MFMA cycles), and the two waves
 // of a SIMD interleave one's LDS reads with the other's MFMAs.
@@ -427,7 +428,7 @@ __device__ __forceinline__ void staged_epilogue(const v16f (&acc)[4][2], const f
 }
 
 // One 256 x 256 output tile: K loop over two LDS stages, then the scaled bf16 epilogue.
-template <int XD = 0>
+template <int XD = 0, bool HALFK = false>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
                                           int n0, int wave, int lane, int sbase, int nst, int split) {
   const int wn = wave & 1, wm = wave >> 1;        // 128 n rows, 64 m columns
@@ -437,24 +438,32 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
   const int op = wave >> 2;                       // uniform
   const uint8_t* gsrc = op == 0 ? p.w8 : p.x8;
   uint32_t goff[8];
+  uint32_t hi_half = 0;                           // bit t: instruction t's chunk is in bytes 64-127
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int r = 64 * (wave & 3) + 8 * t + (lane >> 3);      // row within the operand tile
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     const int grow = op == 0 ? min(n0 + r, p.N - 1) : min(m0 + r, p.M - 1);
     goff[t] = (uint32_t)grow * (uint32_t)p.K + 16u * (uint32_t)c;
+    hi_half |= (uint32_t)(c >> 2) << t;
   }
+  // K % 128 == 64: the range's last stage holds 64 K bytes; its lanes for bytes 64-127 load
+  // bytes 0-63 again (in bounds; that half of the stage is never read). Instances of their own
+  // (HALFK), so that the K % 128 == 0 kernels keep their code.
+  const bool half_last = HALFK && sbase + nst == (p.K + kFBK - 1) / kFBK;
   const int lbase = op * kFOpBytes + (64 * (wave & 3)) * 128;
   // Issued from inline assembly: the compiler then does not track these LDS writes and does not
   // drain the prefetch before every fragment read; the kernel orders them itself (an explicit
   // vmcnt wait for this wave's loads, then a workgroup barrier, before a stage is read).
   auto issue = [&](uint8_t* stage, int s) __attribute__((always_inline)) {
     const uint32_t k0 = (uint32_t)(sbase + s) * kFBK;
+    const uint32_t back = half_last && s == nst - 1 ? 64u : 0u;
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8_t*)(stage + lbase);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
       asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                   :: "s"(lds + t * 1024), "v"(goff[t] + k0), "s"(gsrc) : "memory", "m0");
+                   :: "s"(lds + t * 1024), "v"(goff[t] + k0 - (((hi_half >> t) & 1u) ? back : 0u)), "s"(gsrc)
+                   : "memory", "m0");
   };
 
   v16f acc[4][2];
@@ -478,6 +487,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
     lds_barrier();                                // ... and every wave's
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc) {
+      if (kc == 1 && half_last && s == nst - 1) break;      // a 64-deep last stage
       v8i a[4], b[2];
 #pragma unroll
       for (int i = 0; i < 4; ++i) a[i] = swz_frag(cur, 4 * wn + i, kc, lane);
@@ -583,6 +593,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* st0, uin
 // (2 x 2 MFMAs per 64-deep K chunk), a stage holding the 256 W rows and 128 X rows (48 of its
 // 64 KB), the same swizzle, barriers and accumulation order as gemm_tile (the results are
 // identical), and the epilogue staged through st0 (128 rows x 512 bytes).
+template <bool HALFK = false>
 __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0, uint8_t* st1, int m0,
                                               int n0, int wave, int lane, int sbase, int nst, int split) {
   const int wn = wave & 3, wm = wave >> 2;        // 64 n rows, 64 m columns
@@ -590,6 +601,7 @@ __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0,
   // instructions of 8 rows, rows 256 .. 383 being X rows 0 .. 127. Instruction t of a wave reads
   // one operand (256 is a multiple of 8), so its base address is a scalar.
   uint32_t goff[6];
+  uint32_t hi_half = 0;                           // bit t: instruction t's chunk is in bytes 64-127
 #pragma unroll
   for (int t = 0; t < 6; ++t) {
     const int row0 = 48 * wave + 8 * t;
@@ -598,9 +610,12 @@ __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0,
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     const int grow = xop ? min(m0 + r, p.M - 1) : min(n0 + r, p.N - 1);
     goff[t] = (uint32_t)grow * (uint32_t)p.K + 16u * (uint32_t)c;
+    hi_half |= (uint32_t)(c >> 2) << t;
   }
+  const bool half_last = HALFK && sbase + nst == (p.K + kFBK - 1) / kFBK;
   auto issue = [&](uint8_t* stage, int s) __attribute__((always_inline)) {
     const uint32_t k0 = (uint32_t)(sbase + s) * kFBK;
+    const uint32_t back = half_last && s == nst - 1 ? 64u : 0u;
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8_t*)stage;
 #pragma unroll
     for (int t = 0; t < 6; ++t) {
@@ -609,7 +624,8 @@ __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0,
       const uint32_t dst = lds + (xop ? kFOpBytes + (row0 - 256) * 128 : row0 * 128);
       const uint8_t* src = xop ? p.x8 : p.w8;
       asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                   :: "s"(dst), "v"(goff[t] + k0), "s"(src) : "memory", "m0");
+                   :: "s"(dst), "v"(goff[t] + k0 - (((hi_half >> t) & 1u) ? back : 0u)), "s"(src)
+                   : "memory", "m0");
     }
   };
 
@@ -630,6 +646,7 @@ __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0,
     lds_barrier();                                // ... and every wave's
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc) {
+      if (kc == 1 && half_last && s == nst - 1) break;      // a 64-deep last stage
       v8i a[2], b[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) a[i] = swz_frag(cur, 2 * wn + i, kc, lane);
@@ -735,7 +752,7 @@ __device__ __forceinline__ void gemm_tile_128(const GemmParams& p, uint8_t* st0,
 
 // XD > 0: the q / k transform epilogue of flw_fp8_scaled_mm_qk_norm_rope_amax for head dim XD,
 // compiled as instances of their own so that the other GEMMs keep their register allocation.
-template <int TM, int XD = 0>
+template <int TM, int XD = 0, bool HALFK = false>
 __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p) {
   // One array per stage: every LDS access below names its stage at compile time, so the
   // compiler can see that the direct-to-LDS loads in flight write the other stage.
@@ -754,7 +771,7 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
   const int ntiles = p.tiles_n * p.tiles_m;
 
   // Split-K: work item t = split * ntiles + tile; split s covers K stages [s nst / S, (s+1) nst / S).
-  const int nst_all = p.K / kFBK;
+  const int nst_all = (p.K + kFBK - 1) / kFBK;     // the last one 64 deep when K % 128 == 64
   for (int t = L; t < ntiles * p.splits; t += G) {
     const int split = t / ntiles, tt = t % ntiles;
     const int group = tt / (kGroupM * p.tiles_n);
@@ -763,8 +780,8 @@ __global__ __launch_bounds__(kFThreads, 1) void fp8_gemm_256_kernel(GemmParams p
     const int tm = first_m + (tt % (kGroupM * p.tiles_n)) % gm;
     const int tn = (tt % (kGroupM * p.tiles_n)) / gm;
     const int s0 = split * nst_all / p.splits, s1 = (split + 1) * nst_all / p.splits;
-    if constexpr (TM == 256) gemm_tile<XD>(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
-    else gemm_tile_128(p, st0, st1, tm * TM, tn * kFBN, wave, lane, s0, s1 - s0, split);
+    if constexpr (TM == 256) gemm_tile<XD, HALFK>(p, st0, st1, tm * kFBM, tn * kFBN, wave, lane, s0, s1 - s0, split);
+    else gemm_tile_128<HALFK>(p, st0, st1, tm * TM, tn * kFBN, wave, lane, s0, s1 - s0, split);
   }
 }
 
@@ -1019,7 +1036,7 @@ static int splitk_of(int64_t tiles, int64_t K) {
 }
 
 static size_t splitk_bytes(int64_t M, int64_t N, int64_t K) {
-  if (K % kFBK != 0) return 0;
+  if (K % 64 != 0) return 0;
   const int64_t tiles = ((N + kFBN - 1) / kFBN) * ((M + kFBM - 1) / kFBM);
   const int sp = splitk_of(tiles, K);
   return sp > 1 ? (size_t)sp * (size_t)M * (size_t)N * sizeof(float) : 0;
@@ -1047,7 +1064,7 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
   p.res = static_cast<const uint16_t*>(res); p.rs = rs;
   FLW_REQUIRE(res == nullptr || (rs >= N && rs % 4 == 0 && ((uintptr_t)res & 7) == 0), FLW_E_INVALID,
               "residual rows must be 8-byte aligned with a stride >= N, a multiple of 4");
-  if (K % kFBK == 0 && N * K < (1ll << 32) && M * K < (1ll << 32)) {
+  if (K % 64 == 0 && N * K < (1ll << 32) && M * K < (1ll << 32)) {
     p.tiles_n = (int)((N + kFBN - 1) / kFBN);
     p.tiles_m = (int)((M + kFBM - 1) / kFBM);
     const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
@@ -1069,8 +1086,13 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
       p.splits = p.splits / 2 > 1 ? p.splits / 2 : 1;
       if (p.splits == 1) p.part = nullptr;
     }
-    const void* kern = narrow ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<128>)
-                     : xform == nullptr ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256>)
+    // K % 128 == 64 (no q / k transform: its entry point requires K % 128 == 0): the instances
+    // whose last K stage is 64 deep.
+    const bool halfk = K % kFBK != 0;
+    const void* kern = narrow ? (halfk ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<128, 0, true>)
+                                       : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<128>))
+                     : xform == nullptr ? (halfk ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, 0, true>)
+                                                 : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256>))
                      : gcols == 32 ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, 32>)
                      : gcols == 64 ? reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, 64>)
                      : reinterpret_cast<const void*>(&fp8_gemm_256_kernel<256, 128>);
@@ -1105,7 +1127,7 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
   }
   // The general kernel has no group-amax epilogue: refuse rather than leave amax_out unwritten.
   FLW_REQUIRE(gmax == nullptr, FLW_E_UNSUPPORTED,
-              "the group amax needs K %% %d == 0 and M*K, N*K < 2^32 (the 256 x 256 kernel)", kFBK);
+              "the group amax needs K %% 64 == 0 and M*K, N*K < 2^32 (the 256 x 256 kernel)");
   p.tiles_n = (int)((N + kGBN - 1) / kGBN);
   const int64_t tiles = (int64_t)p.tiles_n * ((M + kGBM - 1) / kGBM);
   FLW_REQUIRE(tiles <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "grid too large");
@@ -1174,7 +1196,7 @@ extern "C" int flw_fp8_scaled_mm_group_amax(const uint8_t* x8, int64_t M, int64_
   FLW_REQUIRE(amax_out != nullptr, FLW_E_INVALID, "null amax_out");
   FLW_REQUIRE(group_cols >= 8 && group_cols <= 256 && (group_cols & (group_cols - 1)) == 0 && N % group_cols == 0,
               FLW_E_INVALID, "group_cols must be a power of two in [8, 256] dividing N");
-  FLW_REQUIRE(K % kFBK == 0, FLW_E_UNSUPPORTED, "the group amax needs K %% %d == 0", kFBK);
+  FLW_REQUIRE(K % 64 == 0, FLW_E_UNSUPPORTED, "the group amax needs K %% 64 == 0");
   return scaled_mm(x8, M, K, w8, N, x_scale, x_scale_count, w_scale, w_scale_count, y, y_row_stride,
                    static_cast<hipStream_t>(stream), nullptr, 0, nullptr, 0, amax_out, (int)group_cols);
 }

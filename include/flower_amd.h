@@ -362,7 +362,7 @@ int flw_fp8_scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8
  * v heads), so that the Q / K / V quantiser needs no amax pass of its own. This is the "fuse
  * quantisation into the producer" step of the path: `qkv_heads` (flower/models/base.py:618-639)
  * feeds `_per_tensor_fp8` (flower/kernels/fp8_swa_attention.py:195-205), whose amax this
- * replaces. group_cols: a power of two in [8, 256] dividing N; K % 128 == 0, N % 8 == 0,
+ * replaces. group_cols: a power of two in [8, 256] dividing N; K % 64 == 0, N % 8 == 0,
  * 16-byte aligned y rows, M * K and N * K < 2^32 (other shapes return FLW_E_UNSUPPORTED; the
  * caller then takes the quantiser's own amax pass). amax_out is overwritten (cleared by the call
  * itself). */

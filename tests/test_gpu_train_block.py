@@ -1,0 +1,121 @@
+"""GPU: the training block (flower_amd.block.TransformerBlock, base.py:698-722 with the SwiGLU feed-
+forward of base.py:485-552) forward and backward, with bf16 Linears and with its Linears converted
+to FP8 by convert_model_to_fp8, against the same block computed in float32 torch from the same
+parameters (RMSNorm, qkv, HeadRMSNorm of q and k, RoPE, masked softmax attention over the window,
+out, SwiGLU, the two residual adds).
+
+Gates (written here): bf16 Linears -- output and every gradient within 3 % (Frobenius, relative)
+of float32, the bf16 rounding of each stage; FP8 Linears -- within 12 % for the output's update
+(out - x) and the gradients (each FP8 GEMM adds 2-4 %, and a backward chains several), and the
+tensorwise and rowwise recipes both inside that gate.
+"""
+
+import copy
+
+import pytest
+import torch
+import torch.nn as nn
+
+pytestmark = pytest.mark.gpu
+
+SHAPE = dict(B=2, T=320)
+CFG = dict(d_model=256, num_heads=4, ffn_dim=1536, local_window=96, max_seq_len=512)
+
+
+def _block():
+    from flower_amd.block import TransformerBlock, block_config, init_block_
+    conf = block_config(**CFG)
+    blk = init_block_(TransformerBlock(conf), std=0.05, seed=5)
+    with torch.no_grad():
+        for norm in (blk.ln1, blk.ln2):
+            norm.weight.copy_(1.0 + 0.1 * torch.randn(norm.weight.shape, generator=torch.Generator().manual_seed(9)))
+    return blk.to("cuda", torch.bfloat16), conf
+
+
+def _reference(blk, conf, x, dy):
+    """float32 forward and backward of the same block, from its parameters."""
+    P = {n: p.detach().float().clone().requires_grad_(True) for n, p in blk.named_parameters()}
+    x = x.detach().float().clone().requires_grad_(True)
+    B, T, d = x.shape
+    H, W = conf.num_heads, conf.local_window
+    D = d // H
+
+    def rms(t, w, eps=1e-6):
+        return t * t.pow(2).mean(-1, keepdim=True).add(eps).rsqrt() * w
+
+    h = rms(x, P["ln1.weight"])
+    q, k, v = (h @ P["attn.qkv.weight"].t()).chunk(3, dim=-1)
+    q, k, v = (t.reshape(B, T, H, D).transpose(1, 2) for t in (q, k, v))
+    q, k = (t * t.pow(2).mean(-1, keepdim=True).add(blk.attn.qk_norm.eps).rsqrt() for t in (q, k))
+    cos, sin = (t.to(x.device).float() for t in blk.attn.rope._tables(T))
+
+    def rot(t):
+        return torch.stack((-t[..., 1::2], t[..., ::2]), dim=-1).flatten(-2)
+    q, k = q * cos + rot(q) * sin, k * cos + rot(k) * sin
+    i = torch.arange(T, device=x.device)
+    band = (i[:, None] >= i[None, :]) & (i[:, None] - i[None, :] < W)
+    s = (q @ k.transpose(-1, -2)) / D ** 0.5
+    a = torch.softmax(s.masked_fill(~band, float("-inf")), dim=-1) @ v
+    x1 = x + a.transpose(1, 2).reshape(B, T, d) @ P["attn.out.weight"].t()
+    h2 = rms(x1, P["ln2.weight"])
+    f = torch.nn.functional.silu(h2 @ P["ff.gate.weight"].t()) * (h2 @ P["ff.up.weight"].t())
+    y = x1 + f @ P["ff.down.weight"].t()
+    y.backward(dy.float())
+    return y.detach(), x.grad, {n: p.grad for n, p in P.items()}
+
+
+def _run(blk, x, dy):
+    x = x.clone().requires_grad_(True)
+    y = blk(x)[0]
+    y.backward(dy)
+    return y.detach().float(), x.grad.float(), {n: p.grad.float() for n, p in blk.named_parameters()}
+
+
+def _rel(a, b):
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _inputs(conf):
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(SHAPE["B"], SHAPE["T"], conf.d_model, generator=g).to("cuda", torch.bfloat16)
+    dy = torch.randn(SHAPE["B"], SHAPE["T"], conf.d_model, generator=g).to("cuda", torch.bfloat16)
+    return x, dy
+
+
+def test_block_shape_and_swiglu_width():
+    blk, conf = _block()
+    assert blk.ff.hidden_dim == 1024          # 2/3 of 1536, a multiple of 64
+    x, _ = _inputs(conf)
+    with torch.no_grad():
+        y, mem = blk(x)
+    assert y.shape == x.shape and y.dtype == torch.bfloat16 and mem is None
+
+
+def test_bf16_block_forward_backward_against_fp32():
+    blk, conf = _block()
+    x, dy = _inputs(conf)
+    y_ref, gx_ref, gp_ref = _reference(blk, conf, x, dy)
+    y, gx, gp = _run(blk, x, dy)
+    assert _rel(y - x.float(), y_ref - x.float()) < 0.03
+    assert _rel(gx, gx_ref) < 0.03
+    for name, g in gp.items():
+        assert _rel(g, gp_ref[name]) < 0.03, name
+
+
+@pytest.mark.parametrize("recipe", ["tensorwise", "rowwise"])
+def test_fp8_block_forward_backward_against_fp32(recipe):
+    from flower_amd.precision import Fp8Linear, convert_model_to_fp8
+    blk, conf = _block()
+    x, dy = _inputs(conf)
+    y_ref, gx_ref, gp_ref = _reference(blk, conf, x, dy)
+    stack = nn.Module()
+    stack.blocks = nn.ModuleList([copy.deepcopy(blk)])
+    info = convert_model_to_fp8(stack, recipe=recipe, keep_bf16_blocks=0, verbose=False)[1]
+    fblk = stack.blocks[0]
+    assert info["fp8_converted_linears"] == 5
+    assert sum(isinstance(m, Fp8Linear) for m in fblk.modules()) == 5
+    y, gx, gp = _run(fblk, x, dy)
+    assert _rel(y - x.float(), y_ref - x.float()) < 0.12
+    assert _rel(gx, gx_ref) < 0.12
+    for name, g in gp.items():
+        assert _rel(g, gp_ref[name]) < 0.12, name
