@@ -1027,6 +1027,60 @@ extern "C" size_t flw_quant_cols_workspace_bytes(int64_t rows, int64_t cols) {
   return (size_t)(nchunks * (cols > ncb ? cols : ncb)) * sizeof(uint32_t);
 }
 
+// ---------------------------------------------------------------- e4m3 codes transposed
+//
+// out_t [cols, ld] = codes [rows, cols] transposed, columns rows .. ld - 1 of out_t zero: the
+// transposed operand of a GEMM from codes quantised with one scale for the whole matrix (the
+// tensorwise recipe), where the column codes equal the row codes. 64 x 64-byte tiles through LDS:
+// thread t loads 16 bytes of row t / 4 (64-byte rows of the tile, padded to 80 in LDS), then
+// gathers the 16 bytes of output row t / 4 at input rows 16 (t % 4) .. + 15 and stores them
+// as one 16-byte vector. Rows past `rows` read as zero, columns past `cols` are not stored.
+constexpr int kTT = 64, kTPitch = 80;
+
+__global__ __launch_bounds__(256) void transpose_u8_kernel(const uint8_t* __restrict__ src, int64_t rows,
+                                                           int64_t cols, int64_t sld, uint8_t* __restrict__ dst,
+                                                           int64_t dld) {
+  __shared__ __align__(16) uint8_t t[kTT * kTPitch];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * kTT, r0 = (int64_t)blockIdx.y * kTT;
+  {
+    const int r = tid >> 2, q = tid & 3;
+    const int64_t gr = r0 + r, gc = c0 + 16 * q;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gr < rows && gc < cols) v = *reinterpret_cast<const uint4*>(src + gr * sld + gc);
+    *reinterpret_cast<uint4*>(t + r * kTPitch + 16 * q) = v;
+  }
+  __syncthreads();
+  const int c = tid >> 2, q = tid & 3;
+  const int64_t oc = c0 + c, orow0 = r0 + 16 * q;
+  if (oc >= cols || orow0 >= dld) return;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) x |= (uint32_t)t[(16 * q + 4 * j + b) * kTPitch + c] << (8 * b);
+    w[j] = x;
+  }
+  *reinterpret_cast<uint4*>(dst + oc * dld + orow0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+extern "C" int flw_transpose_e4m3(const uint8_t* codes, int64_t rows, int64_t cols, int64_t row_stride,
+                                  uint8_t* out_t, int64_t ld, void* stream) {
+  FLW_REQUIRE(codes != nullptr && out_t != nullptr, FLW_E_INVALID, "null pointer");
+  FLW_REQUIRE(rows > 0 && cols > 0, FLW_E_INVALID, "empty matrix");
+  FLW_REQUIRE(cols % 16 == 0 && row_stride % 16 == 0 && row_stride >= cols && ((uintptr_t)codes & 15) == 0,
+              FLW_E_INVALID, "cols and row_stride must be multiples of 16, codes 16-byte aligned");
+  FLW_REQUIRE(ld >= rows && ld % 16 == 0 && ((uintptr_t)out_t & 15) == 0, FLW_E_INVALID,
+              "ld must be >= rows and a multiple of 16, out_t 16-byte aligned");
+  const int64_t gx = (cols + kTT - 1) / kTT, gy = (ld + kTT - 1) / kTT;
+  FLW_REQUIRE(gx <= 0x7FFFFFFF && gy <= 65535, FLW_E_UNSUPPORTED, "matrix too large");
+  (void)launch_args(reinterpret_cast<const void*>(&transpose_u8_kernel), dim3((unsigned)gx, (unsigned)gy),
+                    dim3(256), 0, static_cast<hipStream_t>(stream), nullptr, nullptr, codes, rows, cols,
+                    row_stride, out_t, ld);
+  return check_launch("flw_transpose_e4m3");
+}
+
 extern "C" int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
                                    int granularity, uint8_t* out_t, int64_t ld, float* scale_out,
                                    void* workspace, size_t workspace_bytes, void* stream) {

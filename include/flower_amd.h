@@ -192,6 +192,17 @@ int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, in
                         int granularity, uint8_t* out_t, int64_t ld, float* scale_out, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* e4m3 codes [rows, cols] transposed to out_t [cols, ld] (ld >= rows, ld % 16 == 0; columns
+ * rows .. ld - 1 of out_t zero). With one scale for the whole matrix (the tensorwise recipe) a
+ * matrix's per-column codes equal its per-row codes, so the transposed operands of the backward
+ * GEMMs come from the forward's and the gradient's row codes by this byte transpose, as torchao's
+ * Float8Linear reuses its tensorwise fp8 casts transposed (torchao 0.18.0, not vendored; enabled
+ * at flower/train.py:368-370): flw_quant_cols_e4m3(FLW_SCALE_TENSOR) of the same matrix, bit for
+ * bit, without reading it again in bf16. cols and row_stride multiples of 16, 16-byte aligned
+ * codes and out_t. */
+int flw_transpose_e4m3(const uint8_t* codes, int64_t rows, int64_t cols, int64_t row_stride, uint8_t* out_t,
+                       int64_t ld, void* stream);
+
 /* ---------------------------------------------------------------- attention */
 
 /* FP8 causal sliding-window attention forward on pre-quantised operands, replacing the launch

@@ -135,3 +135,17 @@ def test_c2_shape_gradients_within_fp8_bounds(recipe):
         err = float((got.float() - want).norm() / want.norm())
         ratio = float(got.float().norm() / want.norm())
         assert err < 0.05 and 0.9 < ratio < 1.1, (err, ratio)
+
+
+@pytest.mark.parametrize("R,C,ld", [(4096, 1024, 4096), (300, 48, 384), (1, 16, 16), (129, 3392, 256), (70, 208, 80)])
+def test_transposed_tensorwise_codes_equal_the_column_quantiser(R, C, ld):
+    """flw_transpose_e4m3 on the per-tensor row codes of x gives flw_quant_cols_e4m3's per-tensor
+    column codes of x bit for bit (one scale for the whole matrix), with the columns past R zero."""
+    from flower_amd.precision import _quantize_rows, quantize_cols, transpose_codes
+    x = (_rnd((R, C), R + C) * 3).cuda()
+    x8, sx = _quantize_rows(x, "tensorwise")
+    want8, want_s = quantize_cols(x, "tensor", ld)
+    got8 = transpose_codes(x8, ld)
+    assert torch.equal(sx, want_s)
+    assert torch.equal(got8, want8)
+    assert not got8[:, R:].any()
