@@ -86,6 +86,44 @@ def fp8_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, local_windo
     return fp8_swa_attention_forward(q, k, v, window, granularity=granularity)
 
 
+class _QkvHeadsFn(torch.autograd.Function):
+    """``qkv_heads``' split, HeadRMSNorm and RoPE on the qkv projection's bf16 output y [B, T, 3 H D]
+    in one HIP pass each way (flw_qkv_heads_fwd / flw_qkv_heads_bwd): q', k', v as contiguous
+    (B, H, T, D); the backward returns dy [B, T, 3 H D] as torch's autograd of the same expressions
+    does (its bf16 roundings of the RoPE products, the norm's backward in fp32)."""
+
+    @staticmethod
+    def forward(ctx, y, num_heads, norm, eps, cos, sin):
+        lib = _lib.load()
+        B, T, C = y.shape
+        D = C // (3 * num_heads)
+        if y.stride(-1) != 1 or y.stride(0) != T * y.stride(1) or y.stride(1) % 8 or y.data_ptr() % 16:
+            y = y.contiguous()
+        q, k, v = (torch.empty((B, num_heads, T, D), dtype=y.dtype, device=y.device) for _ in range(3))
+        rc = lib.flw_qkv_heads_fwd(y.data_ptr(), B, T, num_heads, D, y.stride(1), int(norm), float(eps),
+                                   cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   _lib.stream_of(y))
+        _lib.check(rc, "qkv_heads")
+        ctx.save_for_backward(y, cos, sin)
+        ctx.meta = (num_heads, norm, eps, D)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        y, cos, sin = ctx.saved_tensors
+        H, norm, eps, D = ctx.meta
+        B, T, C = y.shape
+        grads = [(g if g is not None else torch.zeros((B, H, T, D), dtype=y.dtype, device=y.device))
+                 .to(y.dtype).contiguous() for g in (dq, dk, dv)]
+        dy = torch.empty((B, T, C), dtype=y.dtype, device=y.device)
+        lib = _lib.load()
+        rc = lib.flw_qkv_heads_bwd(y.data_ptr(), B, T, H, D, y.stride(1), int(norm), float(eps), cos.data_ptr(),
+                                   sin.data_ptr(), grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(),
+                                   dy.data_ptr(), C, _lib.stream_of(y))
+        _lib.check(rc, "qkv_heads backward")
+        return dy, None, None, None, None, None
+
+
 class HeadRMSNorm(nn.Module):
     """Parameter-free RMSNorm over the head dimension (QK-norm), base.py:341-357."""
 
@@ -204,8 +242,18 @@ class CausalSelfAttention(nn.Module):
         return seq_len if self.local_window is None else self.local_window
 
     def qkv_heads(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """Project to per-head (q, k, v), apply QK-norm, then RoPE (base.py:618-639)."""
-        q, k, v = self.qkv(x).chunk(3, dim=-1)
+        """Project to per-head (q, k, v), apply QK-norm, then RoPE (base.py:618-639). bf16 on the
+        GPU: the split, norm and RoPE run as one HIP pass each way (``_QkvHeadsFn``), q, k, v
+        contiguous; otherwise the reference's torch expressions."""
+        y = self.qkv(x)
+        if y.is_cuda and y.dtype == torch.bfloat16 and self.head_dim in (32, 64, 128):
+            cos, sin = self.rope.tables(y.shape[1], y.dtype, y.device)
+            eps = self.qk_norm.eps if self.qk_norm is not None else 0.0
+            q, k, v = _QkvHeadsFn.apply(y, self.num_heads, self.qk_norm is not None, eps, cos, sin)
+            if self.fp8_attention_sim:
+                q, k, v = _fake_quant_e4m3(q), _fake_quant_e4m3(k), _fake_quant_e4m3(v)
+            return q, k, v
+        q, k, v = y.chunk(3, dim=-1)
         q, k, v = self._split(q), self._split(k), self._split(v)
         if self.qk_norm is not None:
             q, k = self.qk_norm(q), self.qk_norm(k)

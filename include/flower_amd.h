@@ -146,6 +146,26 @@ int flw_qk_norm_rope_quant_e4m3(const void* q, const void* k, const void* v, int
                                 void* q_out, void* k_out, void* workspace, size_t workspace_bytes,
                                 void* stream);
 
+/* CausalSelfAttention.qkv_heads (flower/models/base.py:618-639) for training, bf16: the qkv
+ * projection's output qkv [B T, qkv_row_stride] (q | k | v column blocks of H D values) split into
+ * per-head q', k', v, contiguous (B, H, T, D) bf16, with HeadRMSNorm of q and k when qk_norm
+ * (base.py:341-357) and RoPE of q and k from the [T, D] bf16 tables (base.py:436-483), rounded as
+ * torch rounds them (the transform of flw_qk_norm_rope_quant_e4m3); one pass in place of the torch
+ * ops' ~10 forward kernels. D in {32, 64, 128}; 16-byte aligned rows and tables. */
+int flw_qkv_heads_fwd(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t D, int64_t qkv_row_stride,
+                      int qk_norm, float eps, const void* rope_cos, const void* rope_sin, void* q, void* k,
+                      void* v, void* stream);
+
+/* The backward of flw_qkv_heads_fwd, as torch's autograd of the same expressions computes it:
+ * dq', dk', dv contiguous (B, H, T, D) bf16 and the forward's qkv -> dqkv [B T, dqkv_row_stride]
+ * bf16. RoPE backward with torch's bf16 roundings (t1 = bf16(g cos), t2 = bf16(g sin),
+ * dn[2i] = bf16(t1[2i] + t2[2i+1]), dn[2i+1] = bf16(t1[2i+1] - t2[2i])), then the HeadRMSNorm
+ * backward in fp32 from the forward's input x (r = rsqrt(mean(x^2) + eps),
+ * dx = bf16(dn r - x r^3 sum(dn x) / D)); dv copied into the v columns. */
+int flw_qkv_heads_bwd(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t D, int64_t qkv_row_stride,
+                      int qk_norm, float eps, const void* rope_cos, const void* rope_sin, const void* dq,
+                      const void* dk, const void* dv, void* dqkv, int64_t dqkv_row_stride, void* stream);
+
 /* flw_quant_qkv_e4m3 without a workspace: no counterpart in the reference. For callers that
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): the amax partials live in a library-owned device array of

@@ -13,10 +13,18 @@
 ``rope``     base.py:478-483 with rotate_half (:465-469), tables given ([T, D], already in the
              activations' dtype): out = dtype( dtype(x * cos) + dtype(rotate_half(x) * sin) ),
              rotate_half(x)[2i] = -x[2i+1], rotate_half(x)[2i+1] = x[2i].
+``rope_backward``  the gradient torch's autograd gives x of ``rope`` in bf16 (the adjoint of the
+             rotation, each op rounded as autograd rounds it): t1 = dtype(g cos), t2 = dtype(g sin),
+             dx[2i] = dtype(t1[2i] + t2[2i+1]), dx[2i+1] = dtype(t1[2i+1] - t2[2i]).
+``head_rmsnorm_backward``  the gradient torch's autograd gives x of ``head_rmsnorm`` (base.py:355-
+             357: two x.float() casts, each handing back a gradient of x's dtype, summed in it):
+             r = rsqrt(mean(x^2) + eps), dx = dtype(dtype(dn r) - dtype(x r^3 sum(dn x) / D)).
 
 Pinned by tests/test_oracle_block.py against torch's CPU operators on the same bf16 inputs (a
 library routine): identical except for rare last-place differences from summation order and
-the erf implementation.
+the erf implementation; the two backwards also against torch's CPU autograd of the forward
+expressions, against the adjoint identity <rope(x), g> = <x, rope_backward(g)> and against
+central finite differences of the norm in float64.
 """
 
 from __future__ import annotations
@@ -78,3 +86,26 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str = "bf16") -
     a = _round_dtype(xf * np.asarray(cos, F32), dtype)
     b = _round_dtype(rot * np.asarray(sin, F32), dtype)
     return _round_dtype(a + b, dtype)
+
+
+def rope_backward(g: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """g = d/d rope(x) [..., T, D] -> d/dx, with torch autograd's roundings (see the header)."""
+    gf = np.asarray(g, dtype=F32)
+    t1 = _round_dtype(gf * np.asarray(cos, F32), dtype)
+    t2 = _round_dtype(gf * np.asarray(sin, F32), dtype)
+    dx = np.empty_like(gf)
+    dx[..., 0::2] = t1[..., 0::2] + t2[..., 1::2]
+    dx[..., 1::2] = t1[..., 1::2] - t2[..., 0::2]
+    return _round_dtype(dx, dtype)
+
+
+def head_rmsnorm_backward(x: np.ndarray, dn: np.ndarray, eps: float = 1e-6, dtype: str = "bf16") -> np.ndarray:
+    """x [..., D] (the norm's input), dn = d/d head_rmsnorm(x) -> d/dx (see the header)."""
+    xf = np.asarray(x, dtype=F32)
+    dnf = np.asarray(dn, dtype=F32)
+    D = xf.shape[-1]
+    ms = np.mean(xf * xf, axis=-1, keepdims=True, dtype=F32)
+    r = (F32(1.0) / np.sqrt(ms + F32(eps), dtype=F32)).astype(F32)
+    sd = np.sum(dnf * xf, axis=-1, keepdims=True, dtype=F32)
+    k = (sd * (r * r * r) / F32(D)).astype(F32)
+    return _round_dtype(_round_dtype(dnf * r, dtype) - _round_dtype(xf * k, dtype), dtype)

@@ -80,7 +80,9 @@ def test_block_attention_stage_matches_oracle():
     x = torch.randn(B, T, CFG["d_model"], generator=g).to("cuda", torch.bfloat16)
     from flower_amd.kernels.fp8_swa_attention import fp8_swa_attention_forward
     with torch.no_grad():
-        q, k, v = blk.attn.qkv_heads(blk.ln1(x))      # QK-norm and RoPE in torch ops (base.py:618-639)
+        q, k, v = blk.attn.qkv_heads(blk.ln1(x))      # QK-norm and RoPE (base.py:618-639)
+        vt = torch.empty(B, T, v.shape[1], v.shape[3], dtype=v.dtype, device=v.device).transpose(1, 2)
+        v = vt.copy_(v)                                  # the head split's (B, T, H, D) layout:
         assert not v.is_contiguous()                     # read in place through its strides
         out = fp8_swa_attention_forward(q, k, v, CFG["local_window"], granularity="head")
     torch.cuda.synchronize()

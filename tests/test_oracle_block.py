@@ -102,3 +102,59 @@ def test_rope_plants_a_wrong_pair_sign_and_fails():
     wrong = (x * cos + bad_rot * sin).float().numpy()
     got = rope(x.float().numpy(), cos.float().numpy(), sin.float().numpy(), "bf16")
     assert np.array_equal(got, right) and not np.array_equal(got, wrong)
+
+
+def test_rope_and_head_rmsnorm_backward_match_torch_autograd():
+    """oracle.block.rope_backward / head_rmsnorm_backward against torch's CPU autograd of the
+    reference's expressions (base.py:355-357, :478-483) on bf16 (B, H, T, D) tensors: RoPE's
+    gradient bit for bit; the norm's within one bf16 ulp in a small fraction of values (the fp32
+    sums' order)."""
+    from oracle.block import head_rmsnorm_backward, rope_backward
+    g = torch.Generator().manual_seed(6)
+    B, H, T, D, eps = 2, 3, 80, 64, 1e-6
+    cos, sin = (t.to(torch.bfloat16) for t in _rope_tables(T, D))
+    x = (torch.randn(B, H, T, D, generator=g) * 2.0).to(torch.bfloat16).requires_grad_(True)
+    gy = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
+    n = (x.float() * x.float().pow(2).mean(dim=-1, keepdim=True).add(eps).rsqrt()).to(torch.bfloat16)
+    n.retain_grad()
+    y = n * cos + _torch_rotate_half(n) * sin
+    y.backward(gy)
+    dn = rope_backward(gy.float().numpy(), cos.float().numpy(), sin.float().numpy(), "bf16")
+    np.testing.assert_array_equal(dn.view(np.uint32), n.grad.float().numpy().view(np.uint32))
+    dx = head_rmsnorm_backward(x.detach().float().numpy(), dn, eps, "bf16")
+    d = _ulp_diff(dx, x.grad.float().numpy())
+    assert d.max() <= 1 and (d > 0).mean() < 5e-3, ((d > 0).mean(), d.max())
+
+
+def test_rope_backward_is_the_adjoint_and_norm_backward_the_derivative():
+    """Independent of torch: in float64 terms, <rope(x), g> = <x, rope_backward(g)> (the rotation's
+    adjoint; a swapped pair or sign fails it), and head_rmsnorm_backward against central finite
+    differences of head_rmsnorm computed in float64 (a dropped r^3 term or a missing 1/D fails it)."""
+    from oracle.block import head_rmsnorm_backward, rope_backward
+    rng = np.random.default_rng(7)
+    T, D = 16, 32
+    cos32, sin32 = (t.numpy() for t in _rope_tables(T, D))
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    gy = rng.standard_normal((T, D)).astype(np.float32)
+    rot = np.empty_like(x, dtype=np.float64)
+    rot[:, 0::2], rot[:, 1::2] = -x[:, 1::2], x[:, 0::2]
+    lhs = float(np.sum((x * cos32.astype(np.float64) + rot * sin32) * gy))
+    rhs = float(np.sum(x.astype(np.float64) * rope_backward(gy, cos32, sin32, "f32")))
+    assert abs(lhs - rhs) <= 1e-4 * (abs(lhs) + 1.0)
+
+    eps = 1e-6
+    xr = rng.standard_normal((4, D)).astype(np.float64) * 1.5
+    dn = rng.standard_normal((4, D))
+
+    def f(v):
+        return np.sum(dn * v / np.sqrt(np.mean(v * v, axis=-1, keepdims=True) + eps))
+    fd = np.zeros_like(xr)
+    h = 1e-6
+    for i in range(xr.shape[0]):
+        for j in range(D):
+            e = np.zeros_like(xr)
+            e[i, j] = h
+            fd[i, j] = (f(xr + e) - f(xr - e)) / (2 * h)
+    got = head_rmsnorm_backward(xr.astype(np.float32), dn.astype(np.float32), eps, "f32")
+    np.testing.assert_allclose(got, fd, rtol=2e-4, atol=2e-5)
+
