@@ -899,7 +899,8 @@ def bench_block_train(cfg, steps, warmup, recipe):
     """One training step (forward + backward, weight gradients included) of the 450M block
     (flower_amd.block.TransformerBlock, block_config()): its five Linears converted by
     convert_model_to_fp8 with ``recipe`` (None: left in bf16, torch's GEMMs), the attention on the
-    HIP bf16 sliding-window kernels, norms / RoPE / SwiGLU / residual adds in torch."""
+    HIP bf16 sliding-window kernels, RMSNorm, the head split with QK-norm + RoPE and the SwiGLU
+    product on the HIP row kernels (forward and backward), the residual adds in torch."""
     import copy
     import torch.nn as nn
     from flower_amd.block import TransformerBlock, block_config, init_block_

@@ -22,7 +22,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJDIR = os.path.join(ROOT, "_build")
 LIB = os.path.join(HERE, "libflower_amd.so")
 DIAG_LIB = os.path.join(HERE, "libflower_amd_diag.so")
-SOURCES = ["flw_error.hip", "flw_quant.hip", "flw_swa.hip", "flw_swa_bf16.hip", "flw_gemm.hip", "flw_heads.hip"]
+SOURCES = ["flw_error.hip", "flw_quant.hip", "flw_swa.hip", "flw_swa_bf16.hip", "flw_gemm.hip", "flw_heads.hip", "flw_norm_act.hip"]
 # The diagnostics library: its own source plus its own copy of the error / timing state.
 DIAG_SOURCES = ["diag/flw_diag.hip"]
 ARCH = os.environ.get("FLW_OFFLOAD_ARCH", "gfx950")

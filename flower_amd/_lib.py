@@ -63,6 +63,15 @@ SIGNATURES = {
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "flw_qkv_heads_bwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_float, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "flw_rmsnorm_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64,
+                                c_void_p]),
+    "flw_rmsnorm_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),
+    "flw_rmsnorm_bwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64,
+                                c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "flw_swiglu_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64,
+                               c_void_p]),
+    "flw_swiglu_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64,
+                               c_void_p, c_void_p, c_int64, c_void_p]),
     "flw_rmsnorm_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p,
                                             c_void_p, c_void_p, c_void_p]),
     "flw_gelu_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,

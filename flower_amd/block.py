@@ -22,8 +22,8 @@ linear's per-row e4m3 quantisation, QK-norm + RoPE and the per-head maxima in th
 epilogue (or, with ``fuse_qk_epilogue = False``, in the Q / K / V quantiser), residual adds in the
 GEMM epilogues, the attention writing its (B, T, H, D) output in place: library kernels
 only, no torch elementwise kernels);
-``forward_unfused`` is the module-by-module composition (torch norms / GELU / adds around the
-library's linears and attention). Wrap calls in ``fp8_weight_cache(block)`` to quantise the
+``forward_unfused`` is the module-by-module composition (the modules' own norms, GELU and torch
+adds around the library's linears and attention). Wrap calls in ``fp8_weight_cache(block)`` to quantise the
 weights once.
 """
 
@@ -41,13 +41,94 @@ from .kernels.fp8_swa_attention import (fp8_swa_attention_forward, fp8_swa_atten
 from .precision import Fp8Linear
 
 
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """t as a 2-D [rows, last] view with unit column stride and 16-byte aligned rows (a copy when
+    its layout has none)."""
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.stride(-1) != 1 or t2.stride(0) % 8 or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2
+
+
+class _RMSNormFn(torch.autograd.Function):
+    """RMSNorm.forward on bf16 rows as one HIP pass (flw_rmsnorm_fwd), its autograd backward as one
+    more plus the weight gradient's column sum (flw_rmsnorm_bwd), rounded as torch's autograd of the
+    expression rounds (base.py:336-338)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        lib = _lib.load()
+        x2 = _rows(x)
+        rows, cols = x2.shape
+        h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        _lib.check(lib.flw_rmsnorm_fwd(x2.data_ptr(), rows, cols, x2.stride(0), weight.data_ptr(), float(eps),
+                                       h.data_ptr(), cols, _lib.stream_of(x)), "RMSNorm")
+        ctx.save_for_backward(x2, weight)
+        ctx.eps, ctx.shape = float(eps), x.shape
+        return h
+
+    @staticmethod
+    def backward(ctx, dh):
+        x2, weight = ctx.saved_tensors
+        rows, cols = x2.shape
+        lib = _lib.load()
+        d2 = _rows(dh.to(x2.dtype))
+        dx = torch.empty((rows, cols), dtype=x2.dtype, device=x2.device)
+        dw = torch.empty((cols,), dtype=weight.dtype, device=weight.device)
+        ws = _lib.workspace(lib.flw_rmsnorm_bwd_workspace_bytes(rows, cols), x2.device)
+        _lib.check(lib.flw_rmsnorm_bwd(x2.data_ptr(), rows, cols, x2.stride(0), weight.data_ptr(), ctx.eps,
+                                       d2.data_ptr(), d2.stride(0), dx.data_ptr(), cols, dw.data_ptr(),
+                                       ws.data_ptr(), ws.numel(), _lib.stream_of(x2)), "RMSNorm backward")
+        return dx.view(ctx.shape), dw, None
+
+
+class _SwiGLUFn(torch.autograd.Function):
+    """silu(gate) * up on bf16 rows as one HIP pass each way (flw_swiglu_fwd / flw_swiglu_bwd),
+    rounded as torch's silu, product and their autograd round (base.py:540, 550)."""
+
+    @staticmethod
+    def forward(ctx, gate, up):
+        lib = _lib.load()
+        g2, u2 = _rows(gate), _rows(up)
+        rows, cols = g2.shape
+        h = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+        _lib.check(lib.flw_swiglu_fwd(g2.data_ptr(), u2.data_ptr(), rows, cols, g2.stride(0), u2.stride(0),
+                                      h.data_ptr(), cols, _lib.stream_of(gate)), "SwiGLU")
+        ctx.save_for_backward(g2, u2)
+        ctx.shape = gate.shape
+        return h
+
+    @staticmethod
+    def backward(ctx, dh):
+        g2, u2 = ctx.saved_tensors
+        rows, cols = g2.shape
+        lib = _lib.load()
+        d2 = _rows(dh.to(g2.dtype))
+        dg = torch.empty((rows, cols), dtype=g2.dtype, device=g2.device)
+        du = torch.empty((rows, cols), dtype=g2.dtype, device=g2.device)
+        _lib.check(lib.flw_swiglu_bwd(g2.data_ptr(), u2.data_ptr(), rows, cols, g2.stride(0), u2.stride(0),
+                                      d2.data_ptr(), d2.stride(0), dg.data_ptr(), du.data_ptr(), cols,
+                                      _lib.stream_of(g2)), "SwiGLU backward")
+        return dg.view(ctx.shape), du.view(ctx.shape)
+
+
+def _hip_rows_ok(*ts: torch.Tensor) -> bool:
+    """bf16 GPU tensors whose last dimension the row kernels take (a multiple of 8)."""
+    return all(t.is_cuda and t.dtype == torch.bfloat16 for t in ts) and ts[0].shape[-1] % 8 == 0
+
+
 class RMSNorm(nn.Module):
+    """base.py:324-338. bf16 on the GPU (bf16 weight, width a multiple of 8 up to 8192): the HIP
+    pass pair of ``_RMSNormFn``; otherwise the reference's torch expression."""
+
     def __init__(self, dim: int, eps: float = 1e-6) -> None:
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.shape[-1] <= 8192 and x.numel() > 0 and _hip_rows_ok(x, self.weight):
+            return _RMSNormFn.apply(x, self.weight, self.eps)
         rms = x.float().pow(2).mean(dim=-1, keepdim=True).add(self.eps).rsqrt()
         return (x.float() * rms).to(dtype=x.dtype) * self.weight
 
@@ -110,8 +191,8 @@ class Fp8DecoderBlock(nn.Module):
 
     @torch.no_grad()
     def forward_unfused(self, x: torch.Tensor) -> torch.Tensor:
-        """The reference composition, one module after the other (the attention through torch's
-        qkv_heads -- QK-norm and RoPE in torch ops -- and fp8_swa_attention_forward)."""
+        """The reference composition, one module after the other (the attention through its
+        qkv_heads -- the head split, QK-norm and RoPE -- and fp8_swa_attention_forward)."""
         x = x + self.attn.forward_unfused(self.ln1(x))
         return x + self.ff(self.ln2(x))
 
@@ -294,7 +375,10 @@ class FeedForward(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.activation == "gelu":
             return self.net(x)
-        return self.down(torch.nn.functional.silu(self.gate(x)) * self.up(x))
+        gate, up = self.gate(x), self.up(x)
+        if gate.numel() > 0 and _hip_rows_ok(gate, up):
+            return self.down(_SwiGLUFn.apply(gate, up))
+        return self.down(torch.nn.functional.silu(gate) * up)
 
 
 class TransformerBlock(nn.Module):

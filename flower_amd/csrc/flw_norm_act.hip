@@ -1,0 +1,410 @@
+// The block's RMSNorm (flower/models/base.py:324-338) and the SwiGLU product of its FeedForward
+// (base.py:535-551 with smooth_swiglu off: act = silu(gate), down(act * up)) for training on bf16
+// activations, forward and backward, each one memory-bound pass over the rows (plus a small column
+// reduction for the norm's weight gradient), with the roundings of the reference's torch
+// expressions under eager autograd:
+//   RMSNorm forward:  r = 1 / sqrt(mean(x^2) + eps) in fp32, n = bf16(x r), h = bf16(n w);
+//   RMSNorm backward: dn = bf16(dh w); dw = bf16(sum over rows of bf16(dh n)), the sum in fp32;
+//     dx = bf16(bf16(dn r) - bf16(x r^3 sum(dn x) / cols)) -- x.float() appears twice in the
+//     expression, and each cast hands back its own bf16 gradient, summed in bf16;
+//   SwiGLU forward:   s = bf16(g / (1 + exp(-g))), h = bf16(s u);
+//   SwiGLU backward:  ds = bf16(dh u), du = bf16(dh s), sig = 1 / (1 + exp(-g)),
+//     dg = bf16(ds sig (1 + g (1 - sig))) (torch's silu backward).
+// NaN results are written as the quiet 0x7FC0 that torch's bf16 rounding gives.
+//
+// Row kernels: a workgroup of 4 waves, one row per wave at a time; a lane holds chunks of 8 values
+// (16 bytes) v = lane + 64 i, i < NV, so a row of up to 512 NV values stays in registers; the row's
+// sums are wave butterflies. The backward's waves walk rows with a grid stride and keep their
+// columns' dw partial sums in registers; a workgroup folds its 4 waves' partials through LDS into
+// one row of a [blocks, cols] fp32 workspace, which rmsnorm_dw_kernel sums per column.
+
+#include "flw_common.h"
+
+namespace flw {
+
+constexpr int kNormBlocks = 512;   // backward workgroups: rows of the dw partial workspace
+
+__device__ __forceinline__ float norm_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// a, b rounded to bf16 (kept as fp32) by one pair conversion (nearest even; a NaN stays a NaN).
+__device__ __forceinline__ void round2_bf16(float& a, float& b) {
+  const uint32_t t = bf16x2_rne_raw(a, b);
+  a = __uint_as_float(t << 16);
+  b = __uint_as_float(t & 0xFFFF0000u);
+}
+
+__device__ __forceinline__ uint4 pack_bf16x8(const float* f) {
+  return make_uint4(bf16x2_canon_nan(bf16x2_rne_raw(f[0], f[1])), bf16x2_canon_nan(bf16x2_rne_raw(f[2], f[3])),
+                    bf16x2_canon_nan(bf16x2_rne_raw(f[4], f[5])), bf16x2_canon_nan(bf16x2_rne_raw(f[6], f[7])));
+}
+
+// The row's 1 / sqrt(mean(x^2) + eps): an fma chain over the lane's values, the wave butterfly,
+// a division by cols, IEEE sqrt and division. Chunks past the row end hold zeros.
+template <int NV>
+__device__ __forceinline__ float row_rstd(const uint4* xb, int cols, float eps) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float f[8];
+    Vec16<uint16_t>::unpack(xb[i], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+  }
+  const float ms = norm_wave_sum(ss) / (float)cols;
+  return 1.0f / __builtin_sqrtf(ms + eps);
+}
+
+template <int NV>
+__device__ __forceinline__ void load_row(const uint16_t* src, int nvec, int lane, uint4* out) {
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    out[i] = v < nvec ? *reinterpret_cast<const uint4*>(src + 8 * v) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __restrict__ x, int64_t rows, int cols,
+                                                          int64_t xs, const uint16_t* __restrict__ w, float eps,
+                                                          uint16_t* __restrict__ h, int64_t hs) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;                        // wave-uniform
+  const int lane = threadIdx.x & 63, nvec = cols >> 3;
+  uint4 xb[NV];
+  load_row<NV>(x + row * xs, nvec, lane, xb);
+  const float r = row_rstd<NV>(xb, cols, eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v >= nvec) continue;
+    float f[8], g[8], o[8];
+    Vec16<uint16_t>::unpack(xb[i], f);
+    Vec16<uint16_t>::load(w + 8 * v, g);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+#pragma clang fp contract(off)
+      float n0 = f[e] * r, n1 = f[e + 1] * r;
+      round2_bf16(n0, n1);
+      o[e] = n0 * g[e];
+      o[e + 1] = n1 * g[e + 1];
+    }
+    *reinterpret_cast<uint4*>(h + row * hs + 8 * v) = pack_bf16x8(o);
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint16_t* __restrict__ x, int64_t rows, int cols,
+                                                          int64_t xs, const uint16_t* __restrict__ w, float eps,
+                                                          const uint16_t* __restrict__ dh, int64_t dhs,
+                                                          uint16_t* __restrict__ dx, int64_t dxs,
+                                                          float* __restrict__ part) {
+  extern __shared__ float fold[];                 // [cols]: one wave's partials at a time
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nvec = cols >> 3;
+  float acc[NV][8];
+  uint4 wb[NV];
+  load_row<NV>(w, nvec, lane, wb);
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[i][e] = 0.0f;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < rows; row += (int64_t)gridDim.x * 4) {
+    uint4 xb[NV], gb[NV];
+    load_row<NV>(x + row * xs, nvec, lane, xb);
+    load_row<NV>(dh + row * dhs, nvec, lane, gb);
+    const float r = row_rstd<NV>(xb, cols, eps);
+    uint32_t dn[NV][4];                           // bf16(dh w), packed as pairs
+    float sd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float f[8], g[8], wf[8];
+      Vec16<uint16_t>::unpack(xb[i], f);
+      Vec16<uint16_t>::unpack(gb[i], g);
+      Vec16<uint16_t>::unpack(wb[i], wf);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+#pragma clang fp contract(off)
+        float n0 = f[e] * r, n1 = f[e + 1] * r;
+        round2_bf16(n0, n1);
+        float d0 = g[e] * wf[e], d1 = g[e + 1] * wf[e + 1];
+        round2_bf16(d0, d1);
+        float p0 = g[e] * n0, p1 = g[e + 1] * n1;
+        round2_bf16(p0, p1);
+        dn[i][e >> 1] = (__float_as_uint(d0) >> 16) | (__float_as_uint(d1) & 0xFFFF0000u);
+        acc[i][e] += p0;
+        acc[i][e + 1] += p1;
+        sd = fmaf(d0, f[e], sd);
+        sd = fmaf(d1, f[e + 1], sd);
+      }
+    }
+    sd = norm_wave_sum(sd);
+    const float k = sd * (r * r * r) / (float)cols;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int v = lane + 64 * i;
+      if (v >= nvec) continue;
+      float f[8], o[8];
+      Vec16<uint16_t>::unpack(xb[i], f);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+#pragma clang fp contract(off)
+        float a0 = __uint_as_float(dn[i][e >> 1] << 16) * r;
+        float a1 = __uint_as_float(dn[i][e >> 1] & 0xFFFF0000u) * r;
+        float b0 = f[e] * k, b1 = f[e + 1] * k;
+        round2_bf16(a0, a1);
+        round2_bf16(b0, b1);
+        o[e] = a0 - b0;
+        o[e + 1] = a1 - b1;
+      }
+      *reinterpret_cast<uint4*>(dx + row * dxs + 8 * v) = pack_bf16x8(o);
+    }
+  }
+  // Fold the 4 waves' column partials into part[blockIdx.x] in a fixed order (wave 0 + 1 + 2 + 3):
+  // waves 1, 2, 3 in turn hand theirs to wave 0 through one row of LDS.
+  for (int q = 1; q < 4; ++q) {
+    if (wave == q) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int v = lane + 64 * i;
+        if (v >= nvec) continue;
+        float4* dst = reinterpret_cast<float4*>(fold + 8 * v);
+        dst[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+        dst[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int v = lane + 64 * i;
+        if (v >= nvec) continue;
+        const float4* src = reinterpret_cast<const float4*>(fold + 8 * v);
+        const float4 a = src[0], b = src[1];
+        acc[i][0] += a.x; acc[i][1] += a.y; acc[i][2] += a.z; acc[i][3] += a.w;
+        acc[i][4] += b.x; acc[i][5] += b.y; acc[i][6] += b.z; acc[i][7] += b.w;
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int v = lane + 64 * i;
+      if (v >= nvec) continue;
+      float4* dst = reinterpret_cast<float4*>(part + (int64_t)blockIdx.x * cols + 8 * v);
+      dst[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+      dst[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+    }
+  }
+}
+
+// dw[c] = bf16(sum over the nblk partial rows of part[., c]): 16 columns per workgroup, 16 slices
+// of the rows each, folded through LDS in a fixed order.
+__global__ __launch_bounds__(256) void rmsnorm_dw_kernel(const float* __restrict__ part, int nblk, int cols,
+                                                         uint16_t* __restrict__ dw) {
+  __shared__ float red[16][17];
+  const int cl = threadIdx.x & 15, s = threadIdx.x >> 4;
+  const int c = blockIdx.x * 16 + cl;
+  float a = 0.0f;
+  if (c < cols) {
+#pragma unroll 8
+    for (int b = s; b < nblk; b += 16) a += part[(int64_t)b * cols + c];
+  }
+  red[s][cl] = a;
+  __syncthreads();
+  if (s == 0 && c < cols) {
+    float t = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) t += red[j][cl];
+    dw[c] = (uint16_t)f32_to_bf16_bits(t);
+  }
+}
+
+struct SwigluParams {
+  const uint16_t* g;
+  const uint16_t* u;
+  const uint16_t* dh;           // backward
+  uint16_t* out0;               // forward h; backward dgate
+  uint16_t* out1;               // backward dup
+  int64_t gs, us, dhs, os;
+  int cpr;                      // 16-byte chunks per row
+  int total;                    // rows * cpr
+};
+
+// One 16-byte chunk (8 values) of a row per thread, chunk index i -> (row i / cpr, chunk i % cpr).
+__global__ __launch_bounds__(256) void swiglu_fwd_kernel(SwigluParams p) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.total) return;
+  const int64_t m = i / p.cpr;
+  const int c = 8 * (i - (int)m * p.cpr);
+  float g[8], u[8], o[8];
+  Vec16<uint16_t>::load(p.g + m * p.gs + c, g);
+  Vec16<uint16_t>::load(p.u + m * p.us + c, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = round_bf16(g[e] / (1.0f + expf(-g[e]))) * u[e];
+  *reinterpret_cast<uint4*>(p.out0 + m * p.os + c) = pack_bf16x8(o);
+}
+
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(SwigluParams p) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.total) return;
+  const int64_t m = i / p.cpr;
+  const int c = 8 * (i - (int)m * p.cpr);
+  float g[8], u[8], d[8], dg[8], du[8];
+  Vec16<uint16_t>::load(p.g + m * p.gs + c, g);
+  Vec16<uint16_t>::load(p.u + m * p.us + c, u);
+  Vec16<uint16_t>::load(p.dh + m * p.dhs + c, d);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float den = 1.0f + expf(-g[e]);       // silu's and sigmoid's 1 + exp(-g), one exp
+    const float s = round_bf16(g[e] / den);
+    const float ds = round_bf16(d[e] * u[e]);
+    du[e] = d[e] * s;
+    const float sig = 1.0f / den;
+    dg[e] = ds * sig * (1.0f + g[e] * (1.0f - sig));
+  }
+  *reinterpret_cast<uint4*>(p.out0 + m * p.os + c) = pack_bf16x8(dg);
+  *reinterpret_cast<uint4*>(p.out1 + m * p.os + c) = pack_bf16x8(du);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+static int norm_nv(int64_t cols) {
+  const int64_t need = (cols / 8 + 63) / 64;
+  for (int nv : {1, 2, 3, 4, 6, 8, 12, 16})
+    if (need <= nv) return nv;
+  return 0;
+}
+
+#define FLW_NORM_KERNELS(K) \
+  {reinterpret_cast<const void*>(&K<1>), reinterpret_cast<const void*>(&K<2>), reinterpret_cast<const void*>(&K<3>), \
+   reinterpret_cast<const void*>(&K<4>), reinterpret_cast<const void*>(&K<6>), reinterpret_cast<const void*>(&K<8>), \
+   reinterpret_cast<const void*>(&K<12>), reinterpret_cast<const void*>(&K<16>)}
+
+static const void* pick_nv(const void* const* table, int nv) {
+  switch (nv) {
+    case 1: return table[0];
+    case 2: return table[1];
+    case 3: return table[2];
+    case 4: return table[3];
+    case 6: return table[4];
+    case 8: return table[5];
+    case 12: return table[6];
+    default: return table[7];
+  }
+}
+
+static int norm_check(const void* x, int64_t rows, int64_t cols, int64_t xs, const void* w, float eps) {
+  FLW_REQUIRE(x != nullptr && w != nullptr, FLW_E_INVALID, "null pointer");
+  FLW_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0, FLW_E_INVALID, "cols must be a positive multiple of 8");
+  FLW_REQUIRE(cols <= 8192, FLW_E_UNSUPPORTED, "cols must be <= 8192, got %lld", (long long)cols);
+  FLW_REQUIRE(xs >= cols && xs % 8 == 0 && aligned16(x) && aligned16(w), FLW_E_INVALID,
+              "rows must be 16-byte aligned with a stride >= cols");
+  FLW_REQUIRE(eps >= 0.0f, FLW_E_INVALID, "eps must be non-negative");
+  FLW_REQUIRE(rows <= 0x7FFFFFFFll * 4, FLW_E_UNSUPPORTED, "too many rows");
+  return FLW_OK;
+}
+
+static int swiglu_check(const void* g, const void* u, int64_t rows, int64_t cols, int64_t gs, int64_t us) {
+  FLW_REQUIRE(g != nullptr && u != nullptr, FLW_E_INVALID, "null pointer");
+  FLW_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0, FLW_E_INVALID, "cols must be a positive multiple of 8");
+  FLW_REQUIRE(gs >= cols && us >= cols && gs % 8 == 0 && us % 8 == 0 && aligned16(g) && aligned16(u),
+              FLW_E_INVALID, "rows must be 16-byte aligned with a stride >= cols");
+  FLW_REQUIRE(rows * (cols / 8) <= 0x7FFFFFFFll - 255, FLW_E_UNSUPPORTED, "too many elements");
+  return FLW_OK;
+}
+
+}  // namespace flw
+
+using namespace flw;
+
+extern "C" int flw_rmsnorm_fwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, const void* weight,
+                               float eps, void* h, int64_t h_row_stride, void* stream) {
+  int rc = norm_check(x, rows, cols, x_row_stride, weight, eps);
+  if (rc) return rc;
+  FLW_REQUIRE(h != nullptr && aligned16(h) && h_row_stride >= cols && h_row_stride % 8 == 0, FLW_E_INVALID,
+              "h must be 16-byte aligned rows with a stride >= cols");
+  if (rows == 0) return FLW_OK;
+  static const void* const table[] = FLW_NORM_KERNELS(rmsnorm_fwd_kernel);
+  const Timer tm = take_timer();
+  (void)launch_args(pick_nv(table, norm_nv(cols)), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                    static_cast<hipStream_t>(stream), tm.start, tm.stop, static_cast<const uint16_t*>(x), rows,
+                    (int)cols, x_row_stride, static_cast<const uint16_t*>(weight), eps, static_cast<uint16_t*>(h),
+                    h_row_stride);
+  return check_launch("flw_rmsnorm_fwd");
+}
+
+extern "C" size_t flw_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
+  const int64_t nblk = rows <= 0 ? 0 : std::min<int64_t>((rows + 3) / 4, kNormBlocks);
+  return (size_t)(nblk * (cols > 0 ? cols : 0) * 4);
+}
+
+extern "C" int flw_rmsnorm_bwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, const void* weight,
+                               float eps, const void* dh, int64_t dh_row_stride, void* dx, int64_t dx_row_stride,
+                               void* dweight, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = norm_check(x, rows, cols, x_row_stride, weight, eps);
+  if (rc) return rc;
+  FLW_REQUIRE(dh != nullptr && dx != nullptr && dweight != nullptr && aligned16(dh) && aligned16(dx),
+              FLW_E_INVALID, "dh, dx must be 16-byte aligned and dweight non-null");
+  FLW_REQUIRE(dh_row_stride >= cols && dh_row_stride % 8 == 0 && dx_row_stride >= cols && dx_row_stride % 8 == 0,
+              FLW_E_INVALID, "gradient rows need a stride >= cols, a multiple of 8");
+  const size_t need = flw_rmsnorm_bwd_workspace_bytes(rows, cols);
+  FLW_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace != nullptr && aligned16(workspace))),
+              FLW_E_INVALID, "workspace needs %zu bytes (16-byte aligned), got %zu", need, workspace_bytes);
+  const int nblk = (int)std::min<int64_t>((rows + 3) / 4, kNormBlocks);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const Timer tm = take_timer();
+  float* part = static_cast<float*>(workspace);
+  if (nblk > 0) {
+    static const void* const table[] = FLW_NORM_KERNELS(rmsnorm_bwd_kernel);
+    (void)launch_args(pick_nv(table, norm_nv(cols)), dim3((unsigned)nblk), dim3(256), (size_t)(cols * 4), s,
+                      tm.start, nullptr, static_cast<const uint16_t*>(x), rows, (int)cols, x_row_stride,
+                      static_cast<const uint16_t*>(weight), eps, static_cast<const uint16_t*>(dh), dh_row_stride,
+                      static_cast<uint16_t*>(dx), dx_row_stride, part);
+  }
+  (void)launch_args(reinterpret_cast<const void*>(&rmsnorm_dw_kernel), dim3((unsigned)((cols + 15) / 16)),
+                    dim3(256), 0, s, nblk > 0 ? nullptr : tm.start, tm.stop, static_cast<const float*>(part), nblk,
+                    (int)cols, static_cast<uint16_t*>(dweight));
+  return check_launch("flw_rmsnorm_bwd");
+}
+
+extern "C" int flw_swiglu_fwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
+                              int64_t up_row_stride, void* h, int64_t h_row_stride, void* stream) {
+  int rc = swiglu_check(gate, up, rows, cols, gate_row_stride, up_row_stride);
+  if (rc) return rc;
+  FLW_REQUIRE(h != nullptr && aligned16(h) && h_row_stride >= cols && h_row_stride % 8 == 0, FLW_E_INVALID,
+              "h must be 16-byte aligned rows with a stride >= cols");
+  if (rows == 0) return FLW_OK;
+  SwigluParams p{};
+  p.g = static_cast<const uint16_t*>(gate); p.u = static_cast<const uint16_t*>(up);
+  p.out0 = static_cast<uint16_t*>(h);
+  p.gs = gate_row_stride; p.us = up_row_stride; p.os = h_row_stride;
+  p.cpr = (int)(cols / 8); p.total = (int)(rows * p.cpr);
+  (void)launch_timed(reinterpret_cast<const void*>(&swiglu_fwd_kernel), dim3((unsigned)((p.total + 255) / 256)),
+                     dim3(256), static_cast<hipStream_t>(stream), p);
+  return check_launch("flw_swiglu_fwd");
+}
+
+extern "C" int flw_swiglu_bwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
+                              int64_t up_row_stride, const void* dh, int64_t dh_row_stride, void* dgate, void* dup,
+                              int64_t grad_row_stride, void* stream) {
+  int rc = swiglu_check(gate, up, rows, cols, gate_row_stride, up_row_stride);
+  if (rc) return rc;
+  FLW_REQUIRE(dh != nullptr && dgate != nullptr && dup != nullptr && aligned16(dh) && aligned16(dgate) &&
+              aligned16(dup), FLW_E_INVALID, "dh, dgate, dup must be non-null and 16-byte aligned");
+  FLW_REQUIRE(dh_row_stride >= cols && dh_row_stride % 8 == 0 && grad_row_stride >= cols && grad_row_stride % 8 == 0,
+              FLW_E_INVALID, "gradient rows need a stride >= cols, a multiple of 8");
+  if (rows == 0) return FLW_OK;
+  SwigluParams p{};
+  p.g = static_cast<const uint16_t*>(gate); p.u = static_cast<const uint16_t*>(up);
+  p.dh = static_cast<const uint16_t*>(dh);
+  p.out0 = static_cast<uint16_t*>(dgate); p.out1 = static_cast<uint16_t*>(dup);
+  p.gs = gate_row_stride; p.us = up_row_stride; p.dhs = dh_row_stride; p.os = grad_row_stride;
+  p.cpr = (int)(cols / 8); p.total = (int)(rows * p.cpr);
+  (void)launch_timed(reinterpret_cast<const void*>(&swiglu_bwd_kernel), dim3((unsigned)((p.total + 255) / 256)),
+                     dim3(256), static_cast<hipStream_t>(stream), p);
+  return check_launch("flw_swiglu_bwd");
+}

@@ -161,10 +161,44 @@ int flw_qkv_heads_fwd(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t 
  * bf16. RoPE backward with torch's bf16 roundings (t1 = bf16(g cos), t2 = bf16(g sin),
  * dn[2i] = bf16(t1[2i] + t2[2i+1]), dn[2i+1] = bf16(t1[2i+1] - t2[2i])), then the HeadRMSNorm
  * backward in fp32 from the forward's input x (r = rsqrt(mean(x^2) + eps),
- * dx = bf16(dn r - x r^3 sum(dn x) / D)); dv copied into the v columns. */
+ * dx = bf16(bf16(dn r) - bf16(x r^3 sum(dn x) / D)), the two casts' gradients summed in bf16 as
+ * autograd sums them); dv copied into the v columns. */
 int flw_qkv_heads_bwd(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t D, int64_t qkv_row_stride,
                       int qk_norm, float eps, const void* rope_cos, const void* rope_sin, const void* dq,
                       const void* dk, const void* dv, void* dqkv, int64_t dqkv_row_stride, void* stream);
+
+/* RMSNorm forward for training, replacing RMSNorm.forward (flower/models/base.py:336-338) on bf16
+ * rows: x [rows, cols] (row stride x_row_stride), bf16 weight [cols] -> h [rows, cols]
+ * (h_row_stride), r = 1 / sqrt(mean(x^2) + eps) in fp32, h = bf16(bf16(x r) w). cols a multiple of
+ * 8, at most 8192; 16-byte aligned rows. */
+int flw_rmsnorm_fwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, const void* weight, float eps,
+                    void* h, int64_t h_row_stride, void* stream);
+
+/* Bytes of fp32 workspace flw_rmsnorm_bwd needs for its weight-gradient partial sums. */
+size_t flw_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
+
+/* The backward of flw_rmsnorm_fwd as torch's autograd of base.py:337-338 computes it, from the
+ * forward's x and weight and the gradient dh: dn = bf16(dh w),
+ * dx = bf16(bf16(dn r) - bf16(x r^3 sum(dn x) / cols)) (the expression's two x.float() casts each
+ * return a bf16 gradient, summed in bf16), dweight [cols] = bf16(sum over rows of bf16(dh n)),
+ * n = bf16(x r), the sum in fp32 (over a fixed order: deterministic). Two launches; the workspace
+ * holds partial sums only. */
+int flw_rmsnorm_bwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, const void* weight, float eps,
+                    const void* dh, int64_t dh_row_stride, void* dx, int64_t dx_row_stride, void* dweight,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* The SwiGLU product of FeedForward.forward (flower/models/base.py:538-550, smooth_swiglu off) on
+ * bf16 rows: h = bf16(bf16(silu(gate)) up), silu(g) = g / (1 + exp(-g)) in fp32 (torch's silu).
+ * gate, up, h [rows, cols] with their own row strides; cols a multiple of 8. */
+int flw_swiglu_fwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
+                   int64_t up_row_stride, void* h, int64_t h_row_stride, void* stream);
+
+/* The backward of flw_swiglu_fwd as torch's autograd computes it: ds = bf16(dh up),
+ * dup = bf16(dh s) with s = bf16(silu(gate)), dgate = bf16(ds sig (1 + g (1 - sig))),
+ * sig = 1 / (1 + exp(-g)) (torch's silu backward). dgate and dup share grad_row_stride. */
+int flw_swiglu_bwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
+                   int64_t up_row_stride, const void* dh, int64_t dh_row_stride, void* dgate, void* dup,
+                   int64_t grad_row_stride, void* stream);
 
 /* flw_quant_qkv_e4m3 without a workspace: no counterpart in the reference. For callers that
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid

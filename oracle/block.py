@@ -4,6 +4,15 @@
              h = bf16( bf16( x * rsqrt(mean(x^2) + eps) ) * w )
              (fp32 mean of squares and rsqrt, the product rounded to bf16, then the bf16 gain
              multiplied in fp32 and rounded to bf16 again, as torch does for bf16 tensors).
+``rmsnorm_backward``  the gradients torch's autograd gives x and the gain of ``rmsnorm`` (two
+             x.float() casts, each handing back a bf16 gradient, summed in bf16):
+             dn = bf16(dh w), dx = bf16(bf16(dn r) - bf16(x r^3 sum(dn x) / d)),
+             dw = bf16(sum over rows of bf16(dh n)), n = bf16(x r), the sum in fp32.
+``swiglu``, ``swiglu_backward``  FeedForward's SwiGLU product (base.py:538-550, smooth_swiglu
+             off) on bf16 values: s = bf16(g / (1 + exp(-g))), h = bf16(s u); backward
+             ds = bf16(dh u), du = bf16(dh s), sig = 1 / (1 + exp(-g)),
+             dg = bf16(ds sig (1 + g (1 - sig))) (torch's silu backward), fp32 maths with exp
+             correctly rounded to fp32.
 ``gelu``     torch.nn.functional.gelu(approximate="none") on bf16 values:
              bf16( (0.5 x) * (1 + erf(x / sqrt 2)) ), evaluated in fp32 in that order with a
              correctly rounded erf.
@@ -22,9 +31,9 @@
 
 Pinned by tests/test_oracle_block.py against torch's CPU operators on the same bf16 inputs (a
 library routine): identical except for rare last-place differences from summation order and
-the erf implementation; the two backwards also against torch's CPU autograd of the forward
+the erf implementation; the backwards also against torch's CPU autograd of the forward
 expressions, against the adjoint identity <rope(x), g> = <x, rope_backward(g)> and against
-central finite differences of the norm in float64.
+central finite differences in float64.
 """
 
 from __future__ import annotations
@@ -45,6 +54,50 @@ def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     r = (F32(1.0) / np.sqrt(ms + F32(eps), dtype=F32)).astype(F32)
     h = round_bf16((xf * r).astype(F32))
     return round_bf16((h * np.asarray(weight, dtype=F32)).astype(F32))
+
+
+def rmsnorm_backward(x: np.ndarray, weight: np.ndarray, dh: np.ndarray, eps: float = 1e-6):
+    """x [rows, d], weight [d], dh = d/d rmsnorm(x) [rows, d] (bf16 values as fp32) -> (dx, dw)."""
+    xf = np.asarray(x, dtype=F32)
+    w = np.asarray(weight, dtype=F32)
+    g = np.asarray(dh, dtype=F32)
+    d = xf.shape[-1]
+    ms = np.mean(xf * xf, axis=-1, keepdims=True, dtype=F32)
+    r = (F32(1.0) / np.sqrt(ms + F32(eps), dtype=F32)).astype(F32)
+    n = round_bf16((xf * r).astype(F32))
+    dn = round_bf16((g * w).astype(F32))
+    dw = round_bf16(np.sum(round_bf16((g * n).astype(F32)).astype(np.float64), axis=0).astype(F32))
+    sd = np.sum(dn * xf, axis=-1, keepdims=True, dtype=F32)
+    k = (sd * (r * r * r) / F32(d)).astype(F32)
+    dx = round_bf16((round_bf16((dn * r).astype(F32)) - round_bf16((xf * k).astype(F32))).astype(F32))
+    return dx, dw
+
+
+def _exp_f32(x: np.ndarray) -> np.ndarray:
+    """exp of fp32 values, correctly rounded to fp32 (via float64)."""
+    return np.exp(np.asarray(x, dtype=np.float64)).astype(F32)
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """bf16 values in and out (as fp32): bf16(bf16(silu(gate)) up)."""
+    g = np.asarray(gate, dtype=F32)
+    s = round_bf16((g / (F32(1.0) + _exp_f32(-g))).astype(F32))
+    return round_bf16((s * np.asarray(up, dtype=F32)).astype(F32))
+
+
+def swiglu_backward(gate: np.ndarray, up: np.ndarray, dh: np.ndarray):
+    """bf16 values in and out (as fp32): (dgate, dup) of swiglu for the gradient dh."""
+    g = np.asarray(gate, dtype=F32)
+    u = np.asarray(up, dtype=F32)
+    d = np.asarray(dh, dtype=F32)
+    den = (F32(1.0) + _exp_f32(-g)).astype(F32)
+    s = round_bf16((g / den).astype(F32))
+    ds = round_bf16((d * u).astype(F32))
+    du = round_bf16((d * s).astype(F32))
+    sig = (F32(1.0) / den).astype(F32)
+    inner = (F32(1.0) + (g * (F32(1.0) - sig)).astype(F32)).astype(F32)
+    dg = round_bf16(((ds * sig).astype(F32) * inner).astype(F32))
+    return dg, du
 
 
 _erf = np.vectorize(math.erf, otypes=[np.float64])

@@ -270,3 +270,39 @@ def test_lse_forward_and_dequantiser_refusals_on_the_host():
     assert rc == 1 and b"empty" in lib.flw_last_error()
     rc = lib.flw_dequant_e4m3(P, L.LAYOUT_BHTD, 1, 1, 64, 64, P, L.SCALE_HEAD, P + 8, L.BF16, None)
     assert rc == 1 and b"aligned" in lib.flw_last_error()
+
+
+@fake_pointers
+def test_training_row_kernel_refusals_on_the_host():
+    """qkv_heads, RMSNorm and SwiGLU training passes: unsupported widths, misaligned or short rows
+    and an undersized workspace are refused before any launch (fake aligned pointers)."""
+    from flower_amd import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("libflower_amd.so not built")
+    lib = L.load()
+    P = 1 << 20
+    rc = lib.flw_qkv_heads_fwd(P, 1, 16, 2, 48, 288, 1, 1e-6, P, P, P, P, P, None)
+    assert rc == 2 and b"head_dim" in lib.flw_last_error()
+    rc = lib.flw_qkv_heads_fwd(P, 1, 16, 2, 64, 320, 1, 1e-6, P, P, P, P, P, None)
+    assert rc == 1 and b"3 H D" in lib.flw_last_error()
+    rc = lib.flw_qkv_heads_bwd(P, 1, 16, 2, 64, 384, 1, 1e-6, P, P, P, P, P, P + 8, 384, None)
+    assert rc == 1 and b"aligned" in lib.flw_last_error()
+    rc = lib.flw_rmsnorm_fwd(P, 4, 12, 16, P, 1e-6, P, 16, None)
+    assert rc == 1 and b"multiple of 8" in lib.flw_last_error()
+    rc = lib.flw_rmsnorm_fwd(P, 4, 8200, 8200, P, 1e-6, P, 8200, None)
+    assert rc == 2 and b"8192" in lib.flw_last_error()
+    rc = lib.flw_rmsnorm_fwd(P, 4, 64, 32, P, 1e-6, P, 64, None)
+    assert rc == 1 and b"stride" in lib.flw_last_error()
+    rc = lib.flw_rmsnorm_fwd(P, 4, 64, 64, P, -1.0, P, 64, None)
+    assert rc == 1 and b"eps" in lib.flw_last_error()
+    need = lib.flw_rmsnorm_bwd_workspace_bytes(1021, 1280)            # a workgroup per 4 rows
+    assert need == 256 * 1280 * 4 and lib.flw_rmsnorm_bwd_workspace_bytes(0, 1280) == 0
+    assert lib.flw_rmsnorm_bwd_workspace_bytes(1 << 20, 1280) == 512 * 1280 * 4   # at most 512
+    rc = lib.flw_rmsnorm_bwd(P, 1021, 1280, 1280, P, 1e-6, P, 1280, P, 1280, P, P, need - 16, None)
+    assert rc == 1 and b"workspace" in lib.flw_last_error()
+    rc = lib.flw_swiglu_fwd(P, P, 4, 20, 24, 24, P, 24, None)
+    assert rc == 1 and b"multiple of 8" in lib.flw_last_error()
+    rc = lib.flw_swiglu_bwd(P, P, 4, 64, 64, 64, P, 64, P, P + 4, 64, None)
+    assert rc == 1 and b"aligned" in lib.flw_last_error()
+    rc = lib.flw_swiglu_fwd(P, P, 1 << 28, 128, 128, 128, P, 128, None)
+    assert rc == 2 and b"too many" in lib.flw_last_error()

@@ -1,0 +1,130 @@
+"""GPU: the training block's RMSNorm (flower/models/base.py:324-338) and SwiGLU product
+(base.py:538-550) passes, forward and backward (flw_rmsnorm_fwd / _bwd, flw_swiglu_fwd / _bwd),
+through the modules' autograd routes (flower_amd.block._RMSNormFn, _SwiGLUFn) and the C ABI.
+
+Gates (written here), against the oracle (oracle/block.py: the torch expressions' roundings):
+  - RMSNorm h and dx: < 0.5 % of values differ after the norm's fp32 sums (their order differs):
+    h's by <= 2 bf16 ulps (a one-ulp flip of bf16(x r) becomes up to two after the gain's product
+    is rounded again), dx's by <= 2^-7 |ref| + 2^-12 max|ref| of its row, since its difference of
+    two rounded terms can cancel; dw (a sum over every row): within 2 bf16 ulps;
+  - SwiGLU h, dgate, dup: < 0.5 % differ, each by one ulp (the device exp against a correctly
+    rounded one), dgate's with the same cancellation allowance;
+  - both against torch's bf16 autograd of the reference's expressions on the GPU: the same gates;
+  - empty rows: dw is zero, nothing else written.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import to_np
+from oracle.block import rmsnorm, rmsnorm_backward, swiglu, swiglu_backward
+from oracle.e4m3 import f32_to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+def _ulps(a, b):
+    ia = f32_to_bf16_bits(np.asarray(a, np.float32)).astype(np.int64)
+    ib = f32_to_bf16_bits(np.asarray(b, np.float32)).astype(np.int64)
+    return np.abs(ia - ib)
+
+
+def _close(got, ref, frac=5e-3, cancel=False, ulps=1):
+    got, ref = np.asarray(got, np.float32), np.asarray(ref, np.float32)
+    d = _ulps(got, ref)
+    assert (d > 0).mean() < frac, (d > 0).mean()
+    if cancel:
+        row = np.abs(ref).max(axis=-1, keepdims=True)
+        err = np.abs(got.astype(np.float64) - ref)
+        assert (err <= 2.0 ** -7 * np.abs(ref) + 2.0 ** -12 * row).all(), float(err.max())
+    else:
+        assert d.max() <= ulps, int(d.max())
+
+
+def _norm_inputs(rows, cols, seed, pad=0):
+    g = torch.Generator().manual_seed(seed)
+    base = (torch.randn(rows, cols + pad, generator=g) * 2.0).to("cuda", torch.bfloat16)
+    x = base[:, :cols]
+    w = (1.0 + 0.2 * torch.randn(cols, generator=g)).to("cuda", torch.bfloat16)
+    dh = torch.randn(rows, cols, generator=g).to("cuda", torch.bfloat16)
+    return x, w, dh
+
+
+def _fused_norm(x, w, dh):
+    from flower_amd.block import _RMSNormFn
+    xx = x.detach().requires_grad_(True)
+    ww = w.detach().requires_grad_(True)
+    h = _RMSNormFn.apply(xx, ww, EPS)
+    h.backward(dh)
+    return h.detach(), xx.grad, ww.grad
+
+
+NORM_CASES = [(513, 1280, 0), (300, 64, 0), (129, 1288, 16), (77, 4096, 0), (33, 8192, 0), (5, 520, 8)]
+
+
+@pytest.mark.parametrize("rows,cols,pad", NORM_CASES)
+def test_rmsnorm_forward_backward_against_oracle(rows, cols, pad):
+    x, w, dh = _norm_inputs(rows, cols, seed=rows + cols, pad=pad)
+    h, dx, dw = _fused_norm(x, w, dh)
+    xn, wn, dn = to_np(x), to_np(w), to_np(dh)
+    _close(to_np(h), rmsnorm(xn, wn, EPS), ulps=2)
+    rdx, rdw = rmsnorm_backward(xn, wn, dn, EPS)
+    _close(to_np(dx), rdx, cancel=True)
+    assert _ulps(to_np(dw), rdw).max() <= 2
+
+
+def test_rmsnorm_against_torch_autograd():
+    x, w, dh = _norm_inputs(1024, 1280, seed=3)
+    h, dx, dw = _fused_norm(x, w, dh)
+    xx = x.detach().requires_grad_(True)
+    ww = w.detach().requires_grad_(True)
+    rms = xx.float().pow(2).mean(dim=-1, keepdim=True).add(EPS).rsqrt()      # base.py:337-338
+    ht = (xx.float() * rms).to(torch.bfloat16) * ww
+    ht.backward(dh)
+    _close(to_np(h), to_np(ht), ulps=2)
+    _close(to_np(dx), to_np(xx.grad), cancel=True)
+    assert _ulps(to_np(dw), to_np(ww.grad)).max() <= 2
+
+
+def test_rmsnorm_empty_rows_give_zero_weight_gradient():
+    from flower_amd import _lib
+    lib = _lib.load()
+    x = torch.empty((0, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.ones(64, dtype=torch.bfloat16, device="cuda")
+    dw = torch.full((64,), 7.0, dtype=torch.bfloat16, device="cuda")
+    s = _lib.stream_of(w)
+    _lib.check(lib.flw_rmsnorm_bwd(w.data_ptr(), 0, 64, 64, w.data_ptr(), EPS, w.data_ptr(), 64, w.data_ptr(), 64,
+                                   dw.data_ptr(), None, 0, s), "rmsnorm bwd")
+    _lib.check(lib.flw_rmsnorm_fwd(w.data_ptr(), 0, 64, 64, w.data_ptr(), EPS, w.data_ptr(), 64, s), "rmsnorm fwd")
+    torch.cuda.synchronize()
+    assert torch.equal(dw, torch.zeros_like(dw)) and torch.equal(w, torch.ones_like(w)) and x.numel() == 0
+
+
+SWIGLU_CASES = [(2, 1000, 3392, 0), (1, 37, 64, 0), (3, 50, 1024, 64)]
+
+
+@pytest.mark.parametrize("B,T,cols,pad", SWIGLU_CASES)
+def test_swiglu_forward_backward_against_oracle(B, T, cols, pad):
+    from flower_amd.block import _SwiGLUFn
+    g = torch.Generator().manual_seed(cols + T)
+    gu = (torch.randn(B, T, 2 * cols + pad, generator=g) * 3.0).to("cuda", torch.bfloat16)
+    gate, up = gu[..., :cols], gu[..., cols:2 * cols]                   # row stride 2 cols + pad
+    dh = torch.randn(B, T, cols, generator=g).to("cuda", torch.bfloat16)
+    gg, uu = gate.detach().requires_grad_(True), up.detach().requires_grad_(True)
+    h = _SwiGLUFn.apply(gg, uu)
+    h.backward(dh)
+    gn, un, dn = to_np(gate), to_np(up), to_np(dh)
+    _close(to_np(h), swiglu(gn, un))
+    rdg, rdu = swiglu_backward(gn, un, dn)
+    _close(to_np(gg.grad), rdg, cancel=True)
+    _close(to_np(uu.grad), rdu)
+    # torch's bf16 autograd of the reference's expressions on the same inputs
+    gt, ut = gate.detach().requires_grad_(True), up.detach().requires_grad_(True)
+    ht = torch.nn.functional.silu(gt) * ut
+    ht.backward(dh)
+    _close(to_np(h), to_np(ht))
+    _close(to_np(gg.grad), to_np(gt.grad), cancel=True)
+    _close(to_np(uu.grad), to_np(ut.grad))

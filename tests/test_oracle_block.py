@@ -158,3 +158,96 @@ def test_rope_backward_is_the_adjoint_and_norm_backward_the_derivative():
     got = head_rmsnorm_backward(xr.astype(np.float32), dn.astype(np.float32), eps, "f32")
     np.testing.assert_allclose(got, fd, rtol=2e-4, atol=2e-5)
 
+
+def test_rmsnorm_backward_matches_torch_autograd():
+    """oracle.block.rmsnorm_backward against torch's CPU autograd of base.py:337-338 on bf16 rows
+    and a bf16 gain: dx within one bf16 ulp in a small fraction of values (fp32 sums' order), dw
+    (a sum over 512 rows) within one ulp."""
+    from oracle.block import rmsnorm_backward
+    g = torch.Generator().manual_seed(12)
+    x = (torch.randn(512, 320, generator=g) * 2).to(torch.bfloat16).requires_grad_(True)
+    w = (1 + 0.2 * torch.randn(320, generator=g)).to(torch.bfloat16).requires_grad_(True)
+    dh = torch.randn(512, 320, generator=g).to(torch.bfloat16)
+    eps = 1e-6
+    rms = x.float().pow(2).mean(dim=-1, keepdim=True).add(eps).rsqrt()
+    ((x.float() * rms).to(torch.bfloat16) * w).backward(dh)
+    dx, dw = rmsnorm_backward(x.detach().float().numpy(), w.detach().float().numpy(), dh.float().numpy(), eps)
+    d = _ulp_diff(dx, x.grad.float().numpy())
+    assert d.max() <= 1 and (d > 0).mean() < 5e-3, ((d > 0).mean(), d.max())
+    assert _ulp_diff(dw, w.grad.float().numpy()).max() <= 1
+
+
+def test_rmsnorm_backward_is_the_derivative():
+    """Independent of torch: rmsnorm_backward (bf16 roundings at every step, so the check is
+    relative) against central finite differences of sum(dh * x r w) in float64: relative error of
+    dx and dw below 2 %, which the norm's r^3 term dropped fails."""
+    from oracle.block import rmsnorm_backward
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    w = (1 + 0.3 * rng.standard_normal(64)).astype(np.float32)
+    dh = rng.standard_normal((6, 64)).astype(np.float32)
+    eps = 1e-6
+
+    def f(xv, wv):
+        xv = xv.astype(np.float64)
+        return float(np.sum(dh * xv / np.sqrt(np.mean(xv * xv, axis=-1, keepdims=True) + eps) * wv))
+    h = 1e-6
+    fx = np.zeros_like(x, dtype=np.float64)
+    for i in range(x.shape[0]):
+        for j in range(x.shape[1]):
+            e = np.zeros_like(x, dtype=np.float64)
+            e[i, j] = h
+            fx[i, j] = (f(x + e, w) - f(x - e, w)) / (2 * h)
+    fw = np.array([(f(x, w + h * np.eye(64)[j]) - f(x, w - h * np.eye(64)[j])) / (2 * h) for j in range(64)])
+    dx, dw = rmsnorm_backward(x, w, dh, eps)
+    assert np.linalg.norm(dx - fx) / np.linalg.norm(fx) < 0.02
+    assert np.linalg.norm(dw - fw) / np.linalg.norm(fw) < 0.02
+    n = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    dropped = dh * w / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    assert np.linalg.norm(dropped - fx) / np.linalg.norm(fx) > 0.1 and n.shape == x.shape
+
+
+def test_swiglu_and_backward_match_torch_autograd():
+    """oracle.block.swiglu / swiglu_backward against torch's CPU silu, product and autograd on bf16
+    values: within one bf16 ulp in a small fraction of values (torch's CPU exp)."""
+    from oracle.block import swiglu, swiglu_backward
+    g = torch.Generator().manual_seed(14)
+    gate = (torch.randn(64, 1024, generator=g) * 3).to(torch.bfloat16).requires_grad_(True)
+    up = (torch.randn(64, 1024, generator=g) * 2).to(torch.bfloat16).requires_grad_(True)
+    dh = torch.randn(64, 1024, generator=g).to(torch.bfloat16)
+    h = torch.nn.functional.silu(gate) * up
+    h.backward(dh)
+    got = swiglu(gate.detach().float().numpy(), up.detach().float().numpy())
+    d = _ulp_diff(got, h.detach().float().numpy())
+    assert d.max() <= 1 and (d > 0).mean() < 5e-3, ((d > 0).mean(), d.max())
+    dg, du = swiglu_backward(gate.detach().float().numpy(), up.detach().float().numpy(), dh.float().numpy())
+    for a, b in ((dg, gate.grad), (du, up.grad)):
+        d = _ulp_diff(a, b.float().numpy())
+        assert d.max() <= 1 and (d > 0).mean() < 5e-3, ((d > 0).mean(), d.max())
+
+
+def test_swiglu_closed_forms_and_derivative():
+    """silu(0) = 0, silu(x) -> x for large x and -> 0 for very negative x; d silu / dx at 0 is 1/2;
+    swiglu_backward against central differences of swiglu's float64 form (a sign slip in the
+    (1 - sig) term fails it)."""
+    from oracle.block import swiglu, swiglu_backward
+    one = np.ones(3, np.float32)
+    got = swiglu(np.array([0.0, 20.0, -30.0], np.float32), one)
+    assert got[0] == 0.0 and got[1] == 20.0 and -1e-11 < got[2] < 0.0       # -30 / (1 + e^30)
+    dg, du = swiglu_backward(np.zeros(1, np.float32), np.ones(1, np.float32), np.ones(1, np.float32))
+    assert dg[0] == 0.5 and du[0] == 0.0
+    rng = np.random.default_rng(15)
+    gv = rng.standard_normal(256) * 2
+    uv = rng.standard_normal(256)
+
+    def sw(x):
+        return x / (1 + np.exp(-x))
+    h = 1e-6
+    fd_g = (sw(gv + h) - sw(gv - h)) / (2 * h) * uv
+    dg, du = swiglu_backward(gv.astype(np.float32), uv.astype(np.float32), np.ones(256, np.float32))
+    assert np.abs(dg - fd_g).max() < 2e-2 * (np.abs(fd_g).max() + 1)
+    assert np.abs(du - sw(gv)).max() < 2e-2 * (np.abs(sw(gv)).max() + 1)
+    sig = 1 / (1 + np.exp(-gv))
+    wrong = sig * (1 - gv * (1 - sig)) * uv
+    assert np.abs(wrong - fd_g).max() > 0.1
+
