@@ -30,6 +30,9 @@ constexpr int kThreads = 256;
 // ties 256 x 2 on the large shapes and is faster on small ones (more workgroups to spread).
 constexpr int64_t kRowsPerChunk = 128;   // multiple of 64: VTILE chunks hold whole key tiles
 constexpr int kUnroll = 1;               // 16-byte loads in flight per thread per iteration
+// The amax pass without a transform keeps 4 loads in flight per thread: with chunks of wide rows
+// (the tensorwise flat grid) a thread walks many vectors, and the max folds in any order.
+constexpr int kAmaxUnroll = 4;
 
 struct QTensor {
   const void* x;
@@ -112,11 +115,12 @@ __global__ __launch_bounds__(kThreads) void amax_kernel(QuantParams p) {
   const T* base = static_cast<const T*>(t.x) + i0 * t.s0 + i1 * t.s1;
   const int64_t vpr = p.d3 / V::N;
   const int64_t nvec = (r1 - r0) * vpr;
+  constexpr int U = XFORM ? kUnroll : kAmaxUnroll;
   uint32_t m = 0;
-  for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kThreads * kUnroll) {
-    float f[kUnroll][V::N];
+  for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kThreads * U) {
+    float f[U][V::N];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t v = v0 + (int64_t)u * kThreads;
       if (v < nvec) {
         V::load(base + vec_offset(t, r0, v, vpr, V::N, p.d3), f[u]);
@@ -127,13 +131,13 @@ __global__ __launch_bounds__(kThreads) void amax_kernel(QuantParams p) {
     }
     if (XFORM && (t.norm || t.rcos != nullptr)) {          // uniform over the workgroup
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         const int64_t v = v0 + (int64_t)u * kThreads;
         qk_transform<T>(t, f[u], r0 + v / vpr, v % vpr, (int)vpr, p.d3, v < nvec);
       }
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int i = 0; i < V::N; ++i) { const uint32_t a = abs_bits(f[u][i]); m = m > a ? m : a; }
   }
