@@ -1079,8 +1079,12 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
       p.part = static_cast<float*>(workspace);
     }
     // Fewer 256 x 256 tiles than compute units: 256 x 128 tiles (twice as many), and then half
-    // the K ranges of a split (the same number of work items, half the partials to fold).
-    const bool narrow = p.lds_epi && gmax == nullptr && tiles < compute_units();
+    // the K ranges of an even split (the same number of work items, half the partials to fold).
+    // An odd split keeps its 256 x 256 tiles: halving 3 ranges to 1 would leave the items a
+    // third of the GPU short (the 450M block's wgrad outputs [3392 | 3840, 1280] at K = 16384:
+    // 70 / 75 tiles x 3 ranges, 97 / 92 us against 108 / 103 us as 135 / 150 narrow tiles).
+    const bool narrow = p.lds_epi && gmax == nullptr && tiles < compute_units() &&
+                        (p.splits == 1 || p.splits % 2 == 0);
     if (narrow) {
       p.tiles_m = (int)((M + 127) / 128);
       p.splits = p.splits / 2 > 1 ? p.splits / 2 : 1;

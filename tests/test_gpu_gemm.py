@@ -52,11 +52,13 @@ def test_scaled_mm_matches_closed_form(M, N, K, sx_per_row, sw_per_col):
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 4096), (512, 1024, 2048), (4096, 1024, 8192), (300, 260, 1024),
                                    (100, 36, 80), (256, 256, 4160), (4096, 1024, 3392), (1024, 512, 192),
-                                   (300, 260, 320)])
+                                   (300, 260, 320), (3840, 1280, 1536), (2560, 1280, 2560)])
 def test_scaled_mm_split_k_matches_closed_form(M, N, K):
     """flw_fp8_scaled_mm_ws: outputs with few 256 x 256 tiles are split over K into the workspace
-    (1 tile -> 8 ranges, 8 tiles -> 4, the C2 wgrad shape 64 tiles -> 4) and summed by the finish
-    kernel; shapes without a split (K % 64 != 0) take the plain path through the same call.
+    (1 tile -> 8 ranges, 8 tiles -> 4, the C2 wgrad shape 64 tiles -> 4; an even split runs on
+    256 x 128 tiles with half the ranges, an odd one -- 75 tiles -> 3, 50 -> 5 -- on 256 x 256
+    tiles) and summed by the finish kernel; shapes without a split (K % 64 != 0) take the plain
+    path through the same call.
     K % 128 == 64 (the SwiGLU width 3392 of the 450M block among them) ends the last K range on a
     64-deep stage, in the 256 x 256 and the 256 x 128 tiles, split or not. Against the closed
     form, and equal to the unsplit call within the GEMM tolerance."""
