@@ -63,6 +63,9 @@ SIGNATURES = {
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "flw_qkv_heads_bwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_float, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "flw_quant_tensor_t_workspace_bytes": (c_size_t, [c_int64, c_int64]),
+    "flw_quant_tensor_t_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                        c_void_p, c_void_p, c_size_t, c_void_p]),
     "flw_rmsnorm_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64,
                                 c_void_p]),
     "flw_rmsnorm_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),

@@ -1085,6 +1085,132 @@ extern "C" int flw_transpose_e4m3(const uint8_t* codes, int64_t rows, int64_t co
   return check_launch("flw_transpose_e4m3");
 }
 
+// Tensorwise e4m3 of a bf16 matrix writing both layouts in one pass: a 64 x 64 tile's codes go to
+// out8 in rows and, staged in LDS, to out_t in columns (the transpose_u8_kernel gather). The scale
+// comes from the tensor's |x| max (amax_bits, folded by the amax pass before this launch); the
+// arithmetic is quant_kernel's, so both layouts hold exactly the tensorwise quantiser's codes.
+// Rows of out_t past `rows` (up to ld, which grid.y covers) are zero.
+__global__ __launch_bounds__(256) void quant_tensor_t_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                             int64_t cols, int64_t xs,
+                                                             const uint32_t* __restrict__ amax_bits,
+                                                             uint8_t* __restrict__ out8, int64_t ld8,
+                                                             uint8_t* __restrict__ out_t, int64_t ldt,
+                                                             float* __restrict__ scale_out) {
+  __shared__ __align__(16) uint8_t t[kTT * kTPitch];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * kTT, r0 = (int64_t)blockIdx.y * kTT;
+  const float amax = __uint_as_float(*amax_bits);
+  const float scale = (amax < kEps ? kEps : amax) / kE4m3Max;    // IEEE fp32 division
+  const bool fast = __builtin_isfinite(amax);
+  const float rcp = 1.0f / scale;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) scale_out[0] = scale;
+  {
+    const int r = tid >> 2, q = tid & 3;
+    const int64_t gr = r0 + r, gc = c0 + 16 * q;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gr < rows && gc < cols) {
+      float f[16];
+      Vec16<uint16_t>::load(x + gr * xs + gc, f);
+      Vec16<uint16_t>::load(x + gr * xs + gc + 8, f + 8);
+      uint32_t w[4];
+      codes_of<8>(f, scale, rcp, fast, w);
+      codes_of<8>(f + 8, scale, rcp, fast, w + 2);
+      v = make_uint4(w[0], w[1], w[2], w[3]);
+      *reinterpret_cast<uint4*>(out8 + gr * ld8 + gc) = v;
+    }
+    *reinterpret_cast<uint4*>(t + r * kTPitch + 16 * q) = v;
+  }
+  __syncthreads();
+  const int c = tid >> 2, q = tid & 3;
+  const int64_t oc = c0 + c, orow0 = r0 + 16 * q;
+  if (oc >= cols || orow0 >= ldt) return;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) v |= (uint32_t)t[(16 * q + 4 * j + b) * kTPitch + c] << (8 * b);
+    w[j] = v;
+  }
+  *reinterpret_cast<uint4*>(out_t + oc * ldt + orow0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// One workgroup of 1024 threads folds n amax partials into out[0]: eight independent loads in
+// flight per thread, then the wave and workgroup maxima.
+__global__ __launch_bounds__(1024) void amax_fold_tensor_kernel(const uint32_t* __restrict__ part, int64_t n,
+                                                                uint32_t* __restrict__ out) {
+  __shared__ uint32_t red[16];
+  uint32_t m = 0;
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += 1024 * 8) {
+    uint32_t a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + 1024 * u;
+      a[u] = i < n ? part[i] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m = m > a[u] ? m : a[u];
+  }
+  m = wave_max_u32(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = red[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) r = r > red[i] ? r : red[i];
+    out[0] = r;
+  }
+}
+
+extern "C" size_t flw_quant_tensor_t_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const int64_t n = rows * cols;
+  const int64_t flat_rows = n % 64 == 0 ? n / 64 : rows;    // the amax pass's chunk rows
+  return 16 + partial_bytes(1, 1, flat_rows);
+}
+
+extern "C" int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride, uint8_t* out8,
+                                       int64_t ld8, uint8_t* out_t, int64_t ldt, float* scale_out, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  FLW_REQUIRE(x != nullptr && out8 != nullptr && out_t != nullptr && scale_out != nullptr, FLW_E_INVALID,
+              "null pointer");
+  FLW_REQUIRE(rows > 0 && cols > 0, FLW_E_INVALID, "empty matrix");
+  FLW_REQUIRE(cols % 16 == 0 && row_stride % 8 == 0 && row_stride >= cols && ((uintptr_t)x & 15) == 0,
+              FLW_E_INVALID, "cols must be a multiple of 16, bf16 rows 16-byte aligned with a stride >= cols");
+  FLW_REQUIRE(ld8 >= cols && ld8 % 16 == 0 && ((uintptr_t)out8 & 15) == 0, FLW_E_INVALID,
+              "out8 rows must be 16-byte aligned with ld8 >= cols");
+  FLW_REQUIRE(ldt >= rows && ldt % 16 == 0 && ((uintptr_t)out_t & 15) == 0, FLW_E_INVALID,
+              "ld must be >= rows and a multiple of 16, out_t 16-byte aligned");
+  const size_t need = flw_quant_tensor_t_workspace_bytes(rows, cols);
+  FLW_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0 && workspace_bytes >= need, FLW_E_WORKSPACE,
+              "workspace needs %zu bytes (16-byte aligned)", need);
+  const int64_t gx = (cols + kTT - 1) / kTT, gy = (ldt + kTT - 1) / kTT;
+  FLW_REQUIRE(gx <= 0x7FFFFFFF && gy <= 65535, FLW_E_UNSUPPORTED, "matrix too large");
+  // The amax pass over the matrix as 64-value rows when it is contiguous (chunks of 128 such rows
+  // spread over the GPU), else over its own rows; one workgroup of 1024 folds the partials.
+  const bool flat = row_stride == cols && (rows * cols) % 64 == 0;
+  QuantParams p{};
+  const int64_t d2 = flat ? rows * cols / 64 : rows, d3 = flat ? 64 : cols;
+  set_tensor(p.t[0], x, d2 * (flat ? 64 : row_stride), d2 * (flat ? 64 : row_stride), flat ? 64 : row_stride, d3,
+             FLW_LAYOUT_BHTD, nullptr, nullptr, nullptr);
+  p.d0 = 1; p.d1 = 1; p.d2 = d2; p.d3 = d3;
+  p.nchunks = nchunks_of(d2);
+  uint32_t* amax = static_cast<uint32_t*>(workspace);
+  p.partials = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + 16);
+  p.granularity = FLW_SCALE_TENSOR;
+  FLW_REQUIRE(p.nchunks <= 0x7FFFFFFF, FLW_E_UNSUPPORTED, "matrix too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const Timer tm = take_timer();
+  (void)launch_ext(reinterpret_cast<const void*>(&amax_kernel<uint16_t>), dim3((unsigned)p.nchunks, 1u, 1u),
+                   dim3(kThreads), 0, s, p, tm.start, nullptr);
+  (void)launch_args(reinterpret_cast<const void*>(&amax_fold_tensor_kernel), dim3(1u), dim3(1024), 0, s, nullptr,
+                    nullptr, static_cast<const uint32_t*>(p.partials), (int64_t)p.nchunks, amax);
+  (void)launch_args(reinterpret_cast<const void*>(&quant_tensor_t_kernel), dim3((unsigned)gx, (unsigned)gy),
+                    dim3(256), 0, s, nullptr, tm.stop, static_cast<const uint16_t*>(x), rows, cols, row_stride,
+                    static_cast<const uint32_t*>(amax), out8, ld8, out_t, ldt, scale_out);
+  return check_launch("flw_quant_tensor_t_e4m3");
+}
+
 extern "C" int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
                                    int granularity, uint8_t* out_t, int64_t ld, float* scale_out,
                                    void* workspace, size_t workspace_bytes, void* stream) {

@@ -246,6 +246,19 @@ int flw_quant_cols_e4m3(const void* x, int dtype, int64_t rows, int64_t cols, in
                         int granularity, uint8_t* out_t, int64_t ld, float* scale_out, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* The tensorwise e4m3 cast of torchao Float8Linear (one scale for the whole matrix, the
+ * reference's default recipe; torchao 0.18.0, not vendored, enabled at flower/train.py:368-370)
+ * of a bf16 matrix x [rows, cols] written in both layouts the training GEMMs read: out8 [rows, cols]
+ * (row stride ld8) for the forward / dgrad operand and out_t [cols, ldt] (ldt >= rows; columns
+ * rows .. ldt - 1 zero) for the wgrad operand -- the codes of flw_quant_e4m3(FLW_SCALE_TENSOR) and
+ * flw_transpose_e4m3 of them, bit for bit, from one read of x. scale_out[0] = the scale. Three
+ * launches: the amax pass, its fold, the quantise-and-transpose pass. cols % 16 == 0; 16-byte
+ * aligned rows; workspace of flw_quant_tensor_t_workspace_bytes(rows, cols). */
+size_t flw_quant_tensor_t_workspace_bytes(int64_t rows, int64_t cols);
+int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride, uint8_t* out8, int64_t ld8,
+                            uint8_t* out_t, int64_t ldt, float* scale_out, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* e4m3 codes [rows, cols] transposed to out_t [cols, ld] (ld >= rows, ld % 16 == 0; columns
  * rows .. ld - 1 of out_t zero). With one scale for the whole matrix (the tensorwise recipe) a
  * matrix's per-column codes equal its per-row codes, so the transposed operands of the backward

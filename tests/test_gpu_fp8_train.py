@@ -149,3 +149,30 @@ def test_transposed_tensorwise_codes_equal_the_column_quantiser(R, C, ld):
     assert torch.equal(sx, want_s)
     assert torch.equal(got8, want8)
     assert not got8[:, R:].any()
+
+
+@pytest.mark.parametrize("R,C,ld,pad,special", [(4096, 1024, 4096, 0, None), (300, 48, 384, 0, None),
+                                                (1, 16, 16, 0, None), (129, 3392, 256, 0, None),
+                                                (70, 208, 80, 16, None), (257, 1280, 384, 0, "inf"),
+                                                (100, 64, 128, 0, "nan"), (64, 128, 64, 0, "zero")])
+def test_one_pass_tensorwise_codes_in_both_layouts(R, C, ld, pad, special):
+    """flw_quant_tensor_t_e4m3 (through _quantize_tensorwise_t): the row codes and scale of the
+    tensorwise quantiser (_quantize_rows) and their transpose (flw_transpose_e4m3), bit for bit,
+    with the columns past R zero -- contiguous matrices (the amax pass over 64-value rows) and
+    strided rows (over the matrix's rows), an inf or a NaN in the matrix (the exact path) and an
+    all-zero matrix (the scale floor)."""
+    from flower_amd.precision import _quantize_rows, _quantize_tensorwise_t, transpose_codes
+    base = (_rnd((R, C + pad), R + C) * 3).cuda()
+    if special == "inf":
+        base[R // 2, 7] = float("inf")
+    elif special == "nan":
+        base[3, 5] = float("nan")
+    elif special == "zero":
+        base.zero_()
+    x = base[:, :C]
+    x8, x8t, sx = _quantize_tensorwise_t(x, ld)
+    want8, want_s = _quantize_rows(x.contiguous(), "tensorwise")
+    assert torch.equal(sx, want_s) or (special == "nan" and torch.isnan(sx).all() and torch.isnan(want_s).all())
+    assert torch.equal(x8, want8)
+    assert torch.equal(x8t, transpose_codes(want8, ld))
+    assert not x8t[:, R:].any()
