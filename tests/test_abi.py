@@ -306,3 +306,13 @@ def test_training_row_kernel_refusals_on_the_host():
     assert rc == 1 and b"aligned" in lib.flw_last_error()
     rc = lib.flw_swiglu_fwd(P, P, 1 << 28, 128, 128, 128, P, 128, None)
     assert rc == 2 and b"too many" in lib.flw_last_error()
+    need = lib.flw_quant_tensor_t_workspace_bytes(1000, 1280)              # 16 + one u32 per chunk
+    assert need == 16 + 4 * ((1000 * 1280 // 64 + 127) // 128)
+    rc = lib.flw_quant_tensor_t_e4m3(P, 1000, 1288, 1288, P, 1288, P, 1024, P, P, need, None)
+    assert rc == 1 and b"multiple of 16" in lib.flw_last_error()
+    rc = lib.flw_quant_tensor_t_e4m3(P, 1000, 1280, 1280, P, 1280, P, 992, P, P, need, None)
+    assert rc == 1 and b"ld must be >= rows" in lib.flw_last_error()
+    rc = lib.flw_quant_tensor_t_e4m3(P, 1000, 1280, 1280, P, 1280, P, 1024, P, P, need - 4, None)
+    assert rc == 3 and b"workspace" in lib.flw_last_error()
+    rc = lib.flw_quant_tensor_t_e4m3(P, 0, 1280, 1280, P, 1280, P, 1024, P, P, need, None)
+    assert rc == 1 and b"empty" in lib.flw_last_error()
