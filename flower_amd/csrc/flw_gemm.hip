@@ -1083,8 +1083,15 @@ static int scaled_mm(const uint8_t* x8, int64_t M, int64_t K, const uint8_t* w8,
     // An odd split keeps its 256 x 256 tiles: halving 3 ranges to 1 would leave the items a
     // third of the GPU short (the 450M block's wgrad outputs [3392 | 3840, 1280] at K = 16384:
     // 70 / 75 tiles x 3 ranges, 97 / 92 us against 108 / 103 us as 135 / 150 narrow tiles).
-    const bool narrow = p.lds_epi && gmax == nullptr && tiles < compute_units() &&
-                        (p.splits == 1 || p.splits % 2 == 0);
+    // More tiles than compute units: the narrow tiles too when they fill the last round of the
+    // persistent grid enough better to pay their ~10 % higher cost per output (measured at
+    // M = 16384: 320 tiles [N = 1280] 62.5 % -> 83 % filled, -10 to -19 %; 896 tiles 87.5 % ->
+    // 100 %, -3 %; 960 or 512 tiles, equally filled either way, +3 to +13 % narrow).
+    const int cus = compute_units();
+    auto fill = [cus](int64_t items) { return (double)items / (double)(((items + cus - 1) / cus) * cus); };
+    const bool narrow = p.lds_epi && gmax == nullptr && xform == nullptr &&
+                        (tiles < cus ? (p.splits == 1 || p.splits % 2 == 0)
+                                     : p.splits == 1 && fill(2 * tiles) > 1.1 * fill(tiles));
     if (narrow) {
       p.tiles_m = (int)((M + 127) / 128);
       p.splits = p.splits / 2 > 1 ? p.splits / 2 : 1;

@@ -32,9 +32,13 @@ def codes(shape, seed):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 256, 512), (100, 36, 80), (257, 132, 1040), (1, 16, 16),
-                                   (300, 132, 256), (1, 20, 128), (513, 260, 1024), (256, 512, 384)])
+                                   (300, 132, 256), (1, 20, 128), (513, 260, 1024), (256, 512, 384),
+                                   (5120, 3328, 128), (4900, 1280, 320)])
 @pytest.mark.parametrize("sx_per_row,sw_per_col", [(True, True), (False, False), (True, False)])
 def test_scaled_mm_matches_closed_form(M, N, K, sx_per_row, sw_per_col):
+    """The 256-tile kernel against the closed form: small and ragged shapes, and outputs with more
+    256 x 256 tiles than compute units whose last round the 256 x 128 tiles fill better (260 tiles;
+    a ragged 100 with K % 128 == 64)."""
     from flower_amd import _lib as L
     lb = L.load()
     x8, w8 = codes((M, K), 1), codes((N, K), 2)
