@@ -69,8 +69,10 @@ SIGNATURES = {
     "flw_rmsnorm_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64,
                                 c_void_p]),
     "flw_rmsnorm_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),
+    "flw_add_rmsnorm_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_float,
+                                    c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "flw_rmsnorm_bwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64,
-                                c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
+                                c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
     "flw_swiglu_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64,
                                c_void_p]),
     "flw_swiglu_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64,

@@ -50,6 +50,23 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
     return t2
 
 
+def _rmsnorm_backward(x2, weight, eps, dh, dres, shape):
+    """(dx, dweight) of RMSNorm on the saved rows x2 [rows, cols] for the gradient dh; dres (or None):
+    the gradient x2 receives along the residual stream, added in the same pass (flw_rmsnorm_bwd)."""
+    rows, cols = x2.shape
+    lib = _lib.load()
+    d2 = _rows(dh.to(x2.dtype))
+    r2 = _rows(dres.to(x2.dtype)) if dres is not None else None
+    dx = torch.empty((rows, cols), dtype=x2.dtype, device=x2.device)
+    dw = torch.empty((cols,), dtype=weight.dtype, device=weight.device)
+    ws = _lib.workspace(lib.flw_rmsnorm_bwd_workspace_bytes(rows, cols), x2.device)
+    _lib.check(lib.flw_rmsnorm_bwd(x2.data_ptr(), rows, cols, x2.stride(0), weight.data_ptr(), eps,
+                                   d2.data_ptr(), d2.stride(0), _lib.ptr(r2), r2.stride(0) if r2 is not None else 0,
+                                   dx.data_ptr(), cols, dw.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   _lib.stream_of(x2)), "RMSNorm backward")
+    return dx.view(shape), dw
+
+
 class _RMSNormFn(torch.autograd.Function):
     """RMSNorm.forward on bf16 rows as one HIP pass (flw_rmsnorm_fwd), its autograd backward as one
     more plus the weight gradient's column sum (flw_rmsnorm_bwd), rounded as torch's autograd of the
@@ -70,16 +87,57 @@ class _RMSNormFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dh):
         x2, weight = ctx.saved_tensors
-        rows, cols = x2.shape
+        dx, dw = _rmsnorm_backward(x2, weight, ctx.eps, dh, None, ctx.shape)
+        return dx, dw, None
+
+
+class _RMSNormResFn(torch.autograd.Function):
+    """(RMSNorm(x), x) for the block's first norm: the second output is x itself (a view) as the
+    residual stream, so that the gradient x receives along that stream reaches this backward, which
+    adds it to the norm's gradient in its own pass -- the sum autograd would otherwise form with a
+    separate kernel where x has two uses (ln1 and the residual add, base.py:719-720)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        h = _RMSNormFn.forward(ctx, x, weight, eps)
+        return h, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, dh, dres):
+        x2, weight = ctx.saved_tensors
+        if dh is None:
+            return dres, None, None
+        dx, dw = _rmsnorm_backward(x2, weight, ctx.eps, dh, dres, ctx.shape)
+        return dx, dw, None
+
+
+class _AddRMSNormFn(torch.autograd.Function):
+    """(s, RMSNorm(s)) with s = x + a: the block's first residual add and the ln2 that reads it
+    (base.py:720-721) in one pass (flw_add_rmsnorm_fwd); the backward adds s's residual-stream
+    gradient to the norm's in the norm's pass, and hands the sum to both x and a, as the add's
+    autograd does."""
+
+    @staticmethod
+    def forward(ctx, x, a, weight, eps):
         lib = _lib.load()
-        d2 = _rows(dh.to(x2.dtype))
-        dx = torch.empty((rows, cols), dtype=x2.dtype, device=x2.device)
-        dw = torch.empty((cols,), dtype=weight.dtype, device=weight.device)
-        ws = _lib.workspace(lib.flw_rmsnorm_bwd_workspace_bytes(rows, cols), x2.device)
-        _lib.check(lib.flw_rmsnorm_bwd(x2.data_ptr(), rows, cols, x2.stride(0), weight.data_ptr(), ctx.eps,
-                                       d2.data_ptr(), d2.stride(0), dx.data_ptr(), cols, dw.data_ptr(),
-                                       ws.data_ptr(), ws.numel(), _lib.stream_of(x2)), "RMSNorm backward")
-        return dx.view(ctx.shape), dw, None
+        x2, a2 = _rows(x), _rows(a)
+        rows, cols = x2.shape
+        s = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+        h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        _lib.check(lib.flw_add_rmsnorm_fwd(x2.data_ptr(), a2.data_ptr(), rows, cols, x2.stride(0), a2.stride(0),
+                                           weight.data_ptr(), float(eps), s.data_ptr(), cols, h.data_ptr(), cols,
+                                           _lib.stream_of(x)), "residual add + RMSNorm")
+        ctx.save_for_backward(s, weight)
+        ctx.eps, ctx.shape = float(eps), x.shape
+        return s.view(x.shape), h
+
+    @staticmethod
+    def backward(ctx, ds, dh):
+        s2, weight = ctx.saved_tensors
+        if dh is None:
+            return ds, ds, None, None
+        d, dw = _rmsnorm_backward(s2, weight, ctx.eps, dh, ds, ctx.shape)
+        return d, d, dw, None
 
 
 class _SwiGLUFn(torch.autograd.Function):
@@ -397,6 +455,14 @@ class TransformerBlock(nn.Module):
         self.ff = FeedForward(config)
 
     def forward(self, x: torch.Tensor, memory: torch.Tensor | None = None):
+        d = x.shape[-1]
+        if d % 8 == 0 and d <= 8192 and x.numel() > 0 and _hip_rows_ok(x, self.ln1.weight, self.ln2.weight):
+            # bf16 on the GPU: ln1 hands x on as the residual stream and ln2 takes the first
+            # residual add into its pass, so the norms' backward passes also add the residual
+            # gradients (the same bf16 sums autograd forms for x's and x1's two uses).
+            h1, xr = _RMSNormResFn.apply(x, self.ln1.weight, self.ln1.eps)
+            x1, h2 = _AddRMSNormFn.apply(xr, self.attn(h1), self.ln2.weight, self.ln2.eps)
+            return x1 + self.ff(h2), memory
         x = x + self.attn(self.ln1(x))
         x = x + self.ff(self.ln2(x))
         return x, memory

@@ -4,9 +4,12 @@
 // reduction for the norm's weight gradient), with the roundings of the reference's torch
 // expressions under eager autograd:
 //   RMSNorm forward:  r = 1 / sqrt(mean(x^2) + eps) in fp32, n = bf16(x r), h = bf16(n w);
+//     with a residual input a (the block's x + attn(...) feeding ln2), x = bf16(x0 + a) first,
+//     written out as the residual stream;
 //   RMSNorm backward: dn = bf16(dh w); dw = bf16(sum over rows of bf16(dh n)), the sum in fp32;
 //     dx = bf16(bf16(dn r) - bf16(x r^3 sum(dn x) / cols)) -- x.float() appears twice in the
-//     expression, and each cast hands back its own bf16 gradient, summed in bf16;
+//     expression, and each cast hands back its own bf16 gradient, summed in bf16; with the residual
+//     stream's gradient dres, dx = bf16(dres + that), the sum autograd forms where x has two uses;
 //   SwiGLU forward:   s = bf16(g / (1 + exp(-g))), h = bf16(s u);
 //   SwiGLU backward:  ds = bf16(dh u), du = bf16(dh s), sig = 1 / (1 + exp(-g)),
 //     dg = bf16(ds sig (1 + g (1 - sig))) (torch's silu backward).
@@ -67,15 +70,32 @@ __device__ __forceinline__ void load_row(const uint16_t* src, int nvec, int lane
   }
 }
 
-template <int NV>
+template <int NV, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __restrict__ x, int64_t rows, int cols,
                                                           int64_t xs, const uint16_t* __restrict__ w, float eps,
-                                                          uint16_t* __restrict__ h, int64_t hs) {
+                                                          uint16_t* __restrict__ h, int64_t hs,
+                                                          const uint16_t* __restrict__ a, int64_t as,
+                                                          uint16_t* __restrict__ sum, int64_t ss) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;                        // wave-uniform
   const int lane = threadIdx.x & 63, nvec = cols >> 3;
   uint4 xb[NV];
   load_row<NV>(x + row * xs, nvec, lane, xb);
+  if (ADD) {                                      // x = bf16(x0 + a), kept as the residual stream
+    uint4 ab[NV];
+    load_row<NV>(a + row * as, nvec, lane, ab);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float f[8], g[8];
+      Vec16<uint16_t>::unpack(xb[i], f);
+      Vec16<uint16_t>::unpack(ab[i], g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] += g[e];
+      xb[i] = pack_bf16x8(f);
+      const int v = lane + 64 * i;
+      if (v < nvec) *reinterpret_cast<uint4*>(sum + row * ss + 8 * v) = xb[i];
+    }
+  }
   const float r = row_rstd<NV>(xb, cols, eps);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -96,12 +116,13 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __rest
   }
 }
 
-template <int NV>
+template <int NV, bool RES>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint16_t* __restrict__ x, int64_t rows, int cols,
                                                           int64_t xs, const uint16_t* __restrict__ w, float eps,
                                                           const uint16_t* __restrict__ dh, int64_t dhs,
                                                           uint16_t* __restrict__ dx, int64_t dxs,
-                                                          float* __restrict__ part) {
+                                                          float* __restrict__ part,
+                                                          const uint16_t* __restrict__ dres, int64_t drs) {
   extern __shared__ float fold[];                 // [cols]: one wave's partials at a time
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nvec = cols >> 3;
   float acc[NV][8];
@@ -158,6 +179,16 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint16_t* __rest
         round2_bf16(b0, b1);
         o[e] = a0 - b0;
         o[e + 1] = a1 - b1;
+      }
+      if (RES) {                                  // bf16(dres + bf16(o)): autograd's sum
+        float d[8];
+        Vec16<uint16_t>::load(dres + row * drs + 8 * v, d);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          round2_bf16(o[e], o[e + 1]);
+          o[e] += d[e];
+          o[e + 1] += d[e + 1];
+        }
       }
       *reinterpret_cast<uint4*>(dx + row * dxs + 8 * v) = pack_bf16x8(o);
     }
@@ -279,10 +310,11 @@ static int norm_nv(int64_t cols) {
   return 0;
 }
 
-#define FLW_NORM_KERNELS(K) \
-  {reinterpret_cast<const void*>(&K<1>), reinterpret_cast<const void*>(&K<2>), reinterpret_cast<const void*>(&K<3>), \
-   reinterpret_cast<const void*>(&K<4>), reinterpret_cast<const void*>(&K<6>), reinterpret_cast<const void*>(&K<8>), \
-   reinterpret_cast<const void*>(&K<12>), reinterpret_cast<const void*>(&K<16>)}
+#define FLW_NORM_KERNELS(K, B) \
+  {reinterpret_cast<const void*>(&K<1, B>), reinterpret_cast<const void*>(&K<2, B>),  \
+   reinterpret_cast<const void*>(&K<3, B>), reinterpret_cast<const void*>(&K<4, B>),  \
+   reinterpret_cast<const void*>(&K<6, B>), reinterpret_cast<const void*>(&K<8, B>),  \
+   reinterpret_cast<const void*>(&K<12, B>), reinterpret_cast<const void*>(&K<16, B>)}
 
 static const void* pick_nv(const void* const* table, int nv) {
   switch (nv) {
@@ -321,20 +353,40 @@ static int swiglu_check(const void* g, const void* u, int64_t rows, int64_t cols
 
 using namespace flw;
 
+static int rmsnorm_fwd_launch(const void* x, int64_t rows, int64_t cols, int64_t xs, const void* weight, float eps,
+                              void* h, int64_t hs, const void* a, int64_t as, void* sum, int64_t ss, void* stream,
+                              const char* name) {
+  int rc = norm_check(x, rows, cols, xs, weight, eps);
+  if (rc) return rc;
+  FLW_REQUIRE(h != nullptr && aligned16(h) && hs >= cols && hs % 8 == 0, FLW_E_INVALID,
+              "h must be 16-byte aligned rows with a stride >= cols");
+  if (a != nullptr)
+    FLW_REQUIRE(sum != nullptr && aligned16(a) && aligned16(sum) && as >= cols && as % 8 == 0 && ss >= cols &&
+                ss % 8 == 0, FLW_E_INVALID, "a and sum must be 16-byte aligned rows with strides >= cols");
+  if (rows == 0) return FLW_OK;
+  static const void* const plain[] = FLW_NORM_KERNELS(rmsnorm_fwd_kernel, false);
+  static const void* const added[] = FLW_NORM_KERNELS(rmsnorm_fwd_kernel, true);
+  const Timer tm = take_timer();
+  (void)launch_args(pick_nv(a != nullptr ? added : plain, norm_nv(cols)), dim3((unsigned)((rows + 3) / 4)),
+                    dim3(256), 0, static_cast<hipStream_t>(stream), tm.start, tm.stop,
+                    static_cast<const uint16_t*>(x), rows, (int)cols, xs, static_cast<const uint16_t*>(weight), eps,
+                    static_cast<uint16_t*>(h), hs, static_cast<const uint16_t*>(a), as, static_cast<uint16_t*>(sum),
+                    ss);
+  return check_launch(name);
+}
+
 extern "C" int flw_rmsnorm_fwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, const void* weight,
                                float eps, void* h, int64_t h_row_stride, void* stream) {
-  int rc = norm_check(x, rows, cols, x_row_stride, weight, eps);
-  if (rc) return rc;
-  FLW_REQUIRE(h != nullptr && aligned16(h) && h_row_stride >= cols && h_row_stride % 8 == 0, FLW_E_INVALID,
-              "h must be 16-byte aligned rows with a stride >= cols");
-  if (rows == 0) return FLW_OK;
-  static const void* const table[] = FLW_NORM_KERNELS(rmsnorm_fwd_kernel);
-  const Timer tm = take_timer();
-  (void)launch_args(pick_nv(table, norm_nv(cols)), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                    static_cast<hipStream_t>(stream), tm.start, tm.stop, static_cast<const uint16_t*>(x), rows,
-                    (int)cols, x_row_stride, static_cast<const uint16_t*>(weight), eps, static_cast<uint16_t*>(h),
-                    h_row_stride);
-  return check_launch("flw_rmsnorm_fwd");
+  return rmsnorm_fwd_launch(x, rows, cols, x_row_stride, weight, eps, h, h_row_stride, nullptr, 0, nullptr, 0,
+                            stream, "flw_rmsnorm_fwd");
+}
+
+extern "C" int flw_add_rmsnorm_fwd(const void* x, const void* a, int64_t rows, int64_t cols, int64_t x_row_stride,
+                                   int64_t a_row_stride, const void* weight, float eps, void* sum,
+                                   int64_t sum_row_stride, void* h, int64_t h_row_stride, void* stream) {
+  FLW_REQUIRE(a != nullptr && sum != nullptr, FLW_E_INVALID, "null pointer");
+  return rmsnorm_fwd_launch(x, rows, cols, x_row_stride, weight, eps, h, h_row_stride, a, a_row_stride, sum,
+                            sum_row_stride, stream, "flw_add_rmsnorm_fwd");
 }
 
 extern "C" size_t flw_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
@@ -343,14 +395,18 @@ extern "C" size_t flw_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
 }
 
 extern "C" int flw_rmsnorm_bwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, const void* weight,
-                               float eps, const void* dh, int64_t dh_row_stride, void* dx, int64_t dx_row_stride,
-                               void* dweight, void* workspace, size_t workspace_bytes, void* stream) {
+                               float eps, const void* dh, int64_t dh_row_stride, const void* dres,
+                               int64_t dres_row_stride, void* dx, int64_t dx_row_stride, void* dweight,
+                               void* workspace, size_t workspace_bytes, void* stream) {
   int rc = norm_check(x, rows, cols, x_row_stride, weight, eps);
   if (rc) return rc;
   FLW_REQUIRE(dh != nullptr && dx != nullptr && dweight != nullptr && aligned16(dh) && aligned16(dx),
               FLW_E_INVALID, "dh, dx must be 16-byte aligned and dweight non-null");
   FLW_REQUIRE(dh_row_stride >= cols && dh_row_stride % 8 == 0 && dx_row_stride >= cols && dx_row_stride % 8 == 0,
               FLW_E_INVALID, "gradient rows need a stride >= cols, a multiple of 8");
+  if (dres != nullptr)
+    FLW_REQUIRE(aligned16(dres) && dres_row_stride >= cols && dres_row_stride % 8 == 0, FLW_E_INVALID,
+                "dres must be 16-byte aligned rows with a stride >= cols");
   const size_t need = flw_rmsnorm_bwd_workspace_bytes(rows, cols);
   FLW_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace != nullptr && aligned16(workspace))),
               FLW_E_INVALID, "workspace needs %zu bytes (16-byte aligned), got %zu", need, workspace_bytes);
@@ -359,11 +415,13 @@ extern "C" int flw_rmsnorm_bwd(const void* x, int64_t rows, int64_t cols, int64_
   const Timer tm = take_timer();
   float* part = static_cast<float*>(workspace);
   if (nblk > 0) {
-    static const void* const table[] = FLW_NORM_KERNELS(rmsnorm_bwd_kernel);
-    (void)launch_args(pick_nv(table, norm_nv(cols)), dim3((unsigned)nblk), dim3(256), (size_t)(cols * 4), s,
-                      tm.start, nullptr, static_cast<const uint16_t*>(x), rows, (int)cols, x_row_stride,
-                      static_cast<const uint16_t*>(weight), eps, static_cast<const uint16_t*>(dh), dh_row_stride,
-                      static_cast<uint16_t*>(dx), dx_row_stride, part);
+    static const void* const plain[] = FLW_NORM_KERNELS(rmsnorm_bwd_kernel, false);
+    static const void* const withres[] = FLW_NORM_KERNELS(rmsnorm_bwd_kernel, true);
+    (void)launch_args(pick_nv(dres != nullptr ? withres : plain, norm_nv(cols)), dim3((unsigned)nblk), dim3(256),
+                      (size_t)(cols * 4), s, tm.start, nullptr, static_cast<const uint16_t*>(x), rows, (int)cols,
+                      x_row_stride, static_cast<const uint16_t*>(weight), eps, static_cast<const uint16_t*>(dh),
+                      dh_row_stride, static_cast<uint16_t*>(dx), dx_row_stride, part,
+                      static_cast<const uint16_t*>(dres), dres_row_stride);
   }
   (void)launch_args(reinterpret_cast<const void*>(&rmsnorm_dw_kernel), dim3((unsigned)((cols + 15) / 16)),
                     dim3(256), 0, s, nblk > 0 ? nullptr : tm.start, tm.stop, static_cast<const float*>(part), nblk,

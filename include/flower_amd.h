@@ -177,15 +177,23 @@ int flw_rmsnorm_fwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_str
 /* Bytes of fp32 workspace flw_rmsnorm_bwd needs for its weight-gradient partial sums. */
 size_t flw_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 
+/* x + a followed by RMSNorm, the residual add of Block.forward (flower/models/base.py:720) and the
+ * ln2 that reads its result (:721), in one pass: sum = bf16(x + a) [rows, cols] (written: the
+ * residual stream) and h = flw_rmsnorm_fwd of sum, bit for bit the two torch ops. */
+int flw_add_rmsnorm_fwd(const void* x, const void* a, int64_t rows, int64_t cols, int64_t x_row_stride,
+                        int64_t a_row_stride, const void* weight, float eps, void* sum, int64_t sum_row_stride,
+                        void* h, int64_t h_row_stride, void* stream);
+
 /* The backward of flw_rmsnorm_fwd as torch's autograd of base.py:337-338 computes it, from the
  * forward's x and weight and the gradient dh: dn = bf16(dh w),
  * dx = bf16(bf16(dn r) - bf16(x r^3 sum(dn x) / cols)) (the expression's two x.float() casts each
  * return a bf16 gradient, summed in bf16), dweight [cols] = bf16(sum over rows of bf16(dh n)),
- * n = bf16(x r), the sum in fp32 (over a fixed order: deterministic). Two launches; the workspace
- * holds partial sums only. */
+ * n = bf16(x r), the sum in fp32 (over a fixed order: deterministic). dres (may be NULL): the
+ * gradient x receives along the residual stream, added as autograd adds the two uses' gradients:
+ * dx = bf16(dres + that). Two launches; the workspace holds partial sums only. */
 int flw_rmsnorm_bwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, const void* weight, float eps,
-                    const void* dh, int64_t dh_row_stride, void* dx, int64_t dx_row_stride, void* dweight,
-                    void* workspace, size_t workspace_bytes, void* stream);
+                    const void* dh, int64_t dh_row_stride, const void* dres, int64_t dres_row_stride, void* dx,
+                    int64_t dx_row_stride, void* dweight, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The SwiGLU product of FeedForward.forward (flower/models/base.py:538-550, smooth_swiglu off) on
  * bf16 rows: h = bf16(bf16(silu(gate)) up), silu(g) = g / (1 + exp(-g)) in fp32 (torch's silu).

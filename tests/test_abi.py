@@ -298,8 +298,14 @@ def test_training_row_kernel_refusals_on_the_host():
     need = lib.flw_rmsnorm_bwd_workspace_bytes(1021, 1280)            # a workgroup per 4 rows
     assert need == 256 * 1280 * 4 and lib.flw_rmsnorm_bwd_workspace_bytes(0, 1280) == 0
     assert lib.flw_rmsnorm_bwd_workspace_bytes(1 << 20, 1280) == 512 * 1280 * 4   # at most 512
-    rc = lib.flw_rmsnorm_bwd(P, 1021, 1280, 1280, P, 1e-6, P, 1280, P, 1280, P, P, need - 16, None)
+    rc = lib.flw_rmsnorm_bwd(P, 1021, 1280, 1280, P, 1e-6, P, 1280, None, 0, P, 1280, P, P, need - 16, None)
     assert rc == 1 and b"workspace" in lib.flw_last_error()
+    rc = lib.flw_rmsnorm_bwd(P, 1021, 1280, 1280, P, 1e-6, P, 1280, P + 8, 1280, P, 1280, P, P, need, None)
+    assert rc == 1 and b"dres" in lib.flw_last_error()
+    rc = lib.flw_add_rmsnorm_fwd(P, None, 4, 64, 64, 64, P, 1e-6, P, 64, P, 64, None)
+    assert rc == 1 and b"null" in lib.flw_last_error()
+    rc = lib.flw_add_rmsnorm_fwd(P, P, 4, 64, 64, 32, P, 1e-6, P, 64, P, 64, None)
+    assert rc == 1 and b"strides" in lib.flw_last_error()
     rc = lib.flw_swiglu_fwd(P, P, 4, 20, 24, 24, P, 24, None)
     assert rc == 1 and b"multiple of 8" in lib.flw_last_error()
     rc = lib.flw_swiglu_bwd(P, P, 4, 64, 64, 64, P, 64, P, P + 4, 64, None)

@@ -96,7 +96,7 @@ def test_rmsnorm_empty_rows_give_zero_weight_gradient():
     w = torch.ones(64, dtype=torch.bfloat16, device="cuda")
     dw = torch.full((64,), 7.0, dtype=torch.bfloat16, device="cuda")
     s = _lib.stream_of(w)
-    _lib.check(lib.flw_rmsnorm_bwd(w.data_ptr(), 0, 64, 64, w.data_ptr(), EPS, w.data_ptr(), 64, w.data_ptr(), 64,
+    _lib.check(lib.flw_rmsnorm_bwd(w.data_ptr(), 0, 64, 64, w.data_ptr(), EPS, w.data_ptr(), 64, None, 0, w.data_ptr(), 64,
                                    dw.data_ptr(), None, 0, s), "rmsnorm bwd")
     _lib.check(lib.flw_rmsnorm_fwd(w.data_ptr(), 0, 64, 64, w.data_ptr(), EPS, w.data_ptr(), 64, s), "rmsnorm fwd")
     torch.cuda.synchronize()
@@ -128,3 +128,22 @@ def test_swiglu_forward_backward_against_oracle(B, T, cols, pad):
     _close(to_np(h), to_np(ht))
     _close(to_np(gg.grad), to_np(gt.grad), cancel=True)
     _close(to_np(uu.grad), to_np(ut.grad))
+
+
+def test_add_rmsnorm_and_residual_gradient_against_torch():
+    """flw_add_rmsnorm_fwd: s = bf16(x + a) bit for bit torch's add, h = the norm of s (the same
+    kernel arithmetic as flw_rmsnorm_fwd on s); flw_rmsnorm_bwd with dres: bf16(dres + the norm's
+    dx), bit for bit autograd's sum of the two bf16 gradients."""
+    from flower_amd import _lib
+    from flower_amd.block import _AddRMSNormFn, _RMSNormFn
+    x, w, dh = _norm_inputs(333, 1280, seed=21)
+    a, _, dres = _norm_inputs(333, 1280, seed=22)
+    xx, aa = x.detach().requires_grad_(True), a.detach().requires_grad_(True)
+    s, h = _AddRMSNormFn.apply(xx, aa, w, EPS)
+    assert torch.equal(s, x + a)
+    ss = (x + a).detach().requires_grad_(True)
+    h_ref = _RMSNormFn.apply(ss, w, EPS)
+    assert torch.equal(h, h_ref)
+    torch.autograd.backward((s, h), (dres, dh))
+    torch.autograd.backward((ss, h_ref), (dres, dh))       # autograd sums dres and the norm's dx
+    assert torch.equal(xx.grad, ss.grad) and torch.equal(aa.grad, ss.grad)

@@ -119,3 +119,29 @@ def test_fp8_block_forward_backward_against_fp32(recipe):
     assert _rel(gx, gx_ref) < 0.12
     for name, g in gp.items():
         assert _rel(g, gp_ref[name]) < 0.12, name
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_residual_norm_route_bit_identical_to_the_module_route(fp8):
+    """TransformerBlock.forward on bf16 GPU inputs (ln1 handing x on as the residual stream, the
+    first residual add inside ln2's pass, the residual gradients added in the norms' backward
+    passes) against the same block composed module by module with torch's adds and autograd's
+    gradient sums: output, input gradient and every parameter gradient equal bit for bit."""
+    blk, conf = _block()
+    if fp8:
+        from flower_amd.precision import convert_model_to_fp8
+        stack = nn.Module()
+        stack.blocks = nn.ModuleList([blk])
+        convert_model_to_fp8(stack, recipe="tensorwise", keep_bf16_blocks=0, verbose=False)
+        blk = stack.blocks[0]
+    x, dy = _inputs(conf)
+    y, gx, gp = _run(blk, x, dy)
+    blk.zero_grad(set_to_none=True)
+    xx = x.clone().requires_grad_(True)
+    h = xx + blk.attn(blk.ln1(xx))
+    y2 = h + blk.ff(blk.ln2(h))
+    y2.backward(dy)
+    assert torch.equal(y, y2.detach().float())
+    assert torch.equal(gx, xx.grad.float())
+    for n, p in blk.named_parameters():
+        assert torch.equal(gp[n], p.grad.float()), n
