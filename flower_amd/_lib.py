@@ -66,6 +66,8 @@ SIGNATURES = {
     "flw_quant_tensor_t_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "flw_quant_tensor_t_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                         c_void_p, c_void_p, c_size_t, c_void_p]),
+    "flw_quant_tensor_t_e4m3_amax": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                             c_void_p, c_int64, c_void_p, c_void_p]),
     "flw_rmsnorm_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64,
                                 c_void_p]),
     "flw_rmsnorm_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),
@@ -73,10 +75,11 @@ SIGNATURES = {
                                     c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "flw_rmsnorm_bwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64,
                                 c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "flw_swiglu_amax_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "flw_swiglu_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64,
-                               c_void_p]),
+                               c_void_p, c_void_p, c_size_t, c_void_p]),
     "flw_swiglu_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64,
-                               c_void_p, c_void_p, c_int64, c_void_p]),
+                               c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
     "flw_rmsnorm_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p,
                                             c_void_p, c_void_p, c_void_p]),
     "flw_gelu_quant_rows_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,

@@ -151,7 +151,7 @@ class _SwiGLUFn(torch.autograd.Function):
         rows, cols = g2.shape
         h = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
         _lib.check(lib.flw_swiglu_fwd(g2.data_ptr(), u2.data_ptr(), rows, cols, g2.stride(0), u2.stride(0),
-                                      h.data_ptr(), cols, _lib.stream_of(gate)), "SwiGLU")
+                                      h.data_ptr(), cols, None, None, 0, _lib.stream_of(gate)), "SwiGLU")
         ctx.save_for_backward(g2, u2)
         ctx.shape = gate.shape
         return h
@@ -165,9 +165,85 @@ class _SwiGLUFn(torch.autograd.Function):
         dg = torch.empty((rows, cols), dtype=g2.dtype, device=g2.device)
         du = torch.empty((rows, cols), dtype=g2.dtype, device=g2.device)
         _lib.check(lib.flw_swiglu_bwd(g2.data_ptr(), u2.data_ptr(), rows, cols, g2.stride(0), u2.stride(0),
-                                      d2.data_ptr(), d2.stride(0), dg.data_ptr(), du.data_ptr(), cols,
+                                      d2.data_ptr(), d2.stride(0), dg.data_ptr(), du.data_ptr(), cols, None, None, 0,
                                       _lib.stream_of(g2)), "SwiGLU backward")
         return dg.view(ctx.shape), du.view(ctx.shape)
+
+
+class _Fp8GatedFn(torch.autograd.Function):
+    """silu(gate(x)) * up(x) for two tensorwise Fp8Linears (base.py:538-550) as one autograd node,
+    returning (h, |h| max): x is cast once for both GEMMs (the two Linears would each compute the
+    same codes), the SwiGLU pass also takes h's maximum (so the down projection's cast of h skips
+    its amax pass), and the backward's SwiGLU pass takes dgate's and dup's maxima for their casts.
+    Every code, scale and GEMM is the one the two Fp8Linears and _SwiGLUFn compute, so the result
+    equals the module route bit for bit (the gradient sum for x included: bf16(dx_gate + dx_up))."""
+
+    @staticmethod
+    def forward(ctx, x, w_gate, w_up, gate_mod, up_mod):
+        from . import precision as P
+        lib = _lib.load()
+        x2 = _rows(x)
+        M, K = x2.shape
+        H = gate_mod.out_features
+        ld = ((M + 127) // 128) * 128
+        x8, x8t, sx = P._quantize_tensorwise_t(x2, ld)
+        wg8, swg = gate_mod.weight_codes()
+        wu8, swu = up_mod.weight_codes()
+        g = P.scaled_mm_plain(x8, sx, wg8, swg)
+        u = P.scaled_mm_plain(x8, sx, wu8, swu)
+        h = torch.empty((M, H), dtype=x.dtype, device=x.device)
+        amax = torch.empty(1, dtype=torch.int32, device=x.device)
+        ws = _lib.workspace(lib.flw_swiglu_amax_workspace_bytes(M, H), x.device)
+        _lib.check(lib.flw_swiglu_fwd(g.data_ptr(), u.data_ptr(), M, H, H, H, h.data_ptr(), H, amax.data_ptr(),
+                                      ws.data_ptr(), ws.numel(), _lib.stream_of(x)), "SwiGLU")
+        ctx.save_for_backward(g, u, x8t, sx, wg8, swg, wu8, swu)
+        ctx.mods, ctx.x_shape, ctx.ld = (gate_mod, up_mod), x.shape, ld
+        ctx.mark_non_differentiable(amax)
+        return h.view(*x.shape[:-1], H), amax
+
+    @staticmethod
+    def backward(ctx, dh, _amax_grad):
+        from . import precision as P
+        g, u, x8t, sx, wg8, swg, wu8, swu = ctx.saved_tensors
+        gate_mod, up_mod = ctx.mods
+        M, H = g.shape
+        lib = _lib.load()
+        d2 = _rows(dh.to(g.dtype))
+        dg = torch.empty((M, H), dtype=g.dtype, device=g.device)
+        du = torch.empty((M, H), dtype=g.dtype, device=g.device)
+        amax = torch.empty(2, dtype=torch.int32, device=g.device)
+        ws = _lib.workspace(lib.flw_swiglu_amax_workspace_bytes(M, H), g.device)
+        _lib.check(lib.flw_swiglu_bwd(g.data_ptr(), u.data_ptr(), M, H, H, H, d2.data_ptr(), d2.stride(0),
+                                      dg.data_ptr(), du.data_ptr(), H, amax.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      _lib.stream_of(g)), "SwiGLU backward")
+        dg8, dg8t, sdg = P._quantize_tensorwise_t(dg, ctx.ld, amax[0:1])
+        du8, du8t, sdu = P._quantize_tensorwise_t(du, ctx.ld, amax[1:2])
+
+        def w_cols(mod, w8, sw):                     # as _Fp8LinearFn's backward takes them
+            if getattr(mod, "_fp8_cached", None) is not None:
+                return mod.weight_col_codes()
+            return P.transpose_codes(w8, mod.out_features), sw
+        gx = gwg = gwu = None
+        if ctx.needs_input_grad[0]:
+            gx = (P.scaled_mm(dg8, sdg, *w_cols(gate_mod, wg8, swg))
+                  + P.scaled_mm(du8, sdu, *w_cols(up_mod, wu8, swu))).view(ctx.x_shape)
+        if ctx.needs_input_grad[1]:
+            gwg = P.scaled_mm(dg8t, sdg, x8t, sx).to(gate_mod.weight.dtype)
+        if ctx.needs_input_grad[2]:
+            gwu = P.scaled_mm(du8t, sdu, x8t, sx).to(up_mod.weight.dtype)
+        return gx, gwg, gwu, None, None
+
+
+def _fp8_gated_ok(x: torch.Tensor, ff) -> bool:
+    """The FeedForward's gate, up and down are bias-free tensorwise Fp8Linears with the FP8
+    backward and 16-aligned widths, x a non-empty bf16 GPU tensor, autocast off: _Fp8GatedFn's
+    route."""
+    from .precision import Fp8Linear
+    mods = (ff.gate, ff.up, ff.down)
+    return (x.is_cuda and x.dtype == torch.bfloat16 and x.numel() > 0 and not torch.is_autocast_enabled()
+            and all(type(m) is Fp8Linear and m.recipe == "tensorwise" and getattr(m, "backward_fp8", True)
+                    and m.bias is None and m.in_features % 16 == 0 and m.out_features % 16 == 0 for m in mods)
+            and ff.gate.out_features == ff.up.out_features and x.shape[-1] == ff.gate.in_features)
 
 
 def _hip_rows_ok(*ts: torch.Tensor) -> bool:
@@ -433,6 +509,9 @@ class FeedForward(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.activation == "gelu":
             return self.net(x)
+        if _fp8_gated_ok(x, self):
+            h, h_amax = _Fp8GatedFn.apply(x, self.gate.weight, self.up.weight, self.gate, self.up)
+            return self.down(h, x_amax=h_amax)
         gate, up = self.gate(x), self.up(x)
         if gate.numel() > 0 and _hip_rows_ok(gate, up):
             return self.down(_SwiGLUFn.apply(gate, up))

@@ -263,42 +263,121 @@ struct SwigluParams {
   int64_t gs, us, dhs, os;
   int cpr;                      // 16-byte chunks per row
   int total;                    // rows * cpr
+  uint32_t* part;               // with AMAX: [2][gridDim.x] per-workgroup |out0|, |out1| maxima
 };
 
-// One 16-byte chunk (8 values) of a row per thread, chunk index i -> (row i / cpr, chunk i % cpr).
-__global__ __launch_bounds__(256) void swiglu_fwd_kernel(SwigluParams p) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.total) return;
-  const int64_t m = i / p.cpr;
-  const int c = 8 * (i - (int)m * p.cpr);
-  float g[8], u[8], o[8];
-  Vec16<uint16_t>::load(p.g + m * p.gs + c, g);
-  Vec16<uint16_t>::load(p.u + m * p.us + c, u);
+constexpr int kSwigluBlocks = 2048;   // grid-stride workgroups (at most): rows of the amax partials
+
+// |value| maxima of 8 packed bf16 values as fp32 bit patterns (the amax pass's ordering: NaN above
+// inf), folded into m.
+__device__ __forceinline__ uint32_t absmax_bf16x8(uint4 w, uint32_t m) {
+  const uint32_t q[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = round_bf16(g[e] / (1.0f + expf(-g[e]))) * u[e];
-  *reinterpret_cast<uint4*>(p.out0 + m * p.os + c) = pack_bf16x8(o);
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t lo = (q[e] & 0x7FFFu) << 16, hi = q[e] & 0x7FFF0000u;
+    m = m > lo ? m : lo;
+    m = m > hi ? m : hi;
+  }
+  return m;
 }
 
-__global__ __launch_bounds__(256) void swiglu_bwd_kernel(SwigluParams p) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.total) return;
-  const int64_t m = i / p.cpr;
-  const int c = 8 * (i - (int)m * p.cpr);
-  float g[8], u[8], d[8], dg[8], du[8];
-  Vec16<uint16_t>::load(p.g + m * p.gs + c, g);
-  Vec16<uint16_t>::load(p.u + m * p.us + c, u);
-  Vec16<uint16_t>::load(p.dh + m * p.dhs + c, d);
+__device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float den = 1.0f + expf(-g[e]);       // silu's and sigmoid's 1 + exp(-g), one exp
-    const float s = round_bf16(g[e] / den);
-    const float ds = round_bf16(d[e] * u[e]);
-    du[e] = d[e] * s;
-    const float sig = 1.0f / den;
-    dg[e] = ds * sig * (1.0f + g[e] * (1.0f - sig));
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t t = (uint32_t)__shfl_xor((int)m, o, 64);
+    m = m > t ? m : t;
   }
-  *reinterpret_cast<uint4*>(p.out0 + m * p.os + c) = pack_bf16x8(dg);
-  *reinterpret_cast<uint4*>(p.out1 + m * p.os + c) = pack_bf16x8(du);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  uint32_t r = red[0];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) r = r > red[i] ? r : red[i];
+  return r;
+}
+
+// 16-byte chunks (8 values) of the rows with a grid stride, chunk index i -> (row i / cpr,
+// chunk i % cpr). With AMAX each workgroup also writes the |value| maxima of what it wrote.
+template <bool AMAX>
+__global__ __launch_bounds__(256) void swiglu_fwd_kernel(SwigluParams p) {
+  __shared__ uint32_t red[4];
+  uint32_t mx = 0;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < p.total; i += gridDim.x * 256) {
+    const int64_t m = i / p.cpr;
+    const int c = 8 * (i - (int)m * p.cpr);
+    float g[8], u[8], o[8];
+    Vec16<uint16_t>::load(p.g + m * p.gs + c, g);
+    Vec16<uint16_t>::load(p.u + m * p.us + c, u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = round_bf16(g[e] / (1.0f + expf(-g[e]))) * u[e];
+    const uint4 w = pack_bf16x8(o);
+    *reinterpret_cast<uint4*>(p.out0 + m * p.os + c) = w;
+    if (AMAX) mx = absmax_bf16x8(w, mx);
+  }
+  if (AMAX) {
+    mx = block_max_256(mx, red);
+    if (threadIdx.x == 0) p.part[blockIdx.x] = mx;
+  }
+}
+
+template <bool AMAX>
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(SwigluParams p) {
+  __shared__ uint32_t red[4];
+  uint32_t mg = 0, mu = 0;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < p.total; i += gridDim.x * 256) {
+    const int64_t m = i / p.cpr;
+    const int c = 8 * (i - (int)m * p.cpr);
+    float g[8], u[8], d[8], dg[8], du[8];
+    Vec16<uint16_t>::load(p.g + m * p.gs + c, g);
+    Vec16<uint16_t>::load(p.u + m * p.us + c, u);
+    Vec16<uint16_t>::load(p.dh + m * p.dhs + c, d);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float den = 1.0f + expf(-g[e]);     // silu's and sigmoid's 1 + exp(-g), one exp
+      const float s = round_bf16(g[e] / den);
+      const float ds = round_bf16(d[e] * u[e]);
+      du[e] = d[e] * s;
+      const float sig = 1.0f / den;
+      dg[e] = ds * sig * (1.0f + g[e] * (1.0f - sig));
+    }
+    const uint4 wg = pack_bf16x8(dg), wu = pack_bf16x8(du);
+    *reinterpret_cast<uint4*>(p.out0 + m * p.os + c) = wg;
+    *reinterpret_cast<uint4*>(p.out1 + m * p.os + c) = wu;
+    if (AMAX) {
+      mg = absmax_bf16x8(wg, mg);
+      mu = absmax_bf16x8(wu, mu);
+    }
+  }
+  if (AMAX) {
+    mg = block_max_256(mg, red);
+    __syncthreads();                               // red is reused
+    mu = block_max_256(mu, red);
+    if (threadIdx.x == 0) {
+      p.part[blockIdx.x] = mg;
+      p.part[gridDim.x + blockIdx.x] = mu;
+    }
+  }
+}
+
+// One workgroup of 1024 per array (blockIdx.x) folds n partial maxima into out[blockIdx.x].
+__global__ __launch_bounds__(1024) void fold_max_kernel(const uint32_t* __restrict__ part, int n,
+                                                        uint32_t* __restrict__ out) {
+  __shared__ uint32_t red[16];
+  const uint32_t* src = part + (int64_t)blockIdx.x * n;
+  uint32_t m = 0;
+  for (int i = threadIdx.x; i < n; i += 1024) m = m > src[i] ? m : src[i];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t t = (uint32_t)__shfl_xor((int)m, o, 64);
+    m = m > t ? m : t;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = red[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) r = r > red[i] ? r : red[i];
+    out[blockIdx.x] = r;
+  }
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -429,40 +508,79 @@ extern "C" int flw_rmsnorm_bwd(const void* x, int64_t rows, int64_t cols, int64_
   return check_launch("flw_rmsnorm_bwd");
 }
 
+static int swiglu_blocks(int64_t rows, int64_t cols) {
+  const int64_t total = rows * (cols / 8);
+  return (int)std::min<int64_t>((total + 255) / 256, kSwigluBlocks);
+}
+
+extern "C" size_t flw_swiglu_amax_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)(2 * swiglu_blocks(rows, cols) * 4);
+}
+
+// Launches `kernel` (the AMAX instance when amax_out is given, then the fold of its partials into
+// amax_out[0 .. nout - 1]).
+static int swiglu_launch(SwigluParams& p, const void* plain, const void* with_amax, int nout, uint32_t* amax_out,
+                         void* ws, size_t ws_bytes, int64_t rows, int64_t cols, void* stream, const char* name) {
+  const int blocks = swiglu_blocks(rows, cols);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (amax_out == nullptr) {
+    (void)launch_timed(plain, dim3((unsigned)blocks), dim3(256), s, p);
+    return check_launch(name);
+  }
+  const size_t need = flw_swiglu_amax_workspace_bytes(rows, cols);
+  FLW_REQUIRE(ws != nullptr && aligned16(ws) && ws_bytes >= need, FLW_E_WORKSPACE,
+              "workspace needs %zu bytes (16-byte aligned)", need);
+  p.part = static_cast<uint32_t*>(ws);
+  const Timer tm = take_timer();
+  (void)launch_ext(with_amax, dim3((unsigned)blocks), dim3(256), 0, s, p, tm.start, nullptr);
+  (void)launch_args(reinterpret_cast<const void*>(&fold_max_kernel), dim3((unsigned)nout), dim3(1024), 0, s,
+                    nullptr, tm.stop, static_cast<const uint32_t*>(p.part), blocks, amax_out);
+  return check_launch(name);
+}
+
 extern "C" int flw_swiglu_fwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
-                              int64_t up_row_stride, void* h, int64_t h_row_stride, void* stream) {
+                              int64_t up_row_stride, void* h, int64_t h_row_stride, uint32_t* h_amax,
+                              void* workspace, size_t workspace_bytes, void* stream) {
   int rc = swiglu_check(gate, up, rows, cols, gate_row_stride, up_row_stride);
   if (rc) return rc;
   FLW_REQUIRE(h != nullptr && aligned16(h) && h_row_stride >= cols && h_row_stride % 8 == 0, FLW_E_INVALID,
               "h must be 16-byte aligned rows with a stride >= cols");
-  if (rows == 0) return FLW_OK;
+  if (rows == 0) {
+    FLW_REQUIRE(h_amax == nullptr, FLW_E_INVALID, "no amax of an empty matrix");
+    return FLW_OK;
+  }
   SwigluParams p{};
   p.g = static_cast<const uint16_t*>(gate); p.u = static_cast<const uint16_t*>(up);
   p.out0 = static_cast<uint16_t*>(h);
   p.gs = gate_row_stride; p.us = up_row_stride; p.os = h_row_stride;
   p.cpr = (int)(cols / 8); p.total = (int)(rows * p.cpr);
-  (void)launch_timed(reinterpret_cast<const void*>(&swiglu_fwd_kernel), dim3((unsigned)((p.total + 255) / 256)),
-                     dim3(256), static_cast<hipStream_t>(stream), p);
-  return check_launch("flw_swiglu_fwd");
+  return swiglu_launch(p, reinterpret_cast<const void*>(&swiglu_fwd_kernel<false>),
+                       reinterpret_cast<const void*>(&swiglu_fwd_kernel<true>), 1, h_amax, workspace,
+                       workspace_bytes, rows, cols, stream, "flw_swiglu_fwd");
 }
 
 extern "C" int flw_swiglu_bwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
                               int64_t up_row_stride, const void* dh, int64_t dh_row_stride, void* dgate, void* dup,
-                              int64_t grad_row_stride, void* stream) {
+                              int64_t grad_row_stride, uint32_t* grad_amax, void* workspace, size_t workspace_bytes,
+                              void* stream) {
   int rc = swiglu_check(gate, up, rows, cols, gate_row_stride, up_row_stride);
   if (rc) return rc;
   FLW_REQUIRE(dh != nullptr && dgate != nullptr && dup != nullptr && aligned16(dh) && aligned16(dgate) &&
               aligned16(dup), FLW_E_INVALID, "dh, dgate, dup must be non-null and 16-byte aligned");
   FLW_REQUIRE(dh_row_stride >= cols && dh_row_stride % 8 == 0 && grad_row_stride >= cols && grad_row_stride % 8 == 0,
               FLW_E_INVALID, "gradient rows need a stride >= cols, a multiple of 8");
-  if (rows == 0) return FLW_OK;
+  if (rows == 0) {
+    FLW_REQUIRE(grad_amax == nullptr, FLW_E_INVALID, "no amax of an empty matrix");
+    return FLW_OK;
+  }
   SwigluParams p{};
   p.g = static_cast<const uint16_t*>(gate); p.u = static_cast<const uint16_t*>(up);
   p.dh = static_cast<const uint16_t*>(dh);
   p.out0 = static_cast<uint16_t*>(dgate); p.out1 = static_cast<uint16_t*>(dup);
   p.gs = gate_row_stride; p.us = up_row_stride; p.dhs = dh_row_stride; p.os = grad_row_stride;
   p.cpr = (int)(cols / 8); p.total = (int)(rows * p.cpr);
-  (void)launch_timed(reinterpret_cast<const void*>(&swiglu_bwd_kernel), dim3((unsigned)((p.total + 255) / 256)),
-                     dim3(256), static_cast<hipStream_t>(stream), p);
-  return check_launch("flw_swiglu_bwd");
+  return swiglu_launch(p, reinterpret_cast<const void*>(&swiglu_bwd_kernel<false>),
+                       reinterpret_cast<const void*>(&swiglu_bwd_kernel<true>), 2, grad_amax, workspace,
+                       workspace_bytes, rows, cols, stream, "flw_swiglu_bwd");
 }

@@ -1169,9 +1169,8 @@ extern "C" size_t flw_quant_tensor_t_workspace_bytes(int64_t rows, int64_t cols)
   return 16 + partial_bytes(1, 1, flat_rows);
 }
 
-extern "C" int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride, uint8_t* out8,
-                                       int64_t ld8, uint8_t* out_t, int64_t ldt, float* scale_out, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
+static int quant_t_check(const void* x, int64_t rows, int64_t cols, int64_t row_stride, const uint8_t* out8,
+                         int64_t ld8, const uint8_t* out_t, int64_t ldt, const float* scale_out) {
   FLW_REQUIRE(x != nullptr && out8 != nullptr && out_t != nullptr && scale_out != nullptr, FLW_E_INVALID,
               "null pointer");
   FLW_REQUIRE(rows > 0 && cols > 0, FLW_E_INVALID, "empty matrix");
@@ -1181,11 +1180,34 @@ extern "C" int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols
               "out8 rows must be 16-byte aligned with ld8 >= cols");
   FLW_REQUIRE(ldt >= rows && ldt % 16 == 0 && ((uintptr_t)out_t & 15) == 0, FLW_E_INVALID,
               "ld must be >= rows and a multiple of 16, out_t 16-byte aligned");
+  FLW_REQUIRE((cols + kTT - 1) / kTT <= 0x7FFFFFFF && (ldt + kTT - 1) / kTT <= 65535, FLW_E_UNSUPPORTED,
+              "matrix too large");
+  return FLW_OK;
+}
+
+extern "C" int flw_quant_tensor_t_e4m3_amax(const void* x, int64_t rows, int64_t cols, int64_t row_stride,
+                                            const uint32_t* amax, uint8_t* out8, int64_t ld8, uint8_t* out_t,
+                                            int64_t ldt, float* scale_out, void* stream) {
+  int rc = quant_t_check(x, rows, cols, row_stride, out8, ld8, out_t, ldt, scale_out);
+  if (rc) return rc;
+  FLW_REQUIRE(amax != nullptr, FLW_E_INVALID, "null amax");
+  const int64_t gx = (cols + kTT - 1) / kTT, gy = (ldt + kTT - 1) / kTT;
+  const Timer tm = take_timer();
+  (void)launch_args(reinterpret_cast<const void*>(&quant_tensor_t_kernel), dim3((unsigned)gx, (unsigned)gy),
+                    dim3(256), 0, static_cast<hipStream_t>(stream), tm.start, tm.stop,
+                    static_cast<const uint16_t*>(x), rows, cols, row_stride, amax, out8, ld8, out_t, ldt, scale_out);
+  return check_launch("flw_quant_tensor_t_e4m3_amax");
+}
+
+extern "C" int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride, uint8_t* out8,
+                                       int64_t ld8, uint8_t* out_t, int64_t ldt, float* scale_out, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  int rc = quant_t_check(x, rows, cols, row_stride, out8, ld8, out_t, ldt, scale_out);
+  if (rc) return rc;
   const size_t need = flw_quant_tensor_t_workspace_bytes(rows, cols);
   FLW_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0 && workspace_bytes >= need, FLW_E_WORKSPACE,
               "workspace needs %zu bytes (16-byte aligned)", need);
   const int64_t gx = (cols + kTT - 1) / kTT, gy = (ldt + kTT - 1) / kTT;
-  FLW_REQUIRE(gx <= 0x7FFFFFFF && gy <= 65535, FLW_E_UNSUPPORTED, "matrix too large");
   // The amax pass over the matrix as 64-value rows when it is contiguous (chunks of 128 such rows
   // spread over the GPU), else over its own rows; one workgroup of 1024 folds the partials.
   const bool flat = row_stride == cols && (rows * cols) % 64 == 0;

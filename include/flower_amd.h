@@ -197,16 +197,23 @@ int flw_rmsnorm_bwd(const void* x, int64_t rows, int64_t cols, int64_t x_row_str
 
 /* The SwiGLU product of FeedForward.forward (flower/models/base.py:538-550, smooth_swiglu off) on
  * bf16 rows: h = bf16(bf16(silu(gate)) up), silu(g) = g / (1 + exp(-g)) in fp32 (torch's silu).
- * gate, up, h [rows, cols] with their own row strides; cols a multiple of 8. */
+ * gate, up, h [rows, cols] with their own row strides; cols a multiple of 8. h_amax (may be
+ * NULL): also |h|'s maximum as an fp32 bit pattern (NaN above inf), the amax pass of the next FP8
+ * linear's tensorwise cast done by this pass (per-workgroup maxima in the workspace of
+ * flw_swiglu_amax_workspace_bytes, folded by a second launch). */
+size_t flw_swiglu_amax_workspace_bytes(int64_t rows, int64_t cols);
 int flw_swiglu_fwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
-                   int64_t up_row_stride, void* h, int64_t h_row_stride, void* stream);
+                   int64_t up_row_stride, void* h, int64_t h_row_stride, uint32_t* h_amax, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /* The backward of flw_swiglu_fwd as torch's autograd computes it: ds = bf16(dh up),
  * dup = bf16(dh s) with s = bf16(silu(gate)), dgate = bf16(ds sig (1 + g (1 - sig))),
- * sig = 1 / (1 + exp(-g)) (torch's silu backward). dgate and dup share grad_row_stride. */
+ * sig = 1 / (1 + exp(-g)) (torch's silu backward). dgate and dup share grad_row_stride.
+ * grad_amax (may be NULL): [2] the |dgate| and |dup| maxima, as flw_swiglu_fwd's h_amax. */
 int flw_swiglu_bwd(const void* gate, const void* up, int64_t rows, int64_t cols, int64_t gate_row_stride,
                    int64_t up_row_stride, const void* dh, int64_t dh_row_stride, void* dgate, void* dup,
-                   int64_t grad_row_stride, void* stream);
+                   int64_t grad_row_stride, uint32_t* grad_amax, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /* flw_quant_qkv_e4m3 without a workspace: no counterpart in the reference. For callers that
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
@@ -266,6 +273,12 @@ size_t flw_quant_tensor_t_workspace_bytes(int64_t rows, int64_t cols);
 int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols, int64_t row_stride, uint8_t* out8, int64_t ld8,
                             uint8_t* out_t, int64_t ldt, float* scale_out, void* workspace, size_t workspace_bytes,
                             void* stream);
+/* flw_quant_tensor_t_e4m3 with x's |x| maximum given (a device fp32 bit pattern from its producer,
+ * e.g. flw_swiglu_fwd's h_amax): the quantise-and-transpose pass alone, one launch. The codes are
+ * those of flw_quant_tensor_t_e4m3 when amax is |x|'s true maximum. */
+int flw_quant_tensor_t_e4m3_amax(const void* x, int64_t rows, int64_t cols, int64_t row_stride,
+                                 const uint32_t* amax, uint8_t* out8, int64_t ld8, uint8_t* out_t, int64_t ldt,
+                                 float* scale_out, void* stream);
 
 /* e4m3 codes [rows, cols] transposed to out_t [cols, ld] (ld >= rows, ld % 16 == 0; columns
  * rows .. ld - 1 of out_t zero). With one scale for the whole matrix (the tensorwise recipe) a

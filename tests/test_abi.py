@@ -306,12 +306,20 @@ def test_training_row_kernel_refusals_on_the_host():
     assert rc == 1 and b"null" in lib.flw_last_error()
     rc = lib.flw_add_rmsnorm_fwd(P, P, 4, 64, 64, 32, P, 1e-6, P, 64, P, 64, None)
     assert rc == 1 and b"strides" in lib.flw_last_error()
-    rc = lib.flw_swiglu_fwd(P, P, 4, 20, 24, 24, P, 24, None)
+    rc = lib.flw_swiglu_fwd(P, P, 4, 20, 24, 24, P, 24, None, None, 0, None)
     assert rc == 1 and b"multiple of 8" in lib.flw_last_error()
-    rc = lib.flw_swiglu_bwd(P, P, 4, 64, 64, 64, P, 64, P, P + 4, 64, None)
+    rc = lib.flw_swiglu_bwd(P, P, 4, 64, 64, 64, P, 64, P, P + 4, 64, None, None, 0, None)
     assert rc == 1 and b"aligned" in lib.flw_last_error()
-    rc = lib.flw_swiglu_fwd(P, P, 1 << 28, 128, 128, 128, P, 128, None)
+    rc = lib.flw_swiglu_fwd(P, P, 1 << 28, 128, 128, 128, P, 128, None, None, 0, None)
     assert rc == 2 and b"too many" in lib.flw_last_error()
+    need = lib.flw_swiglu_amax_workspace_bytes(16384, 3392)                 # 2 x 2048 workgroups
+    assert need == 2 * 2048 * 4 and lib.flw_swiglu_amax_workspace_bytes(2, 64) == 2 * 1 * 4
+    rc = lib.flw_swiglu_fwd(P, P, 16384, 3392, 3392, 3392, P, 3392, P, P, need - 4, None)
+    assert rc == 3 and b"workspace" in lib.flw_last_error()
+    rc = lib.flw_swiglu_bwd(P, P, 0, 64, 64, 64, P, 64, P, P, 64, P, P, 64, None)
+    assert rc == 1 and b"empty" in lib.flw_last_error()
+    rc = lib.flw_quant_tensor_t_e4m3_amax(P, 64, 64, 64, None, P, 64, P, 64, P, None)
+    assert rc == 1 and b"null amax" in lib.flw_last_error()
     need = lib.flw_quant_tensor_t_workspace_bytes(1000, 1280)              # 16 + one u32 per chunk
     assert need == 16 + 4 * ((1000 * 1280 // 64 + 127) // 128)
     rc = lib.flw_quant_tensor_t_e4m3(P, 1000, 1288, 1288, P, 1288, P, 1024, P, P, need, None)

@@ -147,3 +147,44 @@ def test_add_rmsnorm_and_residual_gradient_against_torch():
     torch.autograd.backward((s, h), (dres, dh))
     torch.autograd.backward((ss, h_ref), (dres, dh))       # autograd sums dres and the norm's dx
     assert torch.equal(xx.grad, ss.grad) and torch.equal(aa.grad, ss.grad)
+
+
+def test_swiglu_amax_outputs_equal_the_maxima_of_what_they_wrote():
+    """flw_swiglu_fwd's h_amax and flw_swiglu_bwd's [|dgate|, |dup|] maxima: the fp32 bit patterns
+    of max |x| over the tensors they wrote (the amax pass's value), the tensors themselves equal to
+    the calls without them; a NaN in gate makes the maxima NaN (0x7FC00000, above inf)."""
+    from flower_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(31)
+    M, H = 1000, 3392
+    gate = (torch.randn(M, H, generator=g) * 3).to("cuda", torch.bfloat16)
+    up = torch.randn(M, H, generator=g).to("cuda", torch.bfloat16)
+    dh = torch.randn(M, H, generator=g).to("cuda", torch.bfloat16)
+    s = _lib.stream_of(gate)
+    ws = _lib.workspace(lib.flw_swiglu_amax_workspace_bytes(M, H), "cuda")
+
+    def bits(t):
+        return int(t.float().abs().max().view(torch.int32).item())
+    for nan in (False, True):
+        if nan:
+            gate[17, 5] = float("nan")
+        h0, h1 = torch.empty_like(gate), torch.empty_like(gate)
+        am = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+        _lib.check(lib.flw_swiglu_fwd(gate.data_ptr(), up.data_ptr(), M, H, H, H, h0.data_ptr(), H, None, None, 0, s), "f")
+        _lib.check(lib.flw_swiglu_fwd(gate.data_ptr(), up.data_ptr(), M, H, H, H, h1.data_ptr(), H, am.data_ptr(),
+                                      ws.data_ptr(), ws.numel(), s), "f amax")
+        dg0, du0, dg1, du1 = (torch.empty_like(gate) for _ in range(4))
+        am2 = torch.full((2,), -1, dtype=torch.int32, device="cuda")
+        _lib.check(lib.flw_swiglu_bwd(gate.data_ptr(), up.data_ptr(), M, H, H, H, dh.data_ptr(), H, dg0.data_ptr(),
+                                      du0.data_ptr(), H, None, None, 0, s), "b")
+        _lib.check(lib.flw_swiglu_bwd(gate.data_ptr(), up.data_ptr(), M, H, H, H, dh.data_ptr(), H, dg1.data_ptr(),
+                                      du1.data_ptr(), H, am2.data_ptr(), ws.data_ptr(), ws.numel(), s), "b amax")
+        torch.cuda.synchronize()
+        assert torch.equal(h0.view(torch.int16), h1.view(torch.int16))
+        assert torch.equal(dg0.view(torch.int16), dg1.view(torch.int16))
+        assert torch.equal(du0.view(torch.int16), du1.view(torch.int16))
+        if nan:
+            assert int(am.item()) == 0x7FC00000 and int(am2[0].item()) == 0x7FC00000
+        else:
+            assert int(am.item()) == bits(h1)
+            assert int(am2[0].item()) == bits(dg1) and int(am2[1].item()) == bits(du1)

@@ -125,8 +125,11 @@ def test_fp8_block_forward_backward_against_fp32(recipe):
 def test_residual_norm_route_bit_identical_to_the_module_route(fp8):
     """TransformerBlock.forward on bf16 GPU inputs (ln1 handing x on as the residual stream, the
     first residual add inside ln2's pass, the residual gradients added in the norms' backward
-    passes) against the same block composed module by module with torch's adds and autograd's
-    gradient sums: output, input gradient and every parameter gradient equal bit for bit."""
+    passes; with tensorwise FP8 Linears also the fused gate / up / SwiGLU node that casts x once
+    and takes the amax of h, dgate and dup in the SwiGLU passes) against the same block composed
+    module by module -- each Linear on its own, _SwiGLUFn, torch's adds and autograd's gradient
+    sums: output, input gradient and every parameter gradient equal bit for bit."""
+    from flower_amd.block import _SwiGLUFn
     blk, conf = _block()
     if fp8:
         from flower_amd.precision import convert_model_to_fp8
@@ -139,7 +142,8 @@ def test_residual_norm_route_bit_identical_to_the_module_route(fp8):
     blk.zero_grad(set_to_none=True)
     xx = x.clone().requires_grad_(True)
     h = xx + blk.attn(blk.ln1(xx))
-    y2 = h + blk.ff(blk.ln2(h))
+    t = blk.ln2(h)
+    y2 = h + blk.ff.down(_SwiGLUFn.apply(blk.ff.gate(t), blk.ff.up(t)))
     y2.backward(dy)
     assert torch.equal(y, y2.detach().float())
     assert torch.equal(gx, xx.grad.float())
