@@ -266,19 +266,19 @@ struct SwigluParams {
   uint32_t* part;               // with AMAX: [2][gridDim.x] per-workgroup |out0|, |out1| maxima
 };
 
-constexpr int kSwigluBlocks = 2048;   // grid-stride workgroups (at most): rows of the amax partials
+constexpr int kSwigluBlocks = 8192;   // grid-stride workgroups (at most): rows of the amax partials
 
-// |value| maxima of 8 packed bf16 values as fp32 bit patterns (the amax pass's ordering: NaN above
-// inf), folded into m.
-__device__ __forceinline__ uint32_t absmax_bf16x8(uint4 w, uint32_t m) {
-  const uint32_t q[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t lo = (q[e] & 0x7FFFu) << 16, hi = q[e] & 0x7FFF0000u;
-    m = m > lo ? m : lo;
-    m = m > hi ? m : hi;
-  }
-  return m;
+// |value| maxima of 8 packed bf16 values folded into two 16-bit lanes (v_pk_max_u16 over the bit
+// patterns with the sign cleared: the amax pass's ordering, NaN above inf); as_f32_bits widens the
+// larger lane to the fp32 bit pattern of that bf16 value.
+__device__ __forceinline__ flw_u16x2 absmax_bf16x8(uint4 w, flw_u16x2 m) {
+  m = abs_max_bf16x2(m, w.x);
+  m = abs_max_bf16x2(m, w.y);
+  m = abs_max_bf16x2(m, w.z);
+  return abs_max_bf16x2(m, w.w);
+}
+__device__ __forceinline__ uint32_t as_f32_bits(flw_u16x2 m) {
+  return (uint32_t)(m[0] > m[1] ? m[0] : m[1]) << 16;
 }
 
 __device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
@@ -300,7 +300,8 @@ __device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
 template <bool AMAX>
 __global__ __launch_bounds__(256) void swiglu_fwd_kernel(SwigluParams p) {
   __shared__ uint32_t red[4];
-  uint32_t mx = 0;
+  flw_u16x2 mx = {0, 0};
+#pragma unroll 2
   for (int i = blockIdx.x * 256 + threadIdx.x; i < p.total; i += gridDim.x * 256) {
     const int64_t m = i / p.cpr;
     const int c = 8 * (i - (int)m * p.cpr);
@@ -314,15 +315,16 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(SwigluParams p) {
     if (AMAX) mx = absmax_bf16x8(w, mx);
   }
   if (AMAX) {
-    mx = block_max_256(mx, red);
-    if (threadIdx.x == 0) p.part[blockIdx.x] = mx;
+    const uint32_t m = block_max_256(as_f32_bits(mx), red);
+    if (threadIdx.x == 0) p.part[blockIdx.x] = m;
   }
 }
 
 template <bool AMAX>
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(SwigluParams p) {
   __shared__ uint32_t red[4];
-  uint32_t mg = 0, mu = 0;
+  flw_u16x2 mg = {0, 0}, mu = {0, 0};
+#pragma unroll 2
   for (int i = blockIdx.x * 256 + threadIdx.x; i < p.total; i += gridDim.x * 256) {
     const int64_t m = i / p.cpr;
     const int c = 8 * (i - (int)m * p.cpr);
@@ -348,12 +350,12 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(SwigluParams p) {
     }
   }
   if (AMAX) {
-    mg = block_max_256(mg, red);
+    const uint32_t a = block_max_256(as_f32_bits(mg), red);
     __syncthreads();                               // red is reused
-    mu = block_max_256(mu, red);
+    const uint32_t b = block_max_256(as_f32_bits(mu), red);
     if (threadIdx.x == 0) {
-      p.part[blockIdx.x] = mg;
-      p.part[gridDim.x + blockIdx.x] = mu;
+      p.part[blockIdx.x] = a;
+      p.part[gridDim.x + blockIdx.x] = b;
     }
   }
 }

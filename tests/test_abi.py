@@ -312,8 +312,8 @@ def test_training_row_kernel_refusals_on_the_host():
     assert rc == 1 and b"aligned" in lib.flw_last_error()
     rc = lib.flw_swiglu_fwd(P, P, 1 << 28, 128, 128, 128, P, 128, None, None, 0, None)
     assert rc == 2 and b"too many" in lib.flw_last_error()
-    need = lib.flw_swiglu_amax_workspace_bytes(16384, 3392)                 # 2 x 2048 workgroups
-    assert need == 2 * 2048 * 4 and lib.flw_swiglu_amax_workspace_bytes(2, 64) == 2 * 1 * 4
+    need = lib.flw_swiglu_amax_workspace_bytes(16384, 3392)                 # 2 x 8192 workgroups
+    assert need == 2 * 8192 * 4 and lib.flw_swiglu_amax_workspace_bytes(2, 64) == 2 * 1 * 4
     rc = lib.flw_swiglu_fwd(P, P, 16384, 3392, 3392, 3392, P, 3392, P, P, need - 4, None)
     assert rc == 3 and b"workspace" in lib.flw_last_error()
     rc = lib.flw_swiglu_bwd(P, P, 0, 64, 64, 64, P, 64, P, P, 64, P, P, 64, None)
