@@ -5,7 +5,8 @@ allocator), never synchronise with the host and record no memset nodes (buffers 
 at zero are cleared by a fill kernel), so ``torch.cuda.CUDAGraph`` can capture them as they are.
 Each test captures one operator family -- the FP8 attention operator (the Q / K / V quantise pair
 and the attention kernel), the FP8 linear in each recipe, the FP8 decoder block forward inside
-``fp8_weight_cache``, the bf16 sliding-window attention forward -- then replays the graph several
+``fp8_weight_cache``, the bf16 sliding-window attention forward, a whole training step of the block
+(forward and backward) -- then replays the graph several
 times with new values copied into the captured inputs, running the same operator eagerly on those
 values and synchronising between the replays, and compares every replay with that eager call bit
 for bit.
@@ -112,3 +113,34 @@ def test_bf16_swa_forward_in_a_graph():
     with torch.no_grad():
         graph, out = _capture(lambda: swa_attention(q, k, v, W))
         _replay_and_compare(graph, out, (q, k, v), make, lambda a, b, c: swa_attention(a, b, c, W))
+
+
+@pytest.mark.parametrize("recipe", [None, "tensorwise"])
+def test_training_block_step_in_a_graph(recipe):
+    """One training step of the block (flower_amd.block.TransformerBlock: the HIP row kernels, the
+    bf16 attention's forward and backward, FP8 or bf16 Linears; forward, then torch.autograd.grad of
+    the input and every parameter) captured whole, replayed on new inputs: output and gradients
+    equal the eager step's bit for bit."""
+    import torch.nn as nn
+    from flower_amd.block import TransformerBlock, block_config, init_block_
+    from flower_amd.precision import convert_model_to_fp8
+    conf = block_config(d_model=256, num_heads=4, ffn_dim=1536, local_window=96, max_seq_len=512)
+    blk = init_block_(TransformerBlock(conf), std=0.05, seed=3).to("cuda", torch.bfloat16)
+    if recipe is not None:
+        stack = nn.Module()
+        stack.blocks = nn.ModuleList([blk])
+        convert_model_to_fp8(stack, recipe=recipe, keep_bf16_blocks=0, verbose=False)
+        blk = stack.blocks[0]
+    params = list(blk.parameters())
+    shape = (2, 200, 256)
+
+    def make(i):
+        return [_seeded(shape, 600 + 10 * i), _seeded(shape, 601 + 10 * i)]
+
+    def step(x, dy):
+        xx = x.detach().requires_grad_(True)
+        y = blk(xx)[0]
+        return [y.detach()] + list(torch.autograd.grad(y, [xx] + params, dy))
+    x, dy = make(99)
+    graph, out = _capture(lambda: step(x, dy))
+    _replay_and_compare(graph, out, (x, dy), make, step)
