@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libflower_amd.so")
 
 F32, BF16 = 0, 1
 SCALE_TENSOR, SCALE_HEAD, SCALE_BH, SCALE_COLUMN = 0, 1, 2, 3
-LAYOUT_BHTD, LAYOUT_VTILE = 0, 1
+LAYOUT_BHTD, LAYOUT_VTILE, LAYOUT_BTHD = 0, 1, 2
 GEMM_A8W8, GEMM_W8A16 = 0, 1
 
 GRANULARITY = {"tensor": SCALE_TENSOR, "head": SCALE_HEAD, "bh": SCALE_BH}
@@ -113,6 +113,11 @@ SIGNATURES = {
                                               c_void_p, c_void_p, c_size_t, c_void_p]),
     "flw_swa_bf16_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                                  c_void_p, c_void_p, c_void_p]),
+    "flw_swa_bf16_fwd_layout": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                        c_int64, c_void_p, c_int, c_void_p, c_void_p]),
+    "flw_swa_bf16_bwd_layout": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int64,
+                                        c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_size_t, c_void_p]),
     "flw_swa_bf16_bwd_workspace_bytes": (c_size_t, [c_int64] * 4),
     "flw_swa_bf16_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                  c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,

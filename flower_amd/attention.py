@@ -277,7 +277,8 @@ class CausalSelfAttention(nn.Module):
                 return self._forward_fp8_train(x)
             return self._forward_fp8(x, trace)
         q, k, v = self.qkv_heads(x)
-        out = swa_attention(q, k, v, self._window(x.shape[1]))
+        # token-major O: the transpose back to [B, T, H D] rows below is a view, in both directions
+        out = swa_attention(q, k, v, self._window(x.shape[1]), token_major=q.dtype == torch.bfloat16)
         return self.out(out.transpose(1, 2).reshape(x.shape))
 
     def _forward_fp8(self, x: torch.Tensor, trace: dict | None = None) -> torch.Tensor:

@@ -64,7 +64,18 @@ struct SwaB16Params {
   int group_slices;       // slices per dispatch group (one XCD's share when it is whole slices)
   float sm_scale;
   int64_t rows;           // B * H * T (delta kernel)
+  int o_tmaj;             // O and dO token-major, (B, T, H, D): rows of a (b, h) slice H D apart
 };
+
+// O / dO of slice (b, h) = bh: its first row and its row stride in elements. Head-major (B, H, T, D)
+// slices are contiguous; token-major (B, T, H, D) slices interleave with the other heads, which is
+// the layout the output projection reads as [B T, H D] rows.
+__device__ __forceinline__ int64_t o_base(const SwaB16Params& p, int bh, int D) {
+  if (!p.o_tmaj) return (int64_t)bh * p.T * D;
+  const int b = bh / p.H, h = bh - b * p.H;
+  return ((int64_t)b * p.T * p.H + h) * D;
+}
+__device__ __forceinline__ int o_ld(const SwaB16Params& p, int D) { return p.o_tmaj ? p.H * D : D; }
 
 // ---------------------------------------------------------------- LDS tile layouts
 //
@@ -101,13 +112,17 @@ struct TileLoadLds {
   static constexpr int NI = 64 / RPI / 4;           // instructions per wave per tile
   __amdgpu_buffer_rsrc_t rs;
   uint32_t off[NI];
-  __device__ __forceinline__ void init(const uint16_t* base, int T, int wave, int lane) {
-    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, T * D * 2, kBufferFlags);
+  uint32_t row_bytes;
+  // Rows of D values `ld` elements apart (ld = D: a contiguous slice); rows past T read as zeros
+  // (the descriptor ends with row T - 1).
+  __device__ __forceinline__ void init(const uint16_t* base, int T, int wave, int lane, int ld = D) {
+    row_bytes = (uint32_t)ld * 2;
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, (T - 1) * ld * 2 + 2 * D, kBufferFlags);
 #pragma unroll
     for (int t = 0; t < NI; ++t) {
       const int r = RPI * (NI * wave + t) + lane / CPR, slot = lane % CPR;
       const int c = (nat_off<D>(r, slot) - r * 2 * D) / 16;
-      off[t] = (uint32_t)(r * 2 * D + 16 * c);
+      off[t] = (uint32_t)r * row_bytes + 16 * c;
     }
   }
   __device__ __forceinline__ void load(uint8_t* lds, int row0, int wave) const {
@@ -115,7 +130,7 @@ struct TileLoadLds {
     for (int t = 0; t < NI; ++t) {
       const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(lds + RPI * (NI * wave + t) * 2 * D);
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                   :: "s"(dst), "v"(off[t] + (uint32_t)(row0 * 2 * D)), "s"(rs) : "memory", "m0");
+                   :: "s"(dst), "v"(off[t] + (uint32_t)row0 * row_bytes), "s"(rs) : "memory", "m0");
     }
   }
 };
@@ -148,9 +163,9 @@ __device__ __forceinline__ v8bf trr_frag(const uint8_t* lds, int db, int g, int 
 }
 // Fragment of a row of global memory: 8 dims 16 ks + 8 h of row `row` (zero past T).
 template <int D>
-__device__ __forceinline__ v8bf row_frag(const uint16_t* base, int row, int T, int ks, int lane) {
+__device__ __forceinline__ v8bf row_frag(const uint16_t* base, int row, int T, int ks, int lane, int ld = D) {
   if (row >= T) return as_v8bf(make_uint4(0, 0, 0, 0));
-  return as_v8bf(*reinterpret_cast<const uint4*>(base + (int64_t)row * D + 16 * ks + 8 * (lane >> 5)));
+  return as_v8bf(*reinterpret_cast<const uint4*>(base + (int64_t)row * ld + 16 * ks + 8 * (lane >> 5)));
 }
 
 // The 16 values of a 32x32 C block, packed to bf16 as the B (or A) operand of the next product
@@ -324,7 +339,7 @@ __global__ __launch_bounds__(256, 2) void swa_bf16_fwd_kernel(SwaB16Params p) {
   const int qi = q0 + qc;
   if (qi < T) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    uint16_t* op = p.out + slice + (int64_t)qi * D;
+    uint16_t* op = p.out + o_base(p, bh, D) + (int64_t)qi * o_ld(p, D);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -353,9 +368,15 @@ __global__ __launch_bounds__(256) void swa_bf16_delta_kernel(SwaB16Params p) {
   const int part = (int)(gid % LPR);
   float s = 0.0f;
   if (row < rows) {
+    // row = (b H + h) T + t of the (B, H, T) statistics; O / dO's element offset of that row
+    int64_t at = row * D;
+    if (p.o_tmaj) {
+      const int64_t bh = row / p.T, t = row - bh * p.T;
+      at = o_base(p, (int)bh, D) + t * o_ld(p, D);
+    }
     float a[8], b[8];
-    Vec16<uint16_t>::load(o + row * D + 8 * part, a);
-    Vec16<uint16_t>::load(dout + row * D + 8 * part, b);
+    Vec16<uint16_t>::load(o + at + 8 * part, a);
+    Vec16<uint16_t>::load(dout + at + 8 * part, b);
 #pragma unroll
     for (int e = 0; e < 8; ++e) s = fmaf(a[e], b[e], s);
   }
@@ -408,7 +429,7 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void swa_bf16_dkdv_kernel(Sw
   // the 32 x 32 blocks it cuts.
   TileLoadLds<D> tq, tdo;
   tq.init(p.q + slice, T, wave, lane);
-  tdo.init(p.dout + slice, T, wave, lane);
+  tdo.init(p.dout + o_base(p, bh, D), T, wave, lane, o_ld(p, D));
   // Wave 0 carries L of the tile's 64 queries (stored as -L log2(e)), wave 1 their Delta; both
   // through buffer descriptors over the slice's T values, so queries past T read as 0.
   const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(LSE), 0, T * 4, kBufferFlags);
@@ -528,7 +549,7 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 3) void swa_bf16_dq_kernel(SwaB
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     qf[ks] = row_frag<D>(p.q + slice, qi, T, ks, lane);
-    df[ks] = row_frag<D>(p.dout + slice, qi, T, ks, lane);
+    df[ks] = row_frag<D>(p.dout + o_base(p, bh, D), qi, T, ks, lane, o_ld(p, D));
   }
   v16f dq[NDB];
 #pragma unroll
@@ -641,13 +662,24 @@ static int group_slices(int64_t slices, int nwg) {
 
 using namespace flw;
 
-extern "C" int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H,
-                                int64_t T, int64_t D, int64_t window, void* out, float* lse,
-                                void* stream) {
+static int o_layout_check(int layout, int64_t B, int64_t H, int64_t T, int64_t D) {
+  FLW_REQUIRE(layout == FLW_LAYOUT_BHTD || layout == FLW_LAYOUT_BTHD, FLW_E_INVALID,
+              "out layout must be FLW_LAYOUT_BHTD or FLW_LAYOUT_BTHD, got %d", layout);
+  FLW_REQUIRE(layout == FLW_LAYOUT_BHTD || T * H * D * 2 <= 0x7FFFFFFFll, FLW_E_UNSUPPORTED,
+              "a (B, T, H, D) slice must span < 2^31 bytes");
+  (void)B;
+  return FLW_OK;
+}
+
+static int swa_bf16_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t T, int64_t D,
+                        int64_t window, void* out, int out_layout, float* lse, void* stream, const char* name) {
   int rc = check_b16(q, k, v, B, H, T, D, window);
+  if (rc) return rc;
+  rc = o_layout_check(out_layout, B, H, T, D);
   if (rc) return rc;
   FLW_REQUIRE(out && lse && ((uintptr_t)out & 15) == 0, FLW_E_INVALID, "out / lse");
   SwaB16Params p{};
+  p.o_tmaj = out_layout == FLW_LAYOUT_BTHD;
   p.q = static_cast<const uint16_t*>(q); p.k = static_cast<const uint16_t*>(k); p.v = static_cast<const uint16_t*>(v);
   p.out = static_cast<uint16_t*>(out); p.lse = lse;
   p.H = (int)H; p.T = (int)T; p.W = (int)(window < T ? window : T);
@@ -661,7 +693,19 @@ extern "C" int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int
                  : D == 64 ? reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<64>)
                            : reinterpret_cast<const void*>(&swa_bf16_fwd_kernel<128>);
   (void)launch_timed(kf, grid, dim3(256), s, p);
-  return check_launch("flw_swa_bf16_fwd");
+  return check_launch(name);
+}
+
+extern "C" int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H,
+                                int64_t T, int64_t D, int64_t window, void* out, float* lse,
+                                void* stream) {
+  return swa_bf16_fwd(q, k, v, B, H, T, D, window, out, FLW_LAYOUT_BHTD, lse, stream, "flw_swa_bf16_fwd");
+}
+
+extern "C" int flw_swa_bf16_fwd_layout(const void* q, const void* k, const void* v, int64_t B, int64_t H,
+                                       int64_t T, int64_t D, int64_t window, void* out, int out_layout, float* lse,
+                                       void* stream) {
+  return swa_bf16_fwd(q, k, v, B, H, T, D, window, out, out_layout, lse, stream, "flw_swa_bf16_fwd_layout");
 }
 
 extern "C" size_t flw_swa_bf16_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
@@ -669,11 +713,13 @@ extern "C" size_t flw_swa_bf16_bwd_workspace_bytes(int64_t B, int64_t H, int64_t
   return (size_t)(B * H * T) * sizeof(float);
 }
 
-extern "C" int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, const void* out,
-                                const void* dout, const float* lse, int64_t B, int64_t H, int64_t T,
-                                int64_t D, int64_t window, void* dq, void* dk, void* dv,
-                                void* workspace, size_t workspace_bytes, void* stream) {
+static int swa_bf16_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                        int o_layout, const float* lse, int64_t B, int64_t H, int64_t T, int64_t D, int64_t window,
+                        void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, void* stream,
+                        const char* name) {
   int rc = check_b16(q, k, v, B, H, T, D, window);
+  if (rc) return rc;
+  rc = o_layout_check(o_layout, B, H, T, D);
   if (rc) return rc;
   FLW_REQUIRE(out && dout && lse && dq && dk && dv, FLW_E_INVALID, "null pointer argument");
   FLW_REQUIRE(((uintptr_t)out & 15) == 0 && ((uintptr_t)dout & 15) == 0 && ((uintptr_t)dq & 15) == 0 &&
@@ -683,6 +729,7 @@ extern "C" int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, con
   SwaB16Params p{};
   p.q = static_cast<const uint16_t*>(q); p.k = static_cast<const uint16_t*>(k); p.v = static_cast<const uint16_t*>(v);
   p.o = static_cast<const uint16_t*>(out); p.dout = static_cast<const uint16_t*>(dout);
+  p.o_tmaj = o_layout == FLW_LAYOUT_BTHD;
   p.lse = const_cast<float*>(lse); p.delta = static_cast<float*>(workspace);
   p.H = (int)H; p.T = (int)T; p.W = (int)(window < T ? window : T);
   p.nblk = (int)((T + 127) / 128); p.nwg = (int)(B * H * p.nblk);
@@ -712,5 +759,21 @@ extern "C" int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, con
   (void)launch_ext(kd, dgrid, dim3(256), 0, s, p, tm.start, nullptr);
   (void)launch_ext(kk, grid, dim3(256), 0, s, pk, nullptr, nullptr);
   (void)launch_ext(kq, grid, dim3(256), 0, s, pq, nullptr, tm.stop);
-  return check_launch("flw_swa_bf16_bwd");
+  return check_launch(name);
+}
+
+extern "C" int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, const void* out,
+                                const void* dout, const float* lse, int64_t B, int64_t H, int64_t T,
+                                int64_t D, int64_t window, void* dq, void* dk, void* dv,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  return swa_bf16_bwd(q, k, v, out, dout, FLW_LAYOUT_BHTD, lse, B, H, T, D, window, dq, dk, dv, workspace,
+                      workspace_bytes, stream, "flw_swa_bf16_bwd");
+}
+
+extern "C" int flw_swa_bf16_bwd_layout(const void* q, const void* k, const void* v, const void* out,
+                                       const void* dout, int o_layout, const float* lse, int64_t B, int64_t H,
+                                       int64_t T, int64_t D, int64_t window, void* dq, void* dk, void* dv,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  return swa_bf16_bwd(q, k, v, out, dout, o_layout, lse, B, H, T, D, window, dq, dk, dv, workspace,
+                      workspace_bytes, stream, "flw_swa_bf16_bwd_layout");
 }

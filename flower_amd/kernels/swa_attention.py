@@ -28,39 +28,50 @@ _DQ_CFG = (128, 64, 4, 2)
 
 class _SlidingWindowAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, window):
+    def forward(ctx, q, k, v, window, token_major=False):
         lib = _lib.load()
         B, H, T, D = q.shape
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        out = torch.empty_like(q)
+        # token_major: O stored (B, T, H, D) and returned as its (B, H, T, D) view, so that the
+        # caller's transpose(1, 2).reshape(B, T, H D) is a view (no copy); the backward then takes
+        # dO as that layout's view too.
+        out = torch.empty((B, T, H, D) if token_major else (B, H, T, D), dtype=q.dtype, device=q.device)
         lse = torch.empty((B, H, T), device=q.device, dtype=torch.float32)
-        rc = lib.flw_swa_bf16_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), B, H, T, D, int(window),
-                                  out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+        layout = _lib.LAYOUT_BTHD if token_major else _lib.LAYOUT_BHTD
+        rc = lib.flw_swa_bf16_fwd_layout(q.data_ptr(), k.data_ptr(), v.data_ptr(), B, H, T, D, int(window),
+                                         out.data_ptr(), layout, lse.data_ptr(), _lib.stream_of(q))
         _lib.check(rc, "swa_attention forward")
         ctx.save_for_backward(q, k, v, out, lse)
-        ctx.window = int(window)
-        return out
+        ctx.window, ctx.layout = int(window), layout
+        return out.transpose(1, 2) if token_major else out
 
     @staticmethod
     def backward(ctx, do):
         lib = _lib.load()
         q, k, v, out, lse = ctx.saved_tensors
         B, H, T, D = q.shape
-        do = do.contiguous()
         if do.dtype != q.dtype:
             do = do.to(q.dtype)
+        # dO in the forward's O layout: a view of it when the gradient comes that way (the output
+        # projection's gradient, token-major), a copy otherwise
+        do = do.transpose(1, 2).contiguous() if ctx.layout == _lib.LAYOUT_BTHD else do.contiguous()
+        dptr = do.data_ptr()
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         ws = _lib.workspace(lib.flw_swa_bf16_bwd_workspace_bytes(B, H, T, D), q.device)
-        rc = lib.flw_swa_bf16_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), do.data_ptr(),
-                                  lse.data_ptr(), B, H, T, D, ctx.window, dq.data_ptr(), dk.data_ptr(),
-                                  dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+        rc = lib.flw_swa_bf16_bwd_layout(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dptr,
+                                         ctx.layout, lse.data_ptr(), B, H, T, D, ctx.window, dq.data_ptr(),
+                                         dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _lib.stream_of(q))
         _lib.check(rc, "swa_attention backward")
-        return dq, dk, dv, None
+        return dq, dk, dv, None, None
 
 
 def swa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, *,
-                  fwd_cfg=_FWD_CFG, dkdv_cfg=_DKDV_CFG, dq_cfg=_DQ_CFG) -> torch.Tensor:
-    """Causal sliding-window attention. q/k/v: (B, H, T, D) bf16 or fp32 on the GPU. Differentiable."""
+                  fwd_cfg=_FWD_CFG, dkdv_cfg=_DKDV_CFG, dq_cfg=_DQ_CFG, token_major: bool = False) -> torch.Tensor:
+    """Causal sliding-window attention. q/k/v: (B, H, T, D) bf16 or fp32 on the GPU. Differentiable.
+    token_major (this build's addition): the (B, H, T, D) result is a view of a (B, T, H, D) tensor,
+    so that ``out.transpose(1, 2).reshape(B, T, H * D)`` -- the output projection's input -- is a
+    view, not a copy (bf16 inputs; the values are the same either way)."""
     del fwd_cfg, dkdv_cfg, dq_cfg
     try:
         _lib.load()
@@ -84,7 +95,7 @@ def swa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int
         out = _SlidingWindowAttention.apply(q.to(torch.bfloat16), k.to(torch.bfloat16),
                                             v.to(torch.bfloat16), window)
         return out.to(torch.float32)
-    return _SlidingWindowAttention.apply(q, k, v, window)
+    return _SlidingWindowAttention.apply(q, k, v, window, bool(token_major))
 
 
 __all__ = ["swa_attention"]

@@ -42,7 +42,9 @@ enum flw_granularity { FLW_SCALE_TENSOR = 0, FLW_SCALE_HEAD = 1, FLW_SCALE_BH = 
  *        (d/32)*2048 + (kk/32)*1024 + ((d%32) + 32*h)*16 + b,
  *        r = kk%32, h = (r/4)%2, b = 4*(r/8) + r%4,
  *     i.e. each 16-byte run is one lane's share of a 32x32x64 FP8 MFMA operand of V^T. */
-enum flw_layout { FLW_LAYOUT_BHTD = 0, FLW_LAYOUT_VTILE = 1 };
+enum flw_layout { FLW_LAYOUT_BHTD = 0, FLW_LAYOUT_VTILE = 1, FLW_LAYOUT_BTHD = 2 };
+/* FLW_LAYOUT_BTHD -- contiguous (B, T, H, D), token-major: the layout of the attention output the
+ *   output projection reads as rows of H D values (the bf16 attention's O and dO, below). */
 
 /* GEMM modes. A8W8: activations quantised per row to e4m3, FP8 x FP8 MFMA (the _fp8_head
  * recipe). W8A16: e4m3 weights widened to bf16 in the kernel, bf16 activations unquantised. */
@@ -419,11 +421,23 @@ int flw_gelu_quant_rows_e4m3(const void* x, int64_t rows, int64_t cols, int64_t 
  *   Delta = rowsum(dout * out). */
 int flw_swa_bf16_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t T,
                      int64_t D, int64_t window, void* out, float* lse, void* stream);
+/* flw_swa_bf16_fwd writing O in out_layout: FLW_LAYOUT_BHTD (as flw_swa_bf16_fwd) or
+ * FLW_LAYOUT_BTHD, O as (B, T, H, D) -- `a.transpose(1, 2).reshape(B, T, H D)` of
+ * CausalSelfAttention.forward (flower/models/base.py:643-646) then is a view, no copy. */
+int flw_swa_bf16_fwd_layout(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t T,
+                            int64_t D, int64_t window, void* out, int out_layout, float* lse, void* stream);
 size_t flw_swa_bf16_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D);
 int flw_swa_bf16_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
                      const float* lse, int64_t B, int64_t H, int64_t T, int64_t D, int64_t window,
                      void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
                      void* stream);
+/* flw_swa_bf16_bwd with O and dO in o_layout (FLW_LAYOUT_BHTD or FLW_LAYOUT_BTHD; q, k, v and the
+ * gradients stay (B, H, T, D)): the forward's token-major O and the output projection's gradient
+ * as it comes, without transposing either. */
+int flw_swa_bf16_bwd_layout(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                            int o_layout, const float* lse, int64_t B, int64_t H, int64_t T, int64_t D,
+                            int64_t window, void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* ---------------------------------------------------------------- GEMM */
 

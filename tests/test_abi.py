@@ -306,6 +306,12 @@ def test_training_row_kernel_refusals_on_the_host():
     assert rc == 1 and b"null" in lib.flw_last_error()
     rc = lib.flw_add_rmsnorm_fwd(P, P, 4, 64, 64, 32, P, 1e-6, P, 64, P, 64, None)
     assert rc == 1 and b"strides" in lib.flw_last_error()
+    rc = lib.flw_swa_bf16_fwd_layout(P, P, P, 1, 4, 128, 64, 32, P, 7, P, None)
+    assert rc == 1 and b"layout" in lib.flw_last_error()
+    rc = lib.flw_swa_bf16_fwd_layout(P, P, P, 1, 64, 1 << 18, 64, 32, P, L.LAYOUT_BTHD, P, None)
+    assert rc == 2 and b"2^31" in lib.flw_last_error()
+    rc = lib.flw_swa_bf16_bwd_layout(P, P, P, P, P, L.LAYOUT_VTILE, P, 1, 4, 128, 64, 32, P, P, P, P, 1 << 20, None)
+    assert rc == 1 and b"layout" in lib.flw_last_error()
     rc = lib.flw_swiglu_fwd(P, P, 4, 20, 24, 24, P, 24, None, None, 0, None)
     assert rc == 1 and b"multiple of 8" in lib.flw_last_error()
     rc = lib.flw_swiglu_bwd(P, P, 4, 64, 64, 64, P, 64, P, P + 4, 64, None, None, 0, None)

@@ -166,3 +166,32 @@ def test_fp32_inputs_against_fp32_attention_of_the_unrounded_inputs():
         assert got.dtype == torch.float32, name
         mean_rel, max_rel = rel(got.cpu(), w)
         assert mean_rel < 0.01 and max_rel < 2e-2, (name, mean_rel, max_rel)
+
+
+@pytest.mark.parametrize("B,H,T,D,W", [(2, 3, 333, 64, 100), (1, 4, 200, 32, 64), (1, 2, 257, 128, 256),
+                                       (2, 20, 1024, 64, 512)])
+def test_token_major_output_is_bit_identical(B, H, T, D, W):
+    """swa_attention(..., token_major=True): O stored (B, T, H, D) (flw_swa_bf16_fwd_layout) and dO
+    read in that layout (flw_swa_bf16_bwd_layout) -- the output, its token-major transpose as a
+    view (no copy), and dQ, dK, dV equal the head-major route bit for bit, with dO handed over
+    both as the output projection gives it (a token-major view) and as a contiguous tensor."""
+    from flower_amd.kernels.swa_attention import swa_attention
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    q, k, v = ((torch.randn(B, H, T, D, generator=g)).to("cuda", torch.bfloat16) for _ in range(3))
+    dy = torch.randn(B, T, H * D, generator=g).to("cuda", torch.bfloat16)
+    grads = []
+    for tm in (False, True):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        o = swa_attention(qq, kk, vv, W, token_major=tm)
+        rows = o.transpose(1, 2).reshape(B, T, H * D)
+        if tm:
+            assert rows.data_ptr() == o.data_ptr() and o.transpose(1, 2).is_contiguous()
+        rows.backward(dy)
+        grads.append((o.detach().contiguous(), qq.grad, kk.grad, vv.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+    qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o = swa_attention(qq, kk, vv, W, token_major=True)
+    o.backward(dy.view(B, T, H, D).transpose(1, 2).contiguous())      # a head-major dO
+    assert torch.equal(qq.grad, grads[0][1]) and torch.equal(kk.grad, grads[0][2])
+    assert torch.equal(vv.grad, grads[0][3])
