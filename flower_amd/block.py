@@ -225,8 +225,15 @@ class _Fp8GatedFn(torch.autograd.Function):
             return P.transpose_codes(w8, mod.out_features), sw
         gx = gwg = gwu = None
         if ctx.needs_input_grad[0]:
-            gx = (P.scaled_mm(dg8, sdg, *w_cols(gate_mod, wg8, swg))
-                  + P.scaled_mm(du8, sdu, *w_cols(up_mod, wu8, swu))).view(ctx.x_shape)
+            gx = P.scaled_mm(dg8, sdg, *w_cols(gate_mod, wg8, swg))
+            K = gx.shape[1]
+            if lib.flw_fp8_scaled_mm_workspace_bytes(M, K, H) == 0:
+                # unsplit: the sum of the two dgrads in the second one's epilogue, bf16(a + bf16(b))
+                # as autograd's add of the two bf16 gradients gives it
+                gx = P.scaled_mm_residual(du8, sdu, *w_cols(up_mod, wu8, swu), gx)
+            else:
+                gx = gx + P.scaled_mm(du8, sdu, *w_cols(up_mod, wu8, swu))
+            gx = gx.view(ctx.x_shape)
         if ctx.needs_input_grad[1]:
             gwg = P.scaled_mm(dg8t, sdg, x8t, sx).to(gate_mod.weight.dtype)
         if ctx.needs_input_grad[2]:
@@ -506,16 +513,21 @@ class FeedForward(nn.Module):
             self.down = nn.Linear(hidden, d, bias=bias)
             self.down._is_residual_out = True
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+        """residual: returns ``residual + ff(x)`` (the block's second residual add), inside the down
+        projection's GEMM epilogue on the fused FP8 route."""
         if self.activation == "gelu":
-            return self.net(x)
-        if _fp8_gated_ok(x, self):
+            out = self.net(x)
+        elif _fp8_gated_ok(x, self):
             h, h_amax = _Fp8GatedFn.apply(x, self.gate.weight, self.up.weight, self.gate, self.up)
-            return self.down(h, x_amax=h_amax)
-        gate, up = self.gate(x), self.up(x)
-        if gate.numel() > 0 and _hip_rows_ok(gate, up):
-            return self.down(_SwiGLUFn.apply(gate, up))
-        return self.down(torch.nn.functional.silu(gate) * up)
+            return self.down(h, x_amax=h_amax, residual=residual)
+        else:
+            gate, up = self.gate(x), self.up(x)
+            if gate.numel() > 0 and _hip_rows_ok(gate, up):
+                out = self.down(_SwiGLUFn.apply(gate, up))
+            else:
+                out = self.down(torch.nn.functional.silu(gate) * up)
+        return out if residual is None else residual + out
 
 
 class TransformerBlock(nn.Module):
@@ -541,7 +553,7 @@ class TransformerBlock(nn.Module):
             # gradients (the same bf16 sums autograd forms for x's and x1's two uses).
             h1, xr = _RMSNormResFn.apply(x, self.ln1.weight, self.ln1.eps)
             x1, h2 = _AddRMSNormFn.apply(xr, self.attn(h1), self.ln2.weight, self.ln2.eps)
-            return x1 + self.ff(h2), memory
+            return self.ff(h2, residual=x1), memory
         x = x + self.attn(self.ln1(x))
         x = x + self.ff(self.ln2(x))
         return x, memory
