@@ -199,12 +199,15 @@ class _Fp8GatedFn(torch.autograd.Function):
         ctx.save_for_backward(g, u, x8t, sx, wg8, swg, wu8, swu)
         ctx.mods, ctx.x_shape, ctx.ld = (gate_mod, up_mod), x.shape, ld
         ctx.mark_non_differentiable(amax)
+        ctx.set_materialize_grads(False)          # no zeros for the maximum's (absent) gradient
         return h.view(*x.shape[:-1], H), amax
 
     @staticmethod
     def backward(ctx, dh, _amax_grad):
         from . import precision as P
         g, u, x8t, sx, wg8, swg, wu8, swu = ctx.saved_tensors
+        if dh is None:
+            return None, None, None, None, None
         gate_mod, up_mod = ctx.mods
         M, H = g.shape
         lib = _lib.load()
