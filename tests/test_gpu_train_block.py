@@ -149,3 +149,27 @@ def test_residual_norm_route_bit_identical_to_the_module_route(fp8):
     assert torch.equal(gx, xx.grad.float())
     for n, p in blk.named_parameters():
         assert torch.equal(gp[n], p.grad.float()), n
+
+
+def test_fused_fp8_routes_inside_the_weight_cache():
+    """Inside fp8_weight_cache the fused gate / up / SwiGLU node and the down projection with the
+    residual take the cached weight codes (forward) and the cached column codes (dgrad): two steps
+    inside the cache equal two uncached steps bit for bit, and the cache quantises each weight's
+    columns once."""
+    from flower_amd.precision import convert_model_to_fp8, fp8_weight_cache
+    blk, conf = _block()
+    stack = nn.Module()
+    stack.blocks = nn.ModuleList([blk])
+    convert_model_to_fp8(stack, recipe="tensorwise", keep_bf16_blocks=0, verbose=False)
+    blk = stack.blocks[0]
+    x, dy = _inputs(conf)
+    y0, gx0, gp0 = _run(blk, x, dy)
+    blk.zero_grad(set_to_none=True)
+    with fp8_weight_cache(stack):
+        for _ in range(2):
+            y1, gx1, _ = _run(blk, x, dy)
+        cols = [m._fp8_cached_cols is not None for m in (blk.ff.gate, blk.ff.up, blk.ff.down)]
+    assert all(cols)
+    assert torch.equal(y0, y1) and torch.equal(gx0, gx1)
+    for n, p in blk.named_parameters():
+        assert torch.equal(p.grad.float(), 2 * gp0[n]), n
