@@ -426,7 +426,8 @@ static int swiglu_check(const void* g, const void* u, int64_t rows, int64_t cols
   FLW_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0, FLW_E_INVALID, "cols must be a positive multiple of 8");
   FLW_REQUIRE(gs >= cols && us >= cols && gs % 8 == 0 && us % 8 == 0 && aligned16(g) && aligned16(u),
               FLW_E_INVALID, "rows must be 16-byte aligned with a stride >= cols");
-  FLW_REQUIRE(rows * (cols / 8) <= 0x7FFFFFFFll - 255, FLW_E_UNSUPPORTED, "too many elements");
+  // the grid-stride index stays below 2^31 through its last step
+  FLW_REQUIRE(rows * (cols / 8) <= 0x7FFFFFFFll - (int64_t)kSwigluBlocks * 256, FLW_E_UNSUPPORTED, "too many elements");
   return FLW_OK;
 }
 
