@@ -900,7 +900,8 @@ def bench_block_train(cfg, steps, warmup, recipe):
     (flower_amd.block.TransformerBlock, block_config()): its five Linears converted by
     convert_model_to_fp8 with ``recipe`` (None: left in bf16, torch's GEMMs), the attention on the
     HIP bf16 sliding-window kernels, RMSNorm, the head split with QK-norm + RoPE and the SwiGLU
-    product on the HIP row kernels (forward and backward), the residual adds in torch."""
+    product on the HIP row kernels (forward and backward), the residual adds folded into the norms'
+    passes and (FP8 tensorwise) the down projection's GEMM epilogue."""
     import copy
     import torch.nn as nn
     from flower_amd.block import TransformerBlock, block_config, init_block_
