@@ -43,19 +43,23 @@ template <int D>
 struct HeadsChunk {
   int64_t m, bhtd;
   int part, h, l, t;
+  // 32-bit index arithmetic (the host keeps the chunk count below 2^31): the divisions by the
+  // run-time cpr, H and T are the kernel's largest instruction cost otherwise.
   __device__ __forceinline__ bool init(const HeadsParams& p) {
-    constexpr int LPR = D / 8;
-    const int64_t cpr = 3 * (int64_t)p.H * LPR;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    m = i / cpr;
-    if (m >= p.M) return false;                 // a whole head row at a time (cpr % LPR == 0)
-    const int c = (int)(i - m * cpr);
-    part = c / (p.H * LPR);
-    h = (c / LPR) % p.H;
-    l = c % LPR;
-    t = (int)(m % p.T);
-    const int64_t b = m / p.T;
-    bhtd = ((b * p.H + h) * p.T + t) * D + 8 * l;
+    constexpr uint32_t LPR = D / 8;
+    const uint32_t cpr = 3u * (uint32_t)p.H * LPR;
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t mm = i / cpr;
+    if ((int64_t)mm >= p.M) return false;       // a whole head row at a time (cpr % LPR == 0)
+    m = mm;
+    const uint32_t c = i - mm * cpr;
+    const uint32_t hl = c / LPR;                 // part * H + h
+    part = (int)(hl / (uint32_t)p.H);
+    h = (int)(hl - (uint32_t)part * (uint32_t)p.H);
+    l = (int)(c % LPR);
+    const uint32_t b = mm / (uint32_t)p.T;
+    t = (int)(mm - b * (uint32_t)p.T);
+    bhtd = (((int64_t)b * p.H + h) * p.T + t) * D + 8 * l;
     return true;
   }
 };
@@ -141,8 +145,8 @@ static int heads_check(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t
   FLW_REQUIRE(((uintptr_t)rcos & 15) == 0 && ((uintptr_t)rsin & 15) == 0, FLW_E_INVALID,
               "RoPE tables must be 16-byte aligned");
   FLW_REQUIRE(qk_norm == 0 || eps >= 0.0f, FLW_E_INVALID, "eps must be non-negative");
-  FLW_REQUIRE(B * T * 3 * H * (D / 8) <= 0x7FFFFFFFll * 256 && T <= 0x7FFFFFFF && H <= 65535,
-              FLW_E_UNSUPPORTED, "shape too large");
+  FLW_REQUIRE(B * T * 3 * H * (D / 8) <= 0x7FFFFFFFll - 255 && H <= 65535, FLW_E_UNSUPPORTED,
+              "shape too large (3 B T H D / 8 chunks must stay below 2^31)");
   return FLW_OK;
 }
 
