@@ -297,7 +297,7 @@ def test_training_row_kernel_refusals_on_the_host():
     assert rc == 1 and b"eps" in lib.flw_last_error()
     need = lib.flw_rmsnorm_bwd_workspace_bytes(1021, 1280)            # a workgroup per 4 rows
     assert need == 256 * 1280 * 4 and lib.flw_rmsnorm_bwd_workspace_bytes(0, 1280) == 0
-    assert lib.flw_rmsnorm_bwd_workspace_bytes(1 << 20, 1280) == 512 * 1280 * 4   # at most 512
+    assert lib.flw_rmsnorm_bwd_workspace_bytes(1 << 20, 1280) == 768 * 1280 * 4   # at most 768
     rc = lib.flw_rmsnorm_bwd(P, 1021, 1280, 1280, P, 1e-6, P, 1280, None, 0, P, 1280, P, P, need - 16, None)
     assert rc == 1 and b"workspace" in lib.flw_last_error()
     rc = lib.flw_rmsnorm_bwd(P, 1021, 1280, 1280, P, 1e-6, P, 1280, P + 8, 1280, P, 1280, P, P, need, None)
