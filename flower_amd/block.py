@@ -187,8 +187,8 @@ class _Fp8GatedFn(torch.autograd.Function):
         H = gate_mod.out_features
         ld = ((M + 127) // 128) * 128
         x8, x8t, sx = P._quantize_tensorwise_t(x2, ld)
-        wg8, swg = gate_mod.weight_codes()
-        wu8, swu = up_mod.weight_codes()
+        wg8, swg, wg8t = gate_mod.tensorwise_codes()
+        wu8, swu, wu8t = up_mod.tensorwise_codes()
         g = P.scaled_mm_plain(x8, sx, wg8, swg)
         u = P.scaled_mm_plain(x8, sx, wu8, swu)
         h = torch.empty((M, H), dtype=x.dtype, device=x.device)
@@ -196,7 +196,7 @@ class _Fp8GatedFn(torch.autograd.Function):
         ws = _lib.workspace(lib.flw_swiglu_amax_workspace_bytes(M, H), x.device)
         _lib.check(lib.flw_swiglu_fwd(g.data_ptr(), u.data_ptr(), M, H, H, H, h.data_ptr(), H, amax.data_ptr(),
                                       ws.data_ptr(), ws.numel(), _lib.stream_of(x)), "SwiGLU")
-        ctx.save_for_backward(g, u, x8t, sx, wg8, swg, wu8, swu)
+        ctx.save_for_backward(g, u, x8t, sx, wg8, swg, wu8, swu, wg8t, wu8t)
         ctx.mods, ctx.x_shape, ctx.ld = (gate_mod, up_mod), x.shape, ld
         ctx.mark_non_differentiable(amax)
         ctx.set_materialize_grads(False)          # no zeros for the maximum's (absent) gradient
@@ -205,7 +205,7 @@ class _Fp8GatedFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dh, _amax_grad):
         from . import precision as P
-        g, u, x8t, sx, wg8, swg, wu8, swu = ctx.saved_tensors
+        g, u, x8t, sx, wg8, swg, wu8, swu, wg8t, wu8t = ctx.saved_tensors
         if dh is None:
             return None, None, None, None, None
         gate_mod, up_mod = ctx.mods
@@ -222,20 +222,20 @@ class _Fp8GatedFn(torch.autograd.Function):
         dg8, dg8t, sdg = P._quantize_tensorwise_t(dg, ctx.ld, amax[0:1])
         du8, du8t, sdu = P._quantize_tensorwise_t(du, ctx.ld, amax[1:2])
 
-        def w_cols(mod, w8, sw):                     # as _Fp8LinearFn's backward takes them
+        def w_cols(mod, w8, sw, w8t):                # as _Fp8LinearFn's backward takes them
             if getattr(mod, "_fp8_cached", None) is not None:
                 return mod.weight_col_codes()
-            return P.transpose_codes(w8, mod.out_features), sw
+            return (w8t if w8t is not None else P.transpose_codes(w8, mod.out_features)), sw
         gx = gwg = gwu = None
         if ctx.needs_input_grad[0]:
-            gx = P.scaled_mm(dg8, sdg, *w_cols(gate_mod, wg8, swg))
+            gx = P.scaled_mm(dg8, sdg, *w_cols(gate_mod, wg8, swg, wg8t))
             K = gx.shape[1]
             if lib.flw_fp8_scaled_mm_workspace_bytes(M, K, H) == 0:
                 # unsplit: the sum of the two dgrads in the second one's epilogue, bf16(a + bf16(b))
                 # as autograd's add of the two bf16 gradients gives it
-                gx = P.scaled_mm_residual(du8, sdu, *w_cols(up_mod, wu8, swu), gx)
+                gx = P.scaled_mm_residual(du8, sdu, *w_cols(up_mod, wu8, swu, wu8t), gx)
             else:
-                gx = gx + P.scaled_mm(du8, sdu, *w_cols(up_mod, wu8, swu))
+                gx = gx + P.scaled_mm(du8, sdu, *w_cols(up_mod, wu8, swu, wu8t))
             gx = gx.view(ctx.x_shape)
         if ctx.needs_input_grad[1]:
             gwg = P.scaled_mm(dg8t, sdg, x8t, sx).to(gate_mod.weight.dtype)

@@ -1090,16 +1090,33 @@ extern "C" int flw_transpose_e4m3(const uint8_t* codes, int64_t rows, int64_t co
 // comes from the tensor's |x| max (amax_bits, folded by the amax pass before this launch); the
 // arithmetic is quant_kernel's, so both layouts hold exactly the tensorwise quantiser's codes.
 // Rows of out_t past `rows` (up to ld, which grid.y covers) are zero.
+// part != nullptr: amax_bits is unused and every workgroup folds the npart amax partials itself (a
+// few hundred: a weight matrix), which spares the fold its own launch.
 __global__ __launch_bounds__(256) void quant_tensor_t_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                              int64_t cols, int64_t xs,
                                                              const uint32_t* __restrict__ amax_bits,
                                                              uint8_t* __restrict__ out8, int64_t ld8,
                                                              uint8_t* __restrict__ out_t, int64_t ldt,
-                                                             float* __restrict__ scale_out) {
+                                                             float* __restrict__ scale_out,
+                                                             const uint32_t* __restrict__ part, int npart) {
   __shared__ __align__(16) uint8_t t[kTT * kTPitch];
+  __shared__ uint32_t red[4];
   const int tid = threadIdx.x;
   const int64_t c0 = (int64_t)blockIdx.x * kTT, r0 = (int64_t)blockIdx.y * kTT;
-  const float amax = __uint_as_float(*amax_bits);
+  uint32_t amax_u;
+  if (part != nullptr) {
+    uint32_t m = 0;
+    for (int i = tid; i < npart; i += 256) m = m > part[i] ? m : part[i];
+    m = wave_max_u32(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    amax_u = red[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) amax_u = amax_u > red[i] ? amax_u : red[i];
+  } else {
+    amax_u = *amax_bits;
+  }
+  const float amax = __uint_as_float(amax_u);
   const float scale = (amax < kEps ? kEps : amax) / kE4m3Max;    // IEEE fp32 division
   const bool fast = __builtin_isfinite(amax);
   const float rcp = 1.0f / scale;
@@ -1195,7 +1212,8 @@ extern "C" int flw_quant_tensor_t_e4m3_amax(const void* x, int64_t rows, int64_t
   const Timer tm = take_timer();
   (void)launch_args(reinterpret_cast<const void*>(&quant_tensor_t_kernel), dim3((unsigned)gx, (unsigned)gy),
                     dim3(256), 0, static_cast<hipStream_t>(stream), tm.start, tm.stop,
-                    static_cast<const uint16_t*>(x), rows, cols, row_stride, amax, out8, ld8, out_t, ldt, scale_out);
+                    static_cast<const uint16_t*>(x), rows, cols, row_stride, amax, out8, ld8, out_t, ldt, scale_out,
+                    static_cast<const uint32_t*>(nullptr), 0);
   return check_launch("flw_quant_tensor_t_e4m3_amax");
 }
 
@@ -1225,11 +1243,17 @@ extern "C" int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols
   const Timer tm = take_timer();
   (void)launch_ext(reinterpret_cast<const void*>(&amax_kernel<uint16_t>), dim3((unsigned)p.nchunks, 1u, 1u),
                    dim3(kThreads), 0, s, p, tm.start, nullptr);
-  (void)launch_args(reinterpret_cast<const void*>(&amax_fold_tensor_kernel), dim3(1u), dim3(1024), 0, s, nullptr,
-                    nullptr, static_cast<const uint32_t*>(p.partials), (int64_t)p.nchunks, amax);
+  // Up to kInlineFold partials (a weight matrix's) every quantising workgroup folds itself; more
+  // (an activation's thousands) one workgroup folds first.
+  constexpr int64_t kInlineFold = 1024;
+  const bool inline_fold = p.nchunks <= kInlineFold;
+  if (!inline_fold)
+    (void)launch_args(reinterpret_cast<const void*>(&amax_fold_tensor_kernel), dim3(1u), dim3(1024), 0, s, nullptr,
+                      nullptr, static_cast<const uint32_t*>(p.partials), (int64_t)p.nchunks, amax);
   (void)launch_args(reinterpret_cast<const void*>(&quant_tensor_t_kernel), dim3((unsigned)gx, (unsigned)gy),
                     dim3(256), 0, s, nullptr, tm.stop, static_cast<const uint16_t*>(x), rows, cols, row_stride,
-                    static_cast<const uint32_t*>(amax), out8, ld8, out_t, ldt, scale_out);
+                    static_cast<const uint32_t*>(amax), out8, ld8, out_t, ldt, scale_out,
+                    static_cast<const uint32_t*>(inline_fold ? p.partials : nullptr), (int)p.nchunks);
   return check_launch("flw_quant_tensor_t_e4m3");
 }
 

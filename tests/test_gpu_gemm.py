@@ -247,17 +247,25 @@ def test_forwards_are_restored_after_exit_and_after_exception():
 
 
 def test_cache_uses_one_quantisation_per_enter():
-    """Inside the cache the layer must not re-quantise its weight on each microstep."""
+    """Inside the cache the layer must not re-quantise its weight on each microstep (counted: the
+    plain weight cast, and the training forward's cast in both layouts when it quantises afresh)."""
     from flower_amd.precision import Fp8Linear, fp8_weight_cache
     m = _fp8_model()
     calls = {"n": 0}
-    orig = Fp8Linear.quantize_weight
+    orig, orig_t = Fp8Linear.quantize_weight, Fp8Linear.tensorwise_codes
 
     def counting(self):
         calls["n"] += 1
         return orig(self)
 
+    def counting_t(self):
+        cached = getattr(self, "_fp8_cached", None) is not None
+        out = orig_t(self)
+        calls["n"] += 0 if cached else 1
+        return out
+
     Fp8Linear.quantize_weight = counting
+    Fp8Linear.tensorwise_codes = counting_t
     try:
         x = torch.randn(64, 256, device="cuda", dtype=torch.bfloat16)
         with fp8_weight_cache(m):
@@ -268,6 +276,7 @@ def test_cache_uses_one_quantisation_per_enter():
         assert calls["n"] == 4
     finally:
         Fp8Linear.quantize_weight = orig
+        Fp8Linear.tensorwise_codes = orig_t
 
 
 
