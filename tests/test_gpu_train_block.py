@@ -173,3 +173,29 @@ def test_fused_fp8_routes_inside_the_weight_cache():
     assert torch.equal(y0, y1) and torch.equal(gx0, gx1)
     for n, p in blk.named_parameters():
         assert torch.equal(p.grad.float(), 2 * gp0[n]), n
+
+
+def test_fused_fp8_block_ragged_tokens_bit_identical():
+    """A ragged token count (B1 x T77: 77 rows, the wgrad operands zero-padded to 128 columns,
+    partial GEMM tiles, a partial last attention tile) through the fused tensorwise routes equals
+    the module-by-module composition bit for bit."""
+    from flower_amd.block import _SwiGLUFn
+    from flower_amd.precision import convert_model_to_fp8
+    blk, conf = _block()
+    stack = nn.Module()
+    stack.blocks = nn.ModuleList([blk])
+    convert_model_to_fp8(stack, recipe="tensorwise", keep_bf16_blocks=0, verbose=False)
+    blk = stack.blocks[0]
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(1, 77, conf.d_model, generator=g).to("cuda", torch.bfloat16)
+    dy = torch.randn(1, 77, conf.d_model, generator=g).to("cuda", torch.bfloat16)
+    y, gx, gp = _run(blk, x, dy)
+    blk.zero_grad(set_to_none=True)
+    xx = x.clone().requires_grad_(True)
+    h = xx + blk.attn(blk.ln1(xx))
+    t = blk.ln2(h)
+    y2 = h + blk.ff.down(_SwiGLUFn.apply(blk.ff.gate(t), blk.ff.up(t)))
+    y2.backward(dy)
+    assert torch.equal(y, y2.detach().float()) and torch.equal(gx, xx.grad.float())
+    for n, p in blk.named_parameters():
+        assert torch.equal(gp[n], p.grad.float()), n
