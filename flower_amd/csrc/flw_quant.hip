@@ -1179,11 +1179,21 @@ __global__ __launch_bounds__(1024) void amax_fold_tensor_kernel(const uint32_t* 
   }
 }
 
+constexpr int64_t kInlineFold = 1024;   // amax partials every quantising workgroup folds itself
+
+// The amax pass's rows for a contiguous matrix of n values: the narrowest of 64 .. 512 values that
+// leaves at most kInlineFold chunks of 128 rows (so no fold launch), else 64; 0: not flat.
+static int64_t tensor_t_flat_cols(int64_t n) {
+  if (n % 64 != 0) return 0;
+  for (int64_t c = 64; c <= 512; c *= 2)
+    if (n % c == 0 && nchunks_of(n / c) <= kInlineFold) return c;
+  return 64;
+}
+
 extern "C" size_t flw_quant_tensor_t_workspace_bytes(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  const int64_t n = rows * cols;
-  const int64_t flat_rows = n % 64 == 0 ? n / 64 : rows;    // the amax pass's chunk rows
-  return 16 + partial_bytes(1, 1, flat_rows);
+  const int64_t n = rows * cols, fc = tensor_t_flat_cols(n);
+  return 16 + partial_bytes(1, 1, fc ? n / fc : rows);     // the amax pass's chunk rows
 }
 
 static int quant_t_check(const void* x, int64_t rows, int64_t cols, int64_t row_stride, const uint8_t* out8,
@@ -1226,12 +1236,13 @@ extern "C" int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols
   FLW_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0 && workspace_bytes >= need, FLW_E_WORKSPACE,
               "workspace needs %zu bytes (16-byte aligned)", need);
   const int64_t gx = (cols + kTT - 1) / kTT, gy = (ldt + kTT - 1) / kTT;
-  // The amax pass over the matrix as 64-value rows when it is contiguous (chunks of 128 such rows
-  // spread over the GPU), else over its own rows; one workgroup of 1024 folds the partials.
-  const bool flat = row_stride == cols && (rows * cols) % 64 == 0;
+  // The amax pass over the matrix as flat rows when it is contiguous (chunks of 128 such rows
+  // spread over the GPU), else over its own rows.
+  const int64_t fc = row_stride == cols ? tensor_t_flat_cols(rows * cols) : 0;
+  const bool flat = fc != 0;
   QuantParams p{};
-  const int64_t d2 = flat ? rows * cols / 64 : rows, d3 = flat ? 64 : cols;
-  set_tensor(p.t[0], x, d2 * (flat ? 64 : row_stride), d2 * (flat ? 64 : row_stride), flat ? 64 : row_stride, d3,
+  const int64_t d2 = flat ? rows * cols / fc : rows, d3 = flat ? fc : cols;
+  set_tensor(p.t[0], x, d2 * (flat ? fc : row_stride), d2 * (flat ? fc : row_stride), flat ? fc : row_stride, d3,
              FLW_LAYOUT_BHTD, nullptr, nullptr, nullptr);
   p.d0 = 1; p.d1 = 1; p.d2 = d2; p.d3 = d3;
   p.nchunks = nchunks_of(d2);
@@ -1243,9 +1254,7 @@ extern "C" int flw_quant_tensor_t_e4m3(const void* x, int64_t rows, int64_t cols
   const Timer tm = take_timer();
   (void)launch_ext(reinterpret_cast<const void*>(&amax_kernel<uint16_t>), dim3((unsigned)p.nchunks, 1u, 1u),
                    dim3(kThreads), 0, s, p, tm.start, nullptr);
-  // Up to kInlineFold partials (a weight matrix's) every quantising workgroup folds itself; more
-  // (an activation's thousands) one workgroup folds first.
-  constexpr int64_t kInlineFold = 1024;
+  // Up to kInlineFold partials every quantising workgroup folds itself; more, one workgroup first.
   const bool inline_fold = p.nchunks <= kInlineFold;
   if (!inline_fold)
     (void)launch_args(reinterpret_cast<const void*>(&amax_fold_tensor_kernel), dim3(1u), dim3(1024), 0, s, nullptr,
