@@ -176,3 +176,39 @@ def test_one_pass_tensorwise_codes_in_both_layouts(R, C, ld, pad, special):
     assert torch.equal(x8, want8)
     assert torch.equal(x8t, transpose_codes(want8, ld))
     assert not x8t[:, R:].any()
+
+
+@pytest.mark.parametrize("recipe", ["rowwise", "tensorwise"])
+@pytest.mark.parametrize("bias", [False, True])
+def test_fp8_linear_residual_argument(recipe, bias):
+    """Fp8Linear(x, residual=r) equals r + Fp8Linear(x) bit for bit (in the tensorwise GEMM's
+    epilogue without a bias, in torch otherwise), and its gradients -- r's is the output's -- equal
+    those of the separate add; the forward's weight codes in both layouts (training) equal the
+    plain weight cast's."""
+    from flower_amd.precision import Fp8Linear
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(256, 384, bias=bias).cuda().to(torch.bfloat16)
+    mod = Fp8Linear.from_linear(lin, recipe)
+    x = _rnd((3, 100, 256), 31).cuda()
+    r = _rnd((3, 100, 384), 32).cuda()
+    g = _rnd((3, 100, 384), 33).cuda()
+    xa, ra = x.clone().requires_grad_(True), r.clone().requires_grad_(True)
+    ya = mod(xa, residual=ra)
+    ya.backward(g)
+    ga = (xa.grad, ra.grad, mod.weight.grad.clone())
+    mod.weight.grad = None
+    if bias:
+        gba = mod.bias.grad.clone()
+        mod.bias.grad = None
+    xb, rb = x.clone().requires_grad_(True), r.clone().requires_grad_(True)
+    yb = rb + mod(xb)
+    yb.backward(g)
+    assert torch.equal(ya, yb)
+    assert torch.equal(ga[0], xb.grad) and torch.equal(ga[1], rb.grad) and torch.equal(ga[2], mod.weight.grad)
+    if bias:
+        assert torch.equal(gba, mod.bias.grad)
+    if recipe == "tensorwise":
+        w8, sw, w8t = mod.tensorwise_codes()
+        p8, ps = mod.quantize_weight()
+        assert torch.equal(w8, p8) and torch.equal(sw, ps)
+        assert torch.equal(w8t[:, :384], w8.t()) and w8t.shape == (256, 384)
