@@ -62,7 +62,9 @@ SIGNATURES = {
     "flw_qkv_heads_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_float, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "flw_qkv_heads_bwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_float, c_void_p,
-                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
+                                  c_size_t, c_void_p]),
+    "flw_qkv_heads_amax_workspace_bytes": (c_size_t, [c_int64] * 4),
     "flw_quant_tensor_t_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "flw_quant_tensor_t_e4m3": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                         c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -119,9 +119,67 @@ class _QkvHeadsFn(torch.autograd.Function):
         lib = _lib.load()
         rc = lib.flw_qkv_heads_bwd(y.data_ptr(), B, T, H, D, y.stride(1), int(norm), float(eps), cos.data_ptr(),
                                    sin.data_ptr(), grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(),
-                                   dy.data_ptr(), C, _lib.stream_of(y))
+                                   dy.data_ptr(), C, None, None, 0, _lib.stream_of(y))
         _lib.check(rc, "qkv_heads backward")
         return dy, None, None, None, None, None
+
+
+class _Fp8QkvHeadsFn(torch.autograd.Function):
+    """The qkv projection as a tensorwise Fp8Linear followed by ``_QkvHeadsFn``'s pass, as one
+    autograd node, so that the backward's qkv_heads pass also reports |dqkv|'s maximum and the
+    projection's gradient cast takes it instead of an amax pass. Every code, scale and GEMM is the
+    one the Fp8Linear and _QkvHeadsFn compute on their own: the same results bit for bit."""
+
+    @staticmethod
+    def forward(ctx, x, weight, qkv_mod, num_heads, norm, eps, cos, sin):
+        from . import precision as P
+        lib = _lib.load()
+        B, T, d = x.shape
+        x2 = x.reshape(B * T, d)
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        M = B * T
+        ld = ((M + 127) // 128) * 128
+        x8, x8t, sx = P._quantize_tensorwise_t(x2, ld)
+        w8, sw, w8t = qkv_mod.tensorwise_codes()
+        y = P.scaled_mm_plain(x8, sx, w8, sw)
+        C = y.shape[1]
+        D = C // (3 * num_heads)
+        q, k, v = (torch.empty((B, num_heads, T, D), dtype=y.dtype, device=y.device) for _ in range(3))
+        _lib.check(lib.flw_qkv_heads_fwd(y.data_ptr(), B, T, num_heads, D, C, int(norm), float(eps), cos.data_ptr(),
+                                         sin.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                         _lib.stream_of(y)), "qkv_heads")
+        ctx.save_for_backward(y, cos, sin, x8t, sx, w8, sw, w8t)
+        ctx.meta = (qkv_mod, num_heads, norm, eps, D, B, T, ld, x.shape)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        from . import precision as P
+        y, cos, sin, x8t, sx, w8, sw, w8t = ctx.saved_tensors
+        qkv_mod, H, norm, eps, D, B, T, ld, x_shape = ctx.meta
+        M, C = y.shape
+        lib = _lib.load()
+        grads = [(g if g is not None else torch.zeros((B, H, T, D), dtype=y.dtype, device=y.device))
+                 .to(y.dtype).contiguous() for g in (dq, dk, dv)]
+        dy = torch.empty((M, C), dtype=y.dtype, device=y.device)
+        amax = torch.empty(1, dtype=torch.int32, device=y.device)
+        ws = _lib.workspace(lib.flw_qkv_heads_amax_workspace_bytes(B, T, H, D), y.device)
+        _lib.check(lib.flw_qkv_heads_bwd(y.data_ptr(), B, T, H, D, C, int(norm), float(eps), cos.data_ptr(),
+                                         sin.data_ptr(), grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(),
+                                         dy.data_ptr(), C, amax.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _lib.stream_of(y)), "qkv_heads backward")
+        g8, g8t, sg = P._quantize_tensorwise_t(dy, ld, amax)
+        gx = gw = None
+        if ctx.needs_input_grad[0]:
+            if getattr(qkv_mod, "_fp8_cached", None) is not None:     # the weight cache's dgrad codes
+                wc, swc = qkv_mod.weight_col_codes()
+            else:
+                wc, swc = (w8t if w8t is not None else P.transpose_codes(w8, C)), sw
+            gx = P.scaled_mm(g8, sg, wc, swc).view(x_shape)
+        if ctx.needs_input_grad[1]:
+            gw = P.scaled_mm(g8t, sg, x8t, sx).to(qkv_mod.weight.dtype)
+        return gx, gw, None, None, None, None, None, None
 
 
 class HeadRMSNorm(nn.Module):
@@ -209,7 +267,12 @@ class CausalSelfAttention(nn.Module):
     attn_precision "bf16": ``qkv_heads`` then the differentiable HIP bf16 sliding-window kernel
     (a full causal window when ``local_window`` is None). The reference's flex / SDPA choice and
     its RBF distance bias (local_attn_kernel_bias "rbf") are not offered: rbf raises ValueError.
+    ``fused_fp8_qkv`` (False): with a tensorwise Fp8Linear ``qkv`` in training, run the projection
+    and the heads pass as one node whose backward hands |dqkv|'s maximum to the gradient cast
+    (``_Fp8QkvHeadsFn``; the same results bit for bit).
     """
+
+    fused_fp8_qkv = False
 
     def __init__(self, config, local_window: int | None = None) -> None:
         super().__init__()
@@ -245,6 +308,14 @@ class CausalSelfAttention(nn.Module):
         """Project to per-head (q, k, v), apply QK-norm, then RoPE (base.py:618-639). bf16 on the
         GPU: the split, norm and RoPE run as one HIP pass each way (``_QkvHeadsFn``), q, k, v
         contiguous; otherwise the reference's torch expressions."""
+        if self._fp8_qkv_ok(x):
+            cos, sin = self.rope.tables(x.shape[1], x.dtype, x.device)
+            eps = self.qk_norm.eps if self.qk_norm is not None else 0.0
+            q, k, v = _Fp8QkvHeadsFn.apply(x, self.qkv.weight, self.qkv, self.num_heads, self.qk_norm is not None,
+                                           eps, cos, sin)
+            if self.fp8_attention_sim:
+                q, k, v = _fake_quant_e4m3(q), _fake_quant_e4m3(k), _fake_quant_e4m3(v)
+            return q, k, v
         y = self.qkv(x)
         if y.is_cuda and y.dtype == torch.bfloat16 and self.head_dim in (32, 64, 128):
             cos, sin = self.rope.tables(y.shape[1], y.dtype, y.device)
@@ -261,6 +332,21 @@ class CausalSelfAttention(nn.Module):
         if self.fp8_attention_sim:
             q, k, v = _fake_quant_e4m3(q), _fake_quant_e4m3(k), _fake_quant_e4m3(v)
         return q, k, v
+
+    def _fp8_qkv_ok(self, x: torch.Tensor) -> bool:
+        """``qkv`` a bias-free tensorwise Fp8Linear with the FP8 backward and 16-aligned widths, x a
+        non-empty (B, T, d) bf16 GPU tensor, autocast off, a gradient to take, and ``fused_fp8_qkv`` set:
+        _Fp8QkvHeadsFn's route. Off by default: on the 450M block the qkv_heads backward with the
+        |dqkv| maximum takes ~8 us longer a call than without it (92.8 against 84.8 us), which is
+        what the amax pass it spares the gradient cast costs, with a fold launch besides."""
+        from .precision import Fp8Linear
+        m = self.qkv
+        return (self.fused_fp8_qkv and type(m) is Fp8Linear and m.recipe == "tensorwise" and getattr(m, "backward_fp8", True)
+                and m.bias is None and m.in_features % 16 == 0 and m.out_features % 16 == 0
+                and x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 3 and x.numel() > 0
+                and not torch.is_autocast_enabled() and self.head_dim in (32, 64, 128)
+                and m.out_features == 3 * self.num_heads * self.head_dim
+                and torch.is_grad_enabled() and (x.requires_grad or m.weight.requires_grad))
 
     def _needs_grad(self, x: torch.Tensor) -> bool:
         return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))

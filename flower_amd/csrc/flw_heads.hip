@@ -32,6 +32,7 @@ struct HeadsParams {
   const uint16_t* grad[3];      // backward: dq', dk', dv as contiguous (B, H, T, D)
   uint16_t* dqkv;               // backward: [M, ds]
   int64_t ds;
+  uint32_t* part;               // backward with AMAX: per-workgroup |dqkv| maxima
   int64_t M;
   int T, H, norm;
   float eps;
@@ -84,55 +85,93 @@ __global__ __launch_bounds__(256) void qkv_heads_fwd_kernel(HeadsParams p) {
                  bf16x2_rne_raw(f[6], f[7]));
 }
 
-template <int D>
+template <int D, bool AMAX>
 __global__ __launch_bounds__(256) void qkv_heads_bwd_kernel(HeadsParams p) {
+  __shared__ uint32_t red[4];
   HeadsChunk<D> ch;
-  if (!ch.init(p)) return;
-  const int64_t dst = ch.m * p.ds + ((int64_t)ch.part * p.H + ch.h) * D + 8 * ch.l;
-  const uint4 graw = *reinterpret_cast<const uint4*>(p.grad[ch.part] + ch.bhtd);
-  if (ch.part == 2) {
-    *reinterpret_cast<uint4*>(p.dqkv + dst) = graw;
-    return;
-  }
-  float g[8], x[8], c[8], sn[8], dn[8];
-  Vec16<uint16_t>::unpack(graw, g);
-  Vec16<uint16_t>::load(p.qkv + ch.m * p.qs + ((int64_t)ch.part * p.H + ch.h) * D + 8 * ch.l, x);
-  Vec16<uint16_t>::load(p.cos + (int64_t)ch.t * D + 8 * ch.l, c);
-  Vec16<uint16_t>::load(p.sin + (int64_t)ch.t * D + 8 * ch.l, sn);
-  {
+  const bool valid = ch.init(p);
+  flw_u16x2 mx = {0, 0};
+  if (valid) {
+    const int64_t dst = ch.m * p.ds + ((int64_t)ch.part * p.H + ch.h) * D + 8 * ch.l;
+    const uint4 graw = *reinterpret_cast<const uint4*>(p.grad[ch.part] + ch.bhtd);
+    uint4 w = graw;
+    if (ch.part != 2) {
+      float g[8], x[8], c[8], sn[8], dn[8];
+      Vec16<uint16_t>::unpack(graw, g);
+      Vec16<uint16_t>::load(p.qkv + ch.m * p.qs + ((int64_t)ch.part * p.H + ch.h) * D + 8 * ch.l, x);
+      Vec16<uint16_t>::load(p.cos + (int64_t)ch.t * D + 8 * ch.l, c);
+      Vec16<uint16_t>::load(p.sin + (int64_t)ch.t * D + 8 * ch.l, sn);
+      {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      const float a0 = round_bf16(g[i] * c[i]), a1 = round_bf16(g[i + 1] * c[i + 1]);
-      const float b0 = round_bf16(g[i] * sn[i]), b1 = round_bf16(g[i + 1] * sn[i + 1]);
-      dn[i] = round_bf16(a0 + b1);
-      dn[i + 1] = round_bf16(a1 - b0);
-    }
-  }
-  float o[8];
-  if (p.norm) {
-    float ss = 0.0f, sd = 0.0f;
+        for (int i = 0; i < 8; i += 2) {
+          const float a0 = round_bf16(g[i] * c[i]), a1 = round_bf16(g[i + 1] * c[i + 1]);
+          const float b0 = round_bf16(g[i] * sn[i]), b1 = round_bf16(g[i + 1] * sn[i + 1]);
+          dn[i] = round_bf16(a0 + b1);
+          dn[i + 1] = round_bf16(a1 - b0);
+        }
+      }
+      float o[8];
+      if (p.norm) {                                 // uniform over a head row's lanes
+        float ss = 0.0f, sd = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ss = fmaf(x[i], x[i], ss);
-      sd = fmaf(dn[i], x[i], sd);
-    }
-    ss = group_sum(ss, D / 8);
-    sd = group_sum(sd, D / 8);
-    const float r = __builtin_amdgcn_rsqf(__builtin_ldexpf(ss, -__builtin_ctz((unsigned)D)) + p.eps);
-    const float k = __builtin_ldexpf(sd * (r * r * r), -__builtin_ctz((unsigned)D));
+        for (int i = 0; i < 8; ++i) {
+          ss = fmaf(x[i], x[i], ss);
+          sd = fmaf(dn[i], x[i], sd);
+        }
+        ss = group_sum(ss, D / 8);
+        sd = group_sum(sd, D / 8);
+        const float r = __builtin_amdgcn_rsqf(__builtin_ldexpf(ss, -__builtin_ctz((unsigned)D)) + p.eps);
+        const float k = __builtin_ldexpf(sd * (r * r * r), -__builtin_ctz((unsigned)D));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 8; ++i) {
 #pragma clang fp contract(off)
-      o[i] = round_bf16(dn[i] * r) - round_bf16(x[i] * k);
-    }
-  } else {
+          o[i] = round_bf16(dn[i] * r) - round_bf16(x[i] * k);
+        }
+      } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = dn[i];
+        for (int i = 0; i < 8; ++i) o[i] = dn[i];
+      }
+      w = make_uint4(bf16x2_canon_nan(bf16x2_rne_raw(o[0], o[1])), bf16x2_canon_nan(bf16x2_rne_raw(o[2], o[3])),
+                     bf16x2_canon_nan(bf16x2_rne_raw(o[4], o[5])), bf16x2_canon_nan(bf16x2_rne_raw(o[6], o[7])));
+    }
+    *reinterpret_cast<uint4*>(p.dqkv + dst) = w;
+    if (AMAX) {
+      mx = abs_max_bf16x2(mx, w.x);
+      mx = abs_max_bf16x2(mx, w.y);
+      mx = abs_max_bf16x2(mx, w.z);
+      mx = abs_max_bf16x2(mx, w.w);
+    }
   }
-  *reinterpret_cast<uint4*>(p.dqkv + dst) =
-      make_uint4(bf16x2_canon_nan(bf16x2_rne_raw(o[0], o[1])), bf16x2_canon_nan(bf16x2_rne_raw(o[2], o[3])),
-                 bf16x2_canon_nan(bf16x2_rne_raw(o[4], o[5])), bf16x2_canon_nan(bf16x2_rne_raw(o[6], o[7])));
+  if (AMAX) {                                       // this workgroup's |dqkv| maximum (fp32 bits)
+    uint32_t m = (uint32_t)(mx[0] > mx[1] ? mx[0] : mx[1]) << 16;
+    m = wave_max_u32(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t r = red[0];
+#pragma unroll
+      for (int i = 1; i < 4; ++i) r = r > red[i] ? r : red[i];
+      p.part[blockIdx.x] = r;
+    }
+  }
+}
+
+// One workgroup of 1024 folds the n per-workgroup maxima into out[0].
+__global__ __launch_bounds__(1024) void heads_fold_kernel(const uint32_t* __restrict__ part, int n,
+                                                          uint32_t* __restrict__ out) {
+  __shared__ uint32_t red[16];
+  uint32_t m = 0;
+  for (int i = threadIdx.x; i < n; i += 1024) m = m > part[i] ? m : part[i];
+  m = wave_max_u32(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = red[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) r = r > red[i] ? r : red[i];
+    out[0] = r;
+  }
 }
 
 static int heads_check(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t D, int64_t qs,
@@ -179,9 +218,15 @@ extern "C" int flw_qkv_heads_fwd(const void* qkv, int64_t B, int64_t T, int64_t 
   return check_launch("flw_qkv_heads_fwd");
 }
 
+extern "C" size_t flw_qkv_heads_amax_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D) {
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0) return 0;
+  return (size_t)((B * T * 3 * H * (D / 8) + 255) / 256) * 4;
+}
+
 extern "C" int flw_qkv_heads_bwd(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t D, int64_t qkv_row_stride,
                                  int qk_norm, float eps, const void* rope_cos, const void* rope_sin, const void* dq,
-                                 const void* dk, const void* dv, void* dqkv, int64_t dqkv_row_stride, void* stream) {
+                                 const void* dk, const void* dv, void* dqkv, int64_t dqkv_row_stride,
+                                 uint32_t* dqkv_amax, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = heads_check(qkv, B, T, H, D, qkv_row_stride, rope_cos, rope_sin, eps, qk_norm);
   if (rc) return rc;
   FLW_REQUIRE(dq && dk && dv && dqkv && ((uintptr_t)dq & 15) == 0 && ((uintptr_t)dk & 15) == 0 &&
@@ -196,8 +241,25 @@ extern "C" int flw_qkv_heads_bwd(const void* qkv, int64_t B, int64_t T, int64_t 
   p.grad[2] = static_cast<const uint16_t*>(dv);
   p.dqkv = static_cast<uint16_t*>(dqkv); p.ds = dqkv_row_stride;
   p.M = B * T; p.T = (int)T; p.H = (int)H; p.norm = qk_norm; p.eps = eps;
-  heads_launch(reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<32>),
-               reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<64>),
-               reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<128>), D, p, static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dqkv_amax == nullptr) {
+    heads_launch(reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<32, false>),
+                 reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<64, false>),
+                 reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<128, false>), D, p, s);
+    return check_launch("flw_qkv_heads_bwd");
+  }
+  const size_t need = flw_qkv_heads_amax_workspace_bytes(B, T, H, D);
+  FLW_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0 && workspace_bytes >= need, FLW_E_WORKSPACE,
+              "workspace needs %zu bytes (16-byte aligned)", need);
+  p.part = static_cast<uint32_t*>(workspace);
+  const int64_t chunks = p.M * 3 * p.H * (D / 8);
+  const int nblk = (int)((chunks + 255) / 256);
+  const void* k = D == 32 ? reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<32, true>)
+                : D == 64 ? reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<64, true>)
+                          : reinterpret_cast<const void*>(&qkv_heads_bwd_kernel<128, true>);
+  const Timer tm = take_timer();
+  (void)launch_ext(k, dim3((unsigned)nblk), dim3(256), 0, s, p, tm.start, nullptr);
+  (void)launch_args(reinterpret_cast<const void*>(&heads_fold_kernel), dim3(1u), dim3(1024), 0, s, nullptr, tm.stop,
+                    static_cast<const uint32_t*>(p.part), nblk, dqkv_amax);
   return check_launch("flw_qkv_heads_bwd");
 }

@@ -167,7 +167,12 @@ int flw_qkv_heads_fwd(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t 
  * autograd sums them); dv copied into the v columns. */
 int flw_qkv_heads_bwd(const void* qkv, int64_t B, int64_t T, int64_t H, int64_t D, int64_t qkv_row_stride,
                       int qk_norm, float eps, const void* rope_cos, const void* rope_sin, const void* dq,
-                      const void* dk, const void* dv, void* dqkv, int64_t dqkv_row_stride, void* stream);
+                      const void* dk, const void* dv, void* dqkv, int64_t dqkv_row_stride, uint32_t* dqkv_amax,
+                      void* workspace, size_t workspace_bytes, void* stream);
+/* dqkv_amax (may be NULL; then workspace may be NULL too): also |dqkv|'s maximum as an fp32 bit
+ * pattern (NaN above inf), the amax half of the qkv projection's tensorwise gradient cast, from
+ * per-workgroup maxima in a workspace of flw_qkv_heads_amax_workspace_bytes and a folding launch. */
+size_t flw_qkv_heads_amax_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D);
 
 /* RMSNorm forward for training, replacing RMSNorm.forward (flower/models/base.py:336-338) on bf16
  * rows: x [rows, cols] (row stride x_row_stride), bf16 weight [cols] -> h [rows, cols]

@@ -285,8 +285,12 @@ def test_training_row_kernel_refusals_on_the_host():
     assert rc == 2 and b"head_dim" in lib.flw_last_error()
     rc = lib.flw_qkv_heads_fwd(P, 1, 16, 2, 64, 320, 1, 1e-6, P, P, P, P, P, None)
     assert rc == 1 and b"3 H D" in lib.flw_last_error()
-    rc = lib.flw_qkv_heads_bwd(P, 1, 16, 2, 64, 384, 1, 1e-6, P, P, P, P, P, P + 8, 384, None)
+    rc = lib.flw_qkv_heads_bwd(P, 1, 16, 2, 64, 384, 1, 1e-6, P, P, P, P, P, P + 8, 384, None, None, 0, None)
     assert rc == 1 and b"aligned" in lib.flw_last_error()
+    need = lib.flw_qkv_heads_amax_workspace_bytes(1, 16, 2, 64)           # one u32 per workgroup
+    assert need == 4 * ((16 * 3 * 2 * 8 + 255) // 256)
+    rc = lib.flw_qkv_heads_bwd(P, 1, 16, 2, 64, 384, 1, 1e-6, P, P, P, P, P, P, 384, P, P, need - 4, None)
+    assert rc == 3 and b"workspace" in lib.flw_last_error()
     rc = lib.flw_rmsnorm_fwd(P, 4, 12, 16, P, 1e-6, P, 16, None)
     assert rc == 1 and b"multiple of 8" in lib.flw_last_error()
     rc = lib.flw_rmsnorm_fwd(P, 4, 8200, 8200, P, 1e-6, P, 8200, None)

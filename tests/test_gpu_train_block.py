@@ -199,3 +199,39 @@ def test_fused_fp8_block_ragged_tokens_bit_identical():
     assert torch.equal(y, y2.detach().float()) and torch.equal(gx, xx.grad.float())
     for n, p in blk.named_parameters():
         assert torch.equal(gp[n], p.grad.float()), n
+
+
+@pytest.mark.parametrize("T,cached", [(320, False), (77, False), (320, True)])
+def test_fused_fp8_qkv_heads_node_bit_identical(T, cached, monkeypatch):
+    """The qkv projection and the heads pass as one node (_Fp8QkvHeadsFn: the qkv_heads backward
+    reports |dqkv|'s maximum, the gradient cast takes it in place of its amax pass) against the
+    tensorwise Fp8Linear followed by _QkvHeadsFn (the default route; the node is opt-in through
+    fused_fp8_qkv): q, k, v, x's gradient and the weight's equal bit for bit -- ragged tokens
+    (B1 x T77) and inside fp8_weight_cache too."""
+    from flower_amd.precision import convert_model_to_fp8, fp8_weight_cache
+    blk, conf = _block()
+    stack = nn.Module()
+    stack.blocks = nn.ModuleList([blk])
+    convert_model_to_fp8(stack, recipe="tensorwise", keep_bf16_blocks=0, verbose=False)
+    attn = stack.blocks[0].attn
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(2 if T == 320 else 1, T, conf.d_model, generator=g).to("cuda", torch.bfloat16)
+    dq, dk, dv = (torch.randn(x.shape[0], conf.num_heads, T, conf.d_model // conf.num_heads,
+                              generator=g).to("cuda", torch.bfloat16) for _ in range(3))
+
+    def run():
+        xx = x.clone().requires_grad_(True)
+        attn.qkv.weight.grad = None
+        ctx = fp8_weight_cache(stack) if cached else torch.enable_grad()
+        with ctx:
+            q, k, v = attn.qkv_heads(xx)
+            torch.autograd.backward((q, k, v), (dq, dk, dv))
+        return q.detach(), k.detach(), v.detach(), xx.grad, attn.qkv.weight.grad.clone()
+
+    assert not attn._fp8_qkv_ok(x.clone().requires_grad_(True))       # opt-in
+    plain = run()
+    monkeypatch.setattr(attn, "fused_fp8_qkv", True)
+    assert attn._fp8_qkv_ok(x.clone().requires_grad_(True))
+    fused = run()
+    for a, b in zip(fused, plain):
+        assert torch.equal(a, b)
